@@ -1,0 +1,661 @@
+// layer.hip -- host side of the C ABI (include/burnext_moe.h): layer upload and repack,
+// workspace layout, and the launch sequence of one MoE forward on a HIP stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/burnext_moe.h"
+#include "kernels.hpp"
+
+using namespace burnext;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+burnext_status fail(burnext_status st, const std::string &msg) {
+  g_last_error = msg;
+  return st;
+}
+
+burnext_status ok() {
+  g_last_error.clear();
+  return BURNEXT_OK;
+}
+
+inline uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+inline uint64_t align_up(uint64_t a, uint64_t b) { return cdiv(a, b) * b; }
+
+float bf16_to_f32_host(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float read_scalar(const void *p, burnext_dtype dt, size_t i) {
+  return dt == BURNEXT_BF16 ? bf16_to_f32_host(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+struct ProfPair {
+  hipEvent_t a, b;
+  int kernel;
+};
+
+}  // namespace
+
+// Tiled MXFP4 layout of one projection (see the expert_gemv comment in kernels.hip).
+struct TiledMx {
+  uint32_t rows = 0, rows_p = 0, cols = 0, nb = 0, nrt = 0;
+  uint64_t blocks_per_expert = 0, scales_per_expert = 0;
+  uint8_t *blocks = nullptr, *scales = nullptr;
+};
+
+struct burnext_moe_layer {
+  int device = 0;
+  uint32_t D = 0, F = 0, E = 0, K = 0;
+  float alpha = 1.702f, limit = 7.0f, eps = 1e-5f;
+  bool disabled = false;
+  uint32_t Dp = 0, Fp = 0;
+  TiledMx w1, w2;
+  float *b1 = nullptr;  // [E, w1.rows_p], interleaved (gate, linear) order
+  float *b2 = nullptr;  // [E, D]
+  void *router_w = nullptr;
+  bool router_bf16 = false;
+  float *router_b = nullptr;  // [E]
+  float *gamma = nullptr;     // [D]
+  std::mutex prof_mu;
+  bool profiling = false;
+  std::vector<ProfPair> prof;
+};
+
+namespace {
+
+// W1 internal row r (interleaved: even = gate, odd = linear) -> source row for `layout`.
+inline uint32_t w1_src_row(uint32_t r, uint32_t F, burnext_gate_up_layout layout) {
+  return layout == BURNEXT_GATE_UP_INTERLEAVED ? r : ((r & 1u) ? F + (r >> 1) : (r >> 1));
+}
+
+// Repacks one expert of a [rows, cols] MXFP4 matrix into the tiled layout.  Scale bytes are
+// normalised to true e8m0 exponents ((stored - ue8_offset) mod 256, the inverse of the model.bin
+// writer's wrapping add, reference src/bin/gptoss_export.rs:562).  Padding rows, columns and
+// blocks are zero codes with scale byte 0.
+void repack_expert(const uint8_t *src_b, const uint8_t *src_s, uint64_t bpr, uint64_t gpr, int ue8,
+                   const TiledMx &t, bool is_w1, uint32_t F, burnext_gate_up_layout layout, uint8_t *dst_b,
+                   uint8_t *dst_s) {
+  const uint32_t nb = t.nb, nkg = (nb + 3) / 4;
+  for (uint32_t rt = 0; rt < t.nrt; ++rt) {
+    for (uint32_t kg = 0; kg < nkg; ++kg) {
+      const uint32_t nbk = std::min(4u, nb - 4 * kg);
+      for (uint32_t q = 0; q < nbk; ++q) {
+        for (uint32_t i = 0; i < 16; ++i) {
+          const uint32_t row = rt * 16 + i, blk = 4 * kg + q, lane = q * 16 + i;
+          uint8_t *db = dst_b + (uint64_t)rt * nb * 256 + (uint64_t)kg * 1024 + (uint64_t)lane * 16;
+          uint8_t *ds = dst_s + (uint64_t)rt * nb * 16 + (uint64_t)kg * 64 + lane;
+          memset(db, 0, 16);
+          *ds = 0;
+          if (row >= t.rows) continue;
+          const uint32_t sr = is_w1 ? w1_src_row(row, F, layout) : row;
+          const uint8_t *rb = src_b + (uint64_t)sr * bpr;
+          const uint64_t b0 = (uint64_t)blk * 16;
+          for (uint64_t u = 0; u < 16 && b0 + u < bpr; ++u) {
+            uint8_t byte = rb[b0 + u];
+            const uint64_t c = 2 * (b0 + u);  // column of the low nibble
+            if (c + 1 >= t.cols) byte &= 0x0F;
+            if (c >= t.cols) byte = 0;
+            db[u] = byte;
+          }
+          *ds = (uint8_t)(((int)src_s[(uint64_t)sr * gpr + blk] - ue8) & 255);
+        }
+      }
+    }
+  }
+}
+
+burnext_status upload_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols, const uint8_t *blocks,
+                            const uint8_t *scales, const burnext_mxfp4_desc &d, bool is_w1, uint32_t F,
+                            burnext_gate_up_layout layout) {
+  t.rows = rows;
+  t.rows_p = (uint32_t)align_up(rows, 16);
+  t.cols = cols;
+  t.nb = (uint32_t)cdiv(cols, 32);
+  t.nrt = t.rows_p / 16;
+  t.blocks_per_expert = (uint64_t)t.rows_p * t.nb * 16;
+  t.scales_per_expert = (uint64_t)t.rows_p * t.nb;
+  std::vector<uint8_t> hb, hs;
+  try {
+    hb.resize(t.blocks_per_expert * E);
+    hs.resize(t.scales_per_expert * E);
+  } catch (const std::bad_alloc &) {
+    return fail(BURNEXT_OUT_OF_MEMORY, "host allocation failed while repacking MXFP4 weights");
+  }
+  const uint64_t src_bpe = (uint64_t)rows * d.bpr, src_spe = (uint64_t)rows * d.gpr;
+  const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const unsigned nthr = std::min<unsigned>(hw, E);
+  std::vector<std::thread> pool;
+  for (unsigned w = 0; w < nthr; ++w) {
+    pool.emplace_back([&, w]() {
+      for (uint32_t e = w; e < E; e += nthr)
+        repack_expert(blocks + e * src_bpe, scales + e * src_spe, d.bpr, d.gpr, d.ue8_offset, t, is_w1, F, layout,
+                      hb.data() + e * t.blocks_per_expert, hs.data() + e * t.scales_per_expert);
+    });
+  }
+  for (auto &th : pool) th.join();
+  if (hipMalloc(&t.blocks, hb.size()) != hipSuccess || hipMalloc(&t.scales, hs.size()) != hipSuccess)
+    return fail(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed for MXFP4 weights");
+  if (hipMemcpy(t.blocks, hb.data(), hb.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(t.scales, hs.data(), hs.size(), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(BURNEXT_DEVICE_ERROR, "hipMemcpy of MXFP4 weights failed");
+  return BURNEXT_OK;
+}
+
+template <typename T>
+burnext_status upload_vec(T **dst, const std::vector<T> &v) {
+  if (hipMalloc((void **)dst, std::max<size_t>(v.size(), 1) * sizeof(T)) != hipSuccess)
+    return fail(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed");
+  if (!v.empty() && hipMemcpy(*dst, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(BURNEXT_DEVICE_ERROR, "hipMemcpy failed");
+  return BURNEXT_OK;
+}
+
+void free_layer(burnext_moe_layer *L) {
+  if (!L) return;
+  DeviceGuard g(L->device);
+  for (void *p : {(void *)L->w1.blocks, (void *)L->w1.scales, (void *)L->w2.blocks, (void *)L->w2.scales,
+                  (void *)L->b1, (void *)L->b2, L->router_w, (void *)L->router_b, (void *)L->gamma})
+    if (p) (void)hipFree(p);
+  for (auto &pp : L->prof) {
+    (void)hipEventDestroy(pp.a);
+    (void)hipEventDestroy(pp.b);
+  }
+  delete L;
+}
+
+bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t cols, const char *name,
+                std::string &msg) {
+  char buf[256];
+  if (d->experts != E || d->rows != rows || d->cols != cols || d->bpr != cdiv(cols, 2) || d->gpr != cdiv(cols, 32) ||
+      d->ue8_offset < 0 || d->ue8_offset > 255) {
+    snprintf(buf, sizeof(buf),
+             "%s descriptor {experts=%llu rows=%llu cols=%llu bpr=%llu gpr=%llu ue8_offset=%d} does not match "
+             "expected {experts=%llu rows=%llu cols=%llu bpr=%llu gpr=%llu ue8_offset in [0,255]}",
+             name, (unsigned long long)d->experts, (unsigned long long)d->rows, (unsigned long long)d->cols,
+             (unsigned long long)d->bpr, (unsigned long long)d->gpr, d->ue8_offset, (unsigned long long)E,
+             (unsigned long long)rows, (unsigned long long)cols, (unsigned long long)cdiv(cols, 2),
+             (unsigned long long)cdiv(cols, 32));
+    msg = buf;
+    return false;
+  }
+  return true;
+}
+
+// Workspace carve-up for n tokens (every region 256-byte aligned).
+struct WsLayout {
+  uint64_t xn, logits, topk_idx, topk_w, meta, perm, pos_of, act, ypart, total;
+};
+
+constexpr uint32_t kMaxTerms = 3;
+
+WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
+  WsLayout w{};
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) {
+    const uint64_t o = off;
+    off = align_up(off + std::max<uint64_t>(bytes, 1), 256);
+    return o;
+  };
+  const uint64_t nk = n * L.K;
+  w.xn = take(n * kMaxTerms * L.Dp * 2);
+  w.logits = take(n * L.E * 4);
+  w.topk_idx = take(nk * 4);
+  w.topk_w = take(nk * 4);
+  w.meta = take((2ull * L.E + 2) * 4);
+  w.perm = take(nk * 4);
+  w.pos_of = take(nk * 4);
+  w.act = take(nk * L.Fp * 4);
+  w.ypart = take(nk * L.Dp * 4);
+  w.total = off;
+  return w;
+}
+
+struct WsPtrs {
+  uint16_t *xn;
+  float *logits;
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *active, *num_active, *perm, *pos_of;
+  float *act, *ypart;
+};
+
+WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
+  uint8_t *b = (uint8_t *)base;
+  WsPtrs p{};
+  p.xn = (uint16_t *)(b + w.xn);
+  p.logits = (float *)(b + w.logits);
+  p.topk_idx = (int32_t *)(b + w.topk_idx);
+  p.topk_w = (float *)(b + w.topk_w);
+  p.seg_off = (int32_t *)(b + w.meta);
+  p.active = p.seg_off + L.E + 1;
+  p.num_active = p.active + L.E;
+  p.perm = (int32_t *)(b + w.perm);
+  p.pos_of = (int32_t *)(b + w.pos_of);
+  p.act = (float *)(b + w.act);
+  p.ypart = (float *)(b + w.ypart);
+  return p;
+}
+
+constexpr size_t kLdsBudget = 160 * 1024;
+
+uint32_t route_tpb(const burnext_moe_layer &L) {
+  uint32_t tpb = 8;
+  while (tpb > 1 && route_lds_bytes(tpb, L.D, L.E, L.K, kRouteThreads) > kLdsBudget) tpb >>= 1;
+  return tpb;
+}
+
+// Records a HIP event pair around a launch when profiling is on.
+struct ProfScope {
+  burnext_moe_layer *L;
+  hipStream_t s;
+  int k;
+  hipEvent_t a = nullptr, b = nullptr;
+  ProfScope(burnext_moe_layer *L_, hipStream_t s_, int k_) : L(L_), s(s_), k(k_) {
+    if (!L->profiling) return;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+      a = b = nullptr;
+      return;
+    }
+    (void)hipEventRecord(a, s);
+  }
+  ~ProfScope() {
+    if (!a) return;
+    (void)hipEventRecord(b, s);
+    std::lock_guard<std::mutex> lk(L->prof_mu);
+    L->prof.push_back({a, b, k});
+  }
+};
+
+burnext_status check_launch(hipError_t e, const char *what) {
+  if (e != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+  return BURNEXT_OK;
+}
+
+// Routing (+ dispatch) into the workspace; shared by forward, route and dispatch entry points.
+burnext_status run_route(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, const WsPtrs &p,
+                         bool want_terms, bool want_dispatch, hipStream_t s) {
+  RouteArgs ra{};
+  ra.x = x;
+  ra.rw = L->router_w;
+  ra.rb = L->router_b;
+  ra.gamma = L->gamma;
+  ra.xn_terms = want_terms ? p.xn : nullptr;
+  ra.logits = p.logits;
+  ra.topk_idx = p.topk_idx;
+  ra.topk_w = p.topk_w;
+  ra.seg_off = p.seg_off;
+  ra.perm = p.perm;
+  ra.pos_of = p.pos_of;
+  ra.active = p.active;
+  ra.num_active = p.num_active;
+  ra.n = (uint32_t)n;
+  ra.D = L->D;
+  ra.Dp = L->Dp;
+  ra.E = L->E;
+  ra.K = L->K;
+  ra.tpb = route_tpb(*L);
+  ra.nt = x_bf16 ? 1 : 3;
+  ra.eps = L->eps;
+  ra.apply_norm = norm ? 1 : 0;
+  ra.fuse_dispatch = (want_dispatch && n <= ra.tpb) ? 1 : 0;
+  {
+    ProfScope ps(L, s, 0);
+    burnext_status st = check_launch(launch_route(ra, x_bf16, L->router_bf16, s), "route kernel launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  if (want_dispatch && !ra.fuse_dispatch) {
+    DispatchArgs da{};
+    da.topk_idx = p.topk_idx;
+    da.seg_off = p.seg_off;
+    da.perm = p.perm;
+    da.pos_of = p.pos_of;
+    da.active = p.active;
+    da.num_active = p.num_active;
+    da.n = (uint32_t)n;
+    da.K = L->K;
+    da.E = L->E;
+    ProfScope ps(L, s, 1);
+    burnext_status st = check_launch(launch_dispatch(da, s), "dispatch kernel launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  return BURNEXT_OK;
+}
+
+burnext_status check_ws(burnext_moe_layer *L, uint64_t n, void *ws, uint64_t ws_bytes, WsLayout &w) {
+  w = ws_layout(*L, n);
+  if (!ws) return fail(BURNEXT_INVALID_ARG, "workspace is null");
+  if (((uintptr_t)ws & 255u) != 0) return fail(BURNEXT_INVALID_ARG, "workspace must be 256-byte aligned");
+  if (ws_bytes < w.total) {
+    char buf[160];
+    snprintf(buf, sizeof(buf), "workspace of %llu bytes is smaller than the %llu bytes needed for %llu tokens",
+             (unsigned long long)ws_bytes, (unsigned long long)w.total, (unsigned long long)n);
+    return fail(BURNEXT_WORKSPACE_TOO_SMALL, buf);
+  }
+  return BURNEXT_OK;
+}
+
+constexpr uint64_t kMaxTokens = 1ull << 22;
+
+}  // namespace
+
+extern "C" {
+
+const char *burnext_last_error(void) { return g_last_error.c_str(); }
+
+burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const burnext_mxfp4_desc *w1_desc,
+                                        const uint8_t *w1_blocks, const uint8_t *w1_scales,
+                                        const burnext_mxfp4_desc *w2_desc, const uint8_t *w2_blocks,
+                                        const uint8_t *w2_scales, const void *b1, const void *b2,
+                                        burnext_dtype bias_dtype, const void *router_w, const void *router_b,
+                                        burnext_dtype router_dtype, const void *norm_gamma, burnext_dtype norm_dtype,
+                                        burnext_gate_up_layout gate_up_layout, int device,
+                                        burnext_moe_layer_t *out_layer) {
+  if (!out_layer) return fail(BURNEXT_INVALID_ARG, "out_layer is null");
+  *out_layer = nullptr;
+  if (!cfg || !w1_desc || !w2_desc || !w1_blocks || !w1_scales || !w2_blocks || !w2_scales || !b1 || !b2 || !router_w)
+    return fail(BURNEXT_INVALID_ARG, "null config, descriptor, weight or bias pointer");
+  const uint32_t D = cfg->d_model, F = cfg->ffn_hidden, E = cfg->num_experts;
+  if (D == 0 || F == 0 || E == 0) return fail(BURNEXT_INVALID_ARG, "d_model, ffn_hidden and num_experts must be > 0");
+  if (E > kMaxExperts) return fail(BURNEXT_UNSUPPORTED, "num_experts above 256 is not supported");
+  const uint32_t K = std::min(std::max(cfg->experts_per_token, 1u), E);
+  if (K > kMaxTopK) return fail(BURNEXT_UNSUPPORTED, "experts_per_token above 32 is not supported");
+  if ((bias_dtype != BURNEXT_F32 && bias_dtype != BURNEXT_BF16) ||
+      (router_dtype != BURNEXT_F32 && router_dtype != BURNEXT_BF16) ||
+      (norm_dtype != BURNEXT_F32 && norm_dtype != BURNEXT_BF16))
+    return fail(BURNEXT_INVALID_ARG, "dtype must be BURNEXT_F32 or BURNEXT_BF16");
+  if (gate_up_layout != BURNEXT_GATE_UP_HALVES && gate_up_layout != BURNEXT_GATE_UP_INTERLEAVED)
+    return fail(BURNEXT_INVALID_ARG, "gate_up_layout must be HALVES or INTERLEAVED");
+  std::string msg;
+  if (!check_desc(w1_desc, E, 2ull * F, D, "w1", msg) || !check_desc(w2_desc, E, D, F, "w2", msg))
+    return fail(BURNEXT_INVALID_ARG, msg);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(BURNEXT_INVALID_ARG, "device index out of range (or no HIP device)");
+
+  DeviceGuard guard(device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  {
+    static std::once_flag once;
+    static hipError_t cfg_err = hipSuccess;
+    std::call_once(once, [] { cfg_err = configure_kernels(); });
+    if (cfg_err != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string("kernel configuration failed: ") + hipGetErrorString(cfg_err));
+  }
+
+  burnext_moe_layer *L = new (std::nothrow) burnext_moe_layer();
+  if (!L) return fail(BURNEXT_OUT_OF_MEMORY, "host allocation failed");
+  L->device = device;
+  L->D = D;
+  L->F = F;
+  L->E = E;
+  L->K = K;
+  L->alpha = cfg->swiglu_alpha;
+  L->limit = cfg->swiglu_limit;
+  L->eps = cfg->rms_eps;
+  L->disabled = cfg->disabled != 0;
+  L->Dp = (uint32_t)align_up(D, 32);
+  L->Fp = (uint32_t)align_up(F, 32);
+
+  burnext_status st = upload_tiled(L->w1, E, 2 * F, D, w1_blocks, w1_scales, *w1_desc, true, F, gate_up_layout);
+  if (st == BURNEXT_OK) st = upload_tiled(L->w2, E, D, F, w2_blocks, w2_scales, *w2_desc, false, F, gate_up_layout);
+  if (st != BURNEXT_OK) {
+    free_layer(L);
+    return st;
+  }
+  // biases (f32 on device), b1 permuted to the interleaved internal row order
+  std::vector<float> hb1((size_t)E * L->w1.rows_p, 0.0f), hb2((size_t)E * D), hrb(E, 0.0f), hg(D, 1.0f);
+  for (uint32_t e = 0; e < E; ++e) {
+    for (uint32_t r = 0; r < 2 * F; ++r)
+      hb1[(size_t)e * L->w1.rows_p + r] = read_scalar(b1, bias_dtype, (size_t)e * 2 * F + w1_src_row(r, F, gate_up_layout));
+    for (uint32_t d = 0; d < D; ++d) hb2[(size_t)e * D + d] = read_scalar(b2, bias_dtype, (size_t)e * D + d);
+    if (router_b) hrb[e] = read_scalar(router_b, router_dtype, e);
+  }
+  if (norm_gamma)
+    for (uint32_t d = 0; d < D; ++d) hg[d] = read_scalar(norm_gamma, norm_dtype, d);
+  st = upload_vec(&L->b1, hb1);
+  if (st == BURNEXT_OK) st = upload_vec(&L->b2, hb2);
+  if (st == BURNEXT_OK) st = upload_vec(&L->router_b, hrb);
+  if (st == BURNEXT_OK) st = upload_vec(&L->gamma, hg);
+  if (st == BURNEXT_OK) {
+    L->router_bf16 = router_dtype == BURNEXT_BF16;
+    const size_t rbytes = (size_t)E * D * (L->router_bf16 ? 2 : 4);
+    if (hipMalloc(&L->router_w, rbytes) != hipSuccess)
+      st = fail(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed for router weight");
+    else if (hipMemcpy(L->router_w, router_w, rbytes, hipMemcpyHostToDevice) != hipSuccess)
+      st = fail(BURNEXT_DEVICE_ERROR, "hipMemcpy failed for router weight");
+  }
+  if (st != BURNEXT_OK) {
+    free_layer(L);
+    return st;
+  }
+  *out_layer = L;
+  return ok();
+}
+
+void burnext_moe_layer_destroy(burnext_moe_layer_t layer) { free_layer(layer); }
+
+burnext_status burnext_moe_workspace_size(burnext_moe_layer_t L, uint64_t n_tokens, uint64_t *bytes) {
+  if (!L || !bytes) return fail(BURNEXT_INVALID_ARG, "null layer or output pointer");
+  if (n_tokens > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  *bytes = ws_layout(*L, n_tokens).total;
+  return ok();
+}
+
+burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, void *y,
+                                   uint64_t n, uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
+  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  if (n == 0) return ok();
+  if (!x || !y) return fail(BURNEXT_INVALID_ARG, "x or y is null");
+  if (x == y) return fail(BURNEXT_INVALID_ARG, "x and y must not alias");
+  const bool xb = x_dtype == BURNEXT_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  DeviceGuard guard(L->device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  if (L->disabled) {  // identity, src/moe/mod.rs:106-108
+    const burnext_status cs =
+        check_launch(hipMemcpyAsync(y, x, n * L->D * (xb ? 2 : 4), hipMemcpyDeviceToDevice, s), "identity copy");
+    return cs == BURNEXT_OK ? ok() : cs;
+  }
+  WsLayout w;
+  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
+  if (st != BURNEXT_OK) return st;
+  const WsPtrs p = ws_ptrs(*L, w, workspace);
+  st = run_route(L, x, xb, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p, true, true, s);
+  if (st != BURNEXT_OK) return st;
+
+  const int nt = xb ? 1 : 3;
+  const uint32_t max_active = (uint32_t)std::min<uint64_t>(L->E, n * L->K);
+  auto gemv = [&](bool gate_up) -> burnext_status {
+    const TiledMx &t = gate_up ? L->w1 : L->w2;
+    GemvArgs g{};
+    g.wb = t.blocks;
+    g.ws = t.scales;
+    g.wb_estride = t.blocks_per_expert;
+    g.ws_estride = t.scales_per_expert;
+    g.bias = L->b1;
+    g.bias_estride = L->w1.rows_p;
+    g.nrt = t.nrt;
+    g.nb = t.nb;
+    g.kt = t.cols;
+    g.out_rows = gate_up ? L->F : L->D;
+    g.tiles_per_wg = 8;
+    const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
+    uint32_t mt = (uint32_t)std::min<uint64_t>(16, n);
+    mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
+    g.mt_max = mt;
+    g.seg_off = p.seg_off;
+    g.active = p.active;
+    g.num_active = p.num_active;
+    g.perm = p.perm;
+    g.topk = L->K;
+    g.bterms = p.xn;
+    g.bf32 = p.act;
+    g.out = gate_up ? p.act : p.ypart;
+    g.out_stride = gate_up ? L->Fp : L->Dp;
+    g.alpha = L->alpha;
+    g.limit = L->limit;
+    const uint32_t gx = (uint32_t)cdiv(t.nrt, g.tiles_per_wg);
+    ProfScope ps(L, s, gate_up ? 2 : 3);
+    return check_launch(launch_gemv(g, nt, gate_up, gx, max_active, s), gate_up ? "gate_up launch" : "down launch");
+  };
+  st = gemv(true);
+  if (st != BURNEXT_OK) return st;
+  st = gemv(false);
+  if (st != BURNEXT_OK) return st;
+
+  CombineArgs c{};
+  c.x = x;
+  c.y = y;
+  c.ypart = p.ypart;
+  c.b2 = L->b2;
+  c.topk_idx = p.topk_idx;
+  c.topk_w = p.topk_w;
+  c.pos_of = p.pos_of;
+  c.n = (uint32_t)n;
+  c.D = L->D;
+  c.Dp = L->Dp;
+  c.E = L->E;
+  c.K = L->K;
+  c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
+  {
+    ProfScope ps(L, s, 4);
+    st = check_launch(launch_combine(c, xb, s), "combine launch");
+  }
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, uint64_t n,
+                                 uint32_t flags, int32_t *topk_idx, float *topk_w, float *logits, void *workspace,
+                                 uint64_t ws_bytes, void *stream) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
+  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  if (n == 0) return ok();
+  if (!x || !topk_idx || !topk_w) return fail(BURNEXT_INVALID_ARG, "null x / topk_idx / topk_w");
+  hipStream_t s = (hipStream_t)stream;
+  DeviceGuard guard(L->device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  WsLayout w;
+  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
+  if (st != BURNEXT_OK) return st;
+  WsPtrs p = ws_ptrs(*L, w, workspace);
+  p.topk_idx = topk_idx;
+  p.topk_w = topk_w;
+  if (logits) p.logits = logits;
+  st = run_route(L, x, x_dtype == BURNEXT_BF16, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p, false, false, s);
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_idx, uint64_t n, int32_t *seg_offsets,
+                                    int32_t *perm, void *workspace, uint64_t ws_bytes, void *stream) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  if (!topk_idx || !seg_offsets || !perm) return fail(BURNEXT_INVALID_ARG, "null topk_idx / seg_offsets / perm");
+  hipStream_t s = (hipStream_t)stream;
+  DeviceGuard guard(L->device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  WsLayout w;
+  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
+  if (st != BURNEXT_OK) return st;
+  const WsPtrs p = ws_ptrs(*L, w, workspace);
+  DispatchArgs da{};
+  da.topk_idx = topk_idx;
+  da.seg_off = seg_offsets;
+  da.perm = perm;
+  da.pos_of = p.pos_of;
+  da.active = p.active;
+  da.num_active = p.num_active;
+  da.n = (uint32_t)n;
+  da.K = L->K;
+  da.E = L->E;
+  st = check_launch(launch_dispatch(da, s), "dispatch kernel launch");
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8_t *blocks, const uint8_t *scales,
+                                     void *out, burnext_dtype out_dtype, void *stream) {
+  if (!desc || !blocks || !scales || !out) return fail(BURNEXT_INVALID_ARG, "null descriptor or buffer");
+  if (out_dtype != BURNEXT_F32 && out_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad out_dtype");
+  if (desc->bpr != cdiv(desc->cols, 2) || desc->gpr != cdiv(desc->cols, 32) || desc->ue8_offset < 0 ||
+      desc->ue8_offset > 255)
+    return fail(BURNEXT_INVALID_ARG, "descriptor bpr/gpr/ue8_offset inconsistent with cols");
+  DequantArgs a{};
+  a.blocks = blocks;
+  a.scales = scales;
+  a.out = out;
+  a.rows = desc->experts * desc->rows;
+  a.cols = desc->cols;
+  a.bpr = desc->bpr;
+  a.gpr = desc->gpr;
+  a.ue8_offset = desc->ue8_offset;
+  a.out_bf16 = out_dtype == BURNEXT_BF16;
+  burnext_status st = check_launch(launch_dequant(a, (hipStream_t)stream), "dequant launch");
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+burnext_status burnext_moe_profile_enable(burnext_moe_layer_t L, int enable) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  L->profiling = enable != 0;
+  return ok();
+}
+
+burnext_status burnext_moe_profile_read(burnext_moe_layer_t L, double *ms_total, uint64_t *launches, int n_kernels) {
+  if (!L || !ms_total || !launches || n_kernels < 0) return fail(BURNEXT_INVALID_ARG, "null argument");
+  for (int k = 0; k < n_kernels; ++k) {
+    ms_total[k] = 0.0;
+    launches[k] = 0;
+  }
+  std::vector<ProfPair> pend;
+  {
+    std::lock_guard<std::mutex> lk(L->prof_mu);
+    pend.swap(L->prof);
+  }
+  DeviceGuard guard(L->device);
+  burnext_status st = BURNEXT_OK;
+  for (auto &pp : pend) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(pp.b) != hipSuccess || hipEventElapsedTime(&ms, pp.a, pp.b) != hipSuccess)
+      st = BURNEXT_DEVICE_ERROR;
+    if (pp.kernel < n_kernels) {
+      ms_total[pp.kernel] += ms;
+      launches[pp.kernel] += 1;
+    }
+    (void)hipEventDestroy(pp.a);
+    (void)hipEventDestroy(pp.b);
+  }
+  if (st != BURNEXT_OK) return fail(st, "event synchronisation failed");
+  return ok();
+}
+
+}  // extern "C"

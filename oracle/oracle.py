@@ -1,0 +1,202 @@
+"""ctypes front-end of the CPU oracle (oracle/moe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() (as the checker) and
+bench.py's cpu_baseline leg.  The product library never loads it.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import pathlib
+import subprocess
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "_build" / "libmoe_oracle.so"
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64 = ctypes.c_int64
+
+
+class _Cfg(ctypes.Structure):
+    _fields_ = [("d", ctypes.c_int64), ("f", ctypes.c_int64), ("e", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("alpha", ctypes.c_float), ("limit", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.oracle_fp4_value.restype = ctypes.c_float
+        L.oracle_fp4_value.argtypes = [ctypes.c_int]
+        L.oracle_e8m0_scale.restype = ctypes.c_float
+        L.oracle_e8m0_scale.argtypes = [ctypes.c_int]
+        L.oracle_dequant_mxfp4_bytes.argtypes = [_u8p, _u8p, _i64, _i64, _f32p]
+        L.oracle_dequant_matrix.argtypes = [_u8p, _u8p, _i64, _i64, _i64, _i64, ctypes.c_int, _f32p]
+        L.oracle_rmsnorm.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_float, _f32p]
+        L.oracle_router.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p]
+        L.oracle_topk_softmax.argtypes = [_f32p, _i64, _i64, _i64, _i32p, _f32p]
+        L.oracle_dispatch.argtypes = [_i32p, _i64, _i64, _i64, _i32p, _i32p, _i32p]
+        L.oracle_swiglu.restype = ctypes.c_float
+        L.oracle_swiglu.argtypes = [ctypes.c_float] * 4
+        fwd = [_f32p, _i64, ctypes.POINTER(_Cfg), _u8p, _u8p, _u8p, _u8p, ctypes.c_int, _f32p, _f32p, _f32p,
+               _f32p, _f32p]
+        L.oracle_moe_forward.argtypes = fwd + [ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _f32p]
+        L.oracle_moe_forward.restype = ctypes.c_int
+        L.oracle_moe_forward_reference.argtypes = fwd + [ctypes.c_int, _f32p]
+        L.oracle_moe_forward_reference.restype = ctypes.c_int
+        L.oracle_num_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t) if a is not None else None
+
+
+def _c(a, dt):
+    return None if a is None else np.ascontiguousarray(a, dtype=dt)
+
+
+def fp4_value(nib: int) -> float:
+    return lib().oracle_fp4_value(nib)
+
+
+def e8m0_scale(s: int) -> float:
+    return lib().oracle_e8m0_scale(s)
+
+
+def dequant_mxfp4_bytes(blocks, blocks_shape, scales, scales_shape) -> np.ndarray:
+    """Signature of the reference test helper (src/loader/mxfp4.rs:56-79)."""
+    rows = int(np.prod(scales_shape)) if len(scales_shape) else 1
+    b = int(blocks_shape[-1])
+    bl = _c(np.asarray(blocks, np.uint8).reshape(-1), np.uint8)
+    sc = _c(np.asarray(scales, np.uint8).reshape(-1), np.uint8)
+    assert bl.size == rows * b and sc.size == rows
+    out = np.empty(rows * 2 * b, np.float32)
+    lib().oracle_dequant_mxfp4_bytes(_p(bl, _u8p), _p(sc, _u8p), rows, b, _p(out, _f32p))
+    return out
+
+
+def dequant_matrix(blocks, scales, rows, cols, ue8_offset=0) -> np.ndarray:
+    bpr, gpr = (cols + 1) // 2, (cols + 31) // 32
+    bl = _c(blocks, np.uint8).reshape(-1)
+    sc = _c(scales, np.uint8).reshape(-1)
+    assert bl.size == rows * bpr and sc.size == rows * gpr
+    out = np.empty((rows, cols), np.float32)
+    lib().oracle_dequant_matrix(_p(bl, _u8p), _p(sc, _u8p), rows, cols, bpr, gpr, ue8_offset, _p(out, _f32p))
+    return out
+
+
+def rmsnorm(x, gamma=None, eps=1e-5) -> np.ndarray:
+    x = _c(x, np.float32)
+    n, d = x.shape
+    g = _c(gamma, np.float32)
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(_p(x, _f32p), n, d, _p(g, _f32p), eps, _p(out, _f32p))
+    return out
+
+
+def router(xn, w, b=None) -> np.ndarray:
+    xn, w, b = _c(xn, np.float32), _c(w, np.float32), _c(b, np.float32)
+    n, d = xn.shape
+    e = w.shape[0]
+    out = np.empty((n, e), np.float32)
+    lib().oracle_router(_p(xn, _f32p), n, d, _p(w, _f32p), _p(b, _f32p), e, _p(out, _f32p))
+    return out
+
+
+def topk_softmax(logits, k):
+    lg = _c(logits, np.float32)
+    n, e = lg.shape
+    kk = min(max(int(k), 1), e)
+    idx = np.empty((n, kk), np.int32)
+    w = np.empty((n, kk), np.float32)
+    lib().oracle_topk_softmax(_p(lg, _f32p), n, e, kk, _p(idx, _i32p), _p(w, _f32p))
+    return idx, w
+
+
+def dispatch(idx, num_experts):
+    idx = _c(idx, np.int32)
+    n, k = idx.shape
+    seg = np.empty(num_experts + 1, np.int32)
+    perm = np.empty(n * k, np.int32)
+    pos = np.empty(n * k, np.int32)
+    lib().oracle_dispatch(_p(idx, _i32p), n, k, num_experts, _p(seg, _i32p), _p(perm, _i32p), _p(pos, _i32p))
+    return seg, perm, pos
+
+
+def swiglu(g, l, alpha=1.702, limit=7.0) -> float:
+    return lib().oracle_swiglu(g, l, alpha, limit)
+
+
+def _layer_args(layer):
+    cfg = _Cfg(layer.d_model, layer.ffn_hidden, layer.num_experts, layer.experts_per_token, layer.swiglu_alpha,
+               layer.swiglu_limit, layer.rms_eps)
+    arrs = dict(w1b=_c(layer.w1_blocks, np.uint8), w1s=_c(layer.w1_scales, np.uint8),
+                w2b=_c(layer.w2_blocks, np.uint8), w2s=_c(layer.w2_scales, np.uint8),
+                b1=_c(layer.b1_f32, np.float32), b2=_c(layer.b2_f32, np.float32),
+                rw=_c(layer.router_w_f32, np.float32), rb=_c(layer.router_b_f32, np.float32),
+                g=_c(layer.gamma_f32, np.float32))
+    return cfg, arrs
+
+
+def moe_forward(layer, x, apply_rmsnorm=True, add_residual=True, layout=None):
+    """The build's layer semantics (see oracle_moe_forward).  Returns (y, idx, w)."""
+    x = _c(x, np.float32)
+    n, d = x.shape
+    assert d == layer.d_model
+    cfg, a = _layer_args(layer)
+    kk = min(max(layer.experts_per_token, 1), layer.num_experts)
+    lay = {"halves": 0, "interleaved": 1}[layout or layer.gate_up_layout]
+    y = np.empty_like(x)
+    idx = np.empty((n, kk), np.int32)
+    w = np.empty((n, kk), np.float32)
+    rc = lib().oracle_moe_forward(_p(x, _f32p), n, ctypes.byref(cfg), _p(a["w1b"], _u8p), _p(a["w1s"], _u8p),
+                                  _p(a["w2b"], _u8p), _p(a["w2s"], _u8p), layer.ue8_offset, _p(a["b1"], _f32p),
+                                  _p(a["b2"], _f32p), _p(a["rw"], _f32p), _p(a["rb"], _f32p), _p(a["g"], _f32p),
+                                  lay, int(apply_rmsnorm), int(add_residual), _p(y, _f32p), _p(idx, _i32p),
+                                  _p(w, _f32p))
+    assert rc == 0
+    return y, idx, w
+
+
+def moe_forward_reference(layer, x, b2_per_ftile=True):
+    """Literal reference algorithm (halves pairing, dense W1, b2 per f-tile unless b2_per_ftile is
+    False), OpenMP-parallel."""
+    x = _c(x, np.float32)
+    n, d = x.shape
+    cfg, a = _layer_args(layer)
+    y = np.empty_like(x)
+    rc = lib().oracle_moe_forward_reference(_p(x, _f32p), n, ctypes.byref(cfg), _p(a["w1b"], _u8p),
+                                            _p(a["w1s"], _u8p), _p(a["w2b"], _u8p), _p(a["w2s"], _u8p),
+                                            layer.ue8_offset, _p(a["b1"], _f32p), _p(a["b2"], _f32p),
+                                            _p(a["rw"], _f32p), _p(a["rb"], _f32p), _p(a["g"], _f32p),
+                                            int(b2_per_ftile), _p(y, _f32p))
+    assert rc == 0
+    return y
+
+
+def num_threads() -> int:
+    return lib().oracle_num_threads()
+
+
+def max_abs_rel(y, ref) -> float:
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.max(np.abs(ref))
+    return float(np.max(np.abs(y - ref)) / (den if den > 0 else 1.0))
+
+
+__all__ = [n for n in dir() if not n.startswith("_")]
+

@@ -1,0 +1,391 @@
+"""CPU tests that pin the oracle (oracle/moe_oracle.c) before it is trusted as the GPU checker.
+
+Each oracle function is checked against something other than its own formula: the reference's
+known answers, exhaustive enumeration against numpy/ldexp, exact rational arithmetic for the
+fixed reduction order, float64 brute force, the HF transformers GPT-OSS experts module (a
+third-party implementation of the same layer), hand-computed closed forms, and invariants chosen
+so that a dropped term, a swapped gate/linear row, a wrong nibble or a transposed operand fails.
+"""
+import json
+import math
+import pathlib
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def synth():
+    from burnext_amd import synth as s
+    return s
+
+
+# e2m1 closed form from the bit fields (sign | e1 e0 | m), independent of the oracle's LUT
+def e2m1_closed_form(code: int) -> float:
+    s, e, m = (code >> 3) & 1, (code >> 1) & 3, code & 1
+    mag = m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2)
+    return -mag if s else mag
+
+
+# ---------------------------------------------------------------------------------------------
+# dequantisation
+# ---------------------------------------------------------------------------------------------
+def test_reference_dequant_kats(oracle):
+    kats = json.loads((GOLDEN / "mxfp4_dequant_kats.json").read_text())
+    for case in kats["cases"]:
+        out = oracle.dequant_mxfp4_bytes(kats["blocks"], kats["blocks_shape"], [case["scale"]], kats["scales_shape"])
+        assert out.tolist() == case["expect"]
+
+
+def test_fp4_lut_closed_form(oracle):
+    for code in range(16):
+        v = oracle.fp4_value(code)
+        assert v == e2m1_closed_form(code)
+        assert math.copysign(1.0, v) == (-1.0 if code >= 8 else 1.0)  # code 8 is -0.0
+
+
+def test_dequant_exhaustive_vs_ldexp(oracle):
+    """All 16 codes x 256 scale bytes, bit-exact against float32 LUT * ldexp (f32 product)."""
+    blocks = np.tile(np.arange(256, dtype=np.uint8), (256, 1))
+    scales = np.arange(256, dtype=np.uint8)
+    out = oracle.dequant_mxfp4_bytes(blocks, [256, 256], scales, [256]).reshape(256, 512)
+    lut = np.array([e2m1_closed_form(c) for c in range(16)], np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        sc = np.array([np.float32(math.ldexp(1.0, s - 127)) if s < 255 else np.float32(np.inf) for s in range(256)],
+                      np.float32)
+        lo = lut[np.arange(256) & 15][None, :] * sc[:, None]
+        hi = lut[np.arange(256) >> 4][None, :] * sc[:, None]
+    exp = np.empty((256, 512), np.float32)
+    exp[:, 0::2], exp[:, 1::2] = lo, hi
+    both_nan = np.isnan(exp) & np.isnan(out)
+    assert np.array_equal(exp.view(np.uint32)[~both_nan], out.view(np.uint32)[~both_nan])
+    assert np.array_equal(np.isnan(exp), np.isnan(out))
+    # special cases: s=0 is the subnormal 2^-127, s=255 overflows to inf, 0*inf is NaN
+    assert oracle.e8m0_scale(0) == 2.0 ** -127 and oracle.e8m0_scale(255) == np.inf
+    assert out[0, 2] == 0.5 * 2.0 ** -127 and np.isnan(out[255, 0]) and out[255, 2] == np.inf
+
+
+def test_dequant_matrix_scale_groups_and_offset(oracle):
+    """Scale group = column // 32, low nibble = even column, and ue8_offset inverts the model.bin
+    writer's wrapping add (stored = s + 14 mod 256)."""
+    rows, cols = 3, 70  # partial last byte-group and last scale group
+    bpr, gpr = (cols + 1) // 2, (cols + 31) // 32
+    rng = np.random.default_rng(1)
+    blocks = rng.integers(0, 256, (rows, bpr), dtype=np.uint8)
+    true_s = rng.integers(100, 140, (rows, gpr))
+    out = oracle.dequant_matrix(blocks, true_s.astype(np.uint8), rows, cols, 0)
+    for r in range(rows):
+        for c in range(cols):
+            b = int(blocks[r, c // 2])
+            code = (b >> 4) if c % 2 else (b & 15)
+            assert out[r, c] == np.float32(e2m1_closed_form(code) * 2.0 ** (int(true_s[r, c // 32]) - 127))
+    stored = ((true_s + 14) & 255).astype(np.uint8)
+    assert np.array_equal(oracle.dequant_matrix(blocks, stored, rows, cols, 14).view(np.uint32), out.view(np.uint32))
+    wrapped = np.array([[250, 5]], np.int64)  # true exponents >= 242 wrap below 14 when stored
+    st = ((wrapped + 14) & 255).astype(np.uint8)
+    b1 = np.full((1, 32), 0x22, np.uint8)
+    o = oracle.dequant_matrix(b1, st, 1, 64, 14)
+    assert o[0, 0] == np.float32(2.0 ** (250 - 127)) and o[0, 32] == np.float32(2.0 ** (5 - 127))
+
+
+# ---------------------------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------------------------
+def _f32(x):
+    return float(np.float32(x))
+
+
+def _exact_fma(a, b, c):
+    return _f32(Fraction(a) * Fraction(b) + Fraction(c))
+
+
+def _exact_lane_dot(a, b):
+    """The route kernel's order with exactly rounded fma (rational arithmetic)."""
+    p = []
+    for lane in range(64):
+        acc = 0.0
+        for c in range(lane, len(a), 64):
+            acc = _exact_fma(float(a[c]), float(b[c]), acc)
+        p.append(acc)
+    for off in (32, 16, 8, 4, 2, 1):
+        p = [_f32(p[i] + p[i ^ off]) for i in range(64)]
+    assert len(set(p)) == 1  # commutativity: every lane ends with the same value
+    return p[0]
+
+
+def test_router_order_exact_rational(oracle):
+    rng = np.random.default_rng(2)
+    D, E, n = 200, 5, 3
+    x = rng.standard_normal((n, D)).astype(np.float32)
+    w = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    lg = oracle.router(x, w, b)
+    for t in range(n):
+        for e in range(E):
+            assert lg[t, e] == _f32(_exact_lane_dot(x[t], w[e]) + float(b[e]))
+    np.testing.assert_allclose(lg, x.astype(np.float64) @ w.T.astype(np.float64) + b, rtol=1e-5, atol=1e-6)
+
+
+def test_rmsnorm_exact_and_f64(oracle):
+    rng = np.random.default_rng(3)
+    D = 150
+    x = rng.standard_normal((4, D)).astype(np.float32) * 3
+    g = rng.standard_normal(D).astype(np.float32)
+    xn = oracle.rmsnorm(x, g, 1e-5)
+    for t in range(4):
+        ss = _exact_lane_dot(x[t], x[t])
+        ms = np.float32(ss) / np.float32(D)
+        r = np.sqrt(np.float32(ms + np.float32(1e-5)), dtype=np.float32)
+        exp = (x[t] / r).astype(np.float32) * g
+        assert np.array_equal(xn[t].view(np.uint32), exp.astype(np.float32).view(np.uint32))
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-5) * g
+    np.testing.assert_allclose(xn, ref, rtol=2e-6, atol=1e-6)
+
+
+def test_topk_brute_force_and_ties(oracle):
+    rng = np.random.default_rng(4)
+    # integer-valued logits: many exact ties, plus -inf entries
+    lg = rng.integers(-3, 3, (200, 16)).astype(np.float32)
+    lg[rng.random(lg.shape) < 0.1] = -np.inf
+    for k in (1, 2, 4, 16):
+        idx, w = oracle.topk_softmax(lg, k)
+        for t in range(lg.shape[0]):
+            order = np.lexsort((np.arange(16), -lg[t]))[:k]  # value desc, then index asc
+            assert idx[t].tolist() == order.tolist()
+            v = lg[t, order].astype(np.float64)
+            finite = np.isfinite(v[0])
+            if finite:
+                e = np.exp(v - v[0])
+                np.testing.assert_allclose(w[t], e / e.sum(), rtol=1e-6)
+                assert abs(w[t].sum() - 1) < 1e-6 * k
+    # k is clamped to [1, E] (src/moe/mod.rs:133)
+    idx, _ = oracle.topk_softmax(lg[:2, :3], 9)
+    assert idx.shape == (2, 3)
+
+
+def test_topk_nan_is_lowest(oracle):
+    lg = np.array([[np.nan, 1.0, np.nan, 0.5]], np.float32)
+    idx, _ = oracle.topk_softmax(lg, 4)
+    assert idx.tolist() == [[1, 3, 0, 2]]
+
+
+def test_dispatch_invariants(oracle):
+    rng = np.random.default_rng(5)
+    for n, E, k in ((1, 4, 4), (37, 7, 3), (2000, 32, 4), (513, 128, 4)):
+        idx = np.stack([rng.permutation(E)[:k] for _ in range(n)]).astype(np.int32)
+        seg, perm, pos = oracle.dispatch(idx, E)
+        assert np.array_equal(np.diff(seg), np.bincount(idx.ravel(), minlength=E))
+        assert seg[0] == 0 and seg[-1] == n * k
+        assert np.array_equal(np.sort(perm), np.arange(n * k))
+        assert np.array_equal(perm[pos], np.arange(n * k))
+        flat = idx.ravel()
+        for e in range(E):
+            ent = perm[seg[e]:seg[e + 1]]
+            assert (flat[ent] == e).all()
+            assert (np.diff(ent // k) > 0).all()  # tokens ascending (stable)
+
+
+def test_swiglu_closed_forms(oracle):
+    a, lim = 1.702, 7.0
+
+    def f64(g, l):
+        g, l = min(g, lim), max(-lim, min(l, lim))
+        return g / (1 + math.exp(-a * g)) * (l + 1)
+
+    for g, l in ((0.3, -0.2), (7.0, 2.0), (12.0, 2.0), (-3.0, 9.0), (1.0, -9.0), (5.0, 0.0)):
+        assert abs(oracle.swiglu(g, l, a, lim) - f64(g, l)) <= 1e-6 * max(1.0, abs(f64(g, l)))
+    assert oracle.swiglu(12.0, 2.0) == oracle.swiglu(7.0, 2.0)  # gate clamps above at 7
+    assert oracle.swiglu(1.0, 30.0) == oracle.swiglu(1.0, 7.0)  # linear clamps at +-7
+    assert oracle.swiglu(1.0, -30.0) == oracle.swiglu(1.0, -7.0)
+    assert oracle.swiglu(-1e30, 3.0) == 0.0  # gate -> -inf gives 0
+    assert oracle.swiglu(2.0, -1.0) == 0.0  # (lin + 1) factor
+
+
+# ---------------------------------------------------------------------------------------------
+# full layer
+# ---------------------------------------------------------------------------------------------
+def dequant_np(blocks, scales, cols, ue8=0):
+    """Independent numpy dequantisation ([..., rows, bpr] bytes -> [..., rows, cols] float64)."""
+    lut = np.array([e2m1_closed_form(c) for c in range(16)])
+    lo, hi = lut[blocks & 15], lut[blocks >> 4]
+    vals = np.stack([lo, hi], axis=-1).reshape(*blocks.shape[:-1], -1)[..., :cols]
+    s = ((scales.astype(np.int64) - ue8) & 255) - 127
+    return vals * np.repeat(np.ldexp(1.0, s), 32, axis=-1)[..., :cols]
+
+
+def layer_f64(L, x, idx, w, layout, norm=True, residual=True):
+    """float64 brute force of the layer for given routing (matmul-based, not the oracle's loops)."""
+    D, F = L.d_model, L.ffn_hidden
+    x64 = x.astype(np.float64)
+    xn = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + L.rms_eps) if norm else x64
+    if L.gamma_f32 is not None and norm:
+        xn = xn * L.gamma_f32
+    W1 = dequant_np(L.w1_blocks, L.w1_scales, D, L.ue8_offset)
+    W2 = dequant_np(L.w2_blocks, L.w2_scales, F, L.ue8_offset)
+    if layout == "interleaved":
+        gi, li = np.arange(F) * 2, np.arange(F) * 2 + 1
+    else:
+        gi, li = np.arange(F), np.arange(F) + F
+    y = x64.copy() if residual else np.zeros_like(x64)
+    for t in range(x.shape[0]):
+        for p in range(idx.shape[1]):
+            e = idx[t, p]
+            h = W1[e] @ xn[t] + L.b1_f32[e]
+            g, l = np.minimum(h[gi], L.swiglu_limit), np.clip(h[li], -L.swiglu_limit, L.swiglu_limit)
+            act = g / (1 + np.exp(-L.swiglu_alpha * g)) * (l + 1)
+            y[t] += w[t, p] * (W2[e] @ act + L.b2_f32[e])
+    return y
+
+
+@pytest.mark.parametrize("layout", ["interleaved", "halves"])
+@pytest.mark.parametrize("ue8", [0, 14])
+def test_forward_vs_f64(oracle, layout, ue8):
+    S = synth()
+    L = S.make_layer(256, 256, 2, 2, seed=0, dtype="f32", ue8_offset=ue8, gate_up_layout=layout)
+    x = S.make_tokens(16, 256, seed=0, dtype="f32")
+    y, idx, w = oracle.moe_forward(L, x)
+    ref = layer_f64(L, x, idx, w.astype(np.float64), layout)
+    assert oracle.max_abs_rel(y, ref) < 2e-6
+
+
+def test_forward_vs_f64_20b_shape(oracle):
+    S = synth()
+    L = S.make_layer(2880, 2880, 32, 4, seed=0, dtype="bf16", with_gamma=True)
+    x = S.make_tokens(2, 2880, seed=0, dtype="bf16")
+    y, idx, w = oracle.moe_forward(L, x)
+    ref = layer_f64(L, x, idx, w.astype(np.float64), "interleaved")
+    assert oracle.max_abs_rel(y, ref) < 1e-5
+    assert oracle.max_abs_rel(y - x, ref - x) < 1e-4
+
+
+def test_forward_matches_hf_gpt_oss_experts(oracle):
+    """Third-party GPT-OSS experts (transformers) with the oracle's routing, float64."""
+    torch = pytest.importorskip("torch")
+    tr = pytest.importorskip("transformers")
+    from transformers.models.gpt_oss import modeling_gpt_oss as hf
+    S = synth()
+    D, F, E, K = 64, 96, 4, 2
+    L = S.make_layer(D, F, E, K, seed=7, dtype="f32")
+    x = S.make_tokens(5, D, seed=7, dtype="f32")
+    y, idx, w = oracle.moe_forward(L, x, apply_rmsnorm=False, add_residual=False)
+    cfg = tr.GptOssConfig(hidden_size=D, intermediate_size=F, num_local_experts=E, num_experts_per_tok=K)
+    ex = hf.GptOssExperts(cfg).double()
+    W1 = dequant_np(L.w1_blocks, L.w1_scales, D)  # [E, 2F, D], interleaved rows
+    W2 = dequant_np(L.w2_blocks, L.w2_scales, F)  # [E, D, F]
+    with torch.no_grad():
+        ex.gate_up_proj.copy_(torch.from_numpy(W1.transpose(0, 2, 1).copy()))
+        ex.gate_up_proj_bias.copy_(torch.from_numpy(L.b1_f32.astype(np.float64)))
+        ex.down_proj.copy_(torch.from_numpy(W2.transpose(0, 2, 1).copy()))
+        ex.down_proj_bias.copy_(torch.from_numpy(L.b2_f32.astype(np.float64)))
+        out = ex(torch.from_numpy(x.astype(np.float64)), torch.from_numpy(idx.astype(np.int64)),
+                 torch.from_numpy(w.astype(np.float64))).numpy()
+    assert oracle.max_abs_rel(y, out) < 2e-6
+
+
+def test_zero_weights_give_residual(oracle):
+    """tests/moe_basic_tests.rs:6-34 invariant (d=16, F=32, E=k=4, zero params => y == x)."""
+    S = synth()
+    L = S.make_layer(16, 32, 4, 4, dtype="f32")
+    for a in (L.w1_blocks, L.w1_scales, L.w2_blocks, L.w2_scales, L.b1_f32, L.b2_f32, L.router_w_f32):
+        a[...] = 0
+    L.swiglu_alpha = 1.0
+    x = S.make_tokens(6, 16, seed=1, dtype="f32")
+    y, _, _ = oracle.moe_forward(L, x)
+    assert np.array_equal(y, x)
+
+
+def test_layout_permutation_invariance(oracle):
+    """Re-ordering W1 rows + b1 from interleaved to halves, with the matching layout flag,
+    leaves the output bit-identical; using the wrong flag changes it."""
+    S = synth()
+    L = S.make_layer(64, 48, 3, 2, seed=3, dtype="f32")
+    x = S.make_tokens(7, 64, seed=3, dtype="f32")
+    y_int, _, _ = oracle.moe_forward(L, x, layout="interleaved")
+    perm = np.concatenate([np.arange(48) * 2, np.arange(48) * 2 + 1])  # halves row r <- interleaved perm[r]
+    H = S.make_layer(64, 48, 3, 2, seed=3, dtype="f32", gate_up_layout="halves")
+    H.w1_blocks, H.w1_scales, H.b1_f32 = L.w1_blocks[:, perm], L.w1_scales[:, perm], L.b1_f32[:, perm]
+    y_hal, _, _ = oracle.moe_forward(H, x, layout="halves")
+    assert np.array_equal(y_int, y_hal)
+    y_wrong, _, _ = oracle.moe_forward(H, x, layout="interleaved")
+    assert oracle.max_abs_rel(y_wrong, y_int) > 1e-3
+
+
+def test_one_hot_closed_form(oracle):
+    """Hand-computed layer: one gate weight, one linear weight, one down weight; k = 1."""
+    S = synth()
+    D, F, E = 32, 32, 2
+    L = S.make_layer(D, F, E, 1, dtype="f32")
+    for arr in (L.w1_blocks, L.w2_blocks, L.b1_f32, L.b2_f32, L.router_w_f32, L.router_b_f32):
+        arr[...] = 0
+    L.w1_scales[...] = 127
+    L.w2_scales[...] = 127
+    L.router_b_f32[1] = 1.0  # every token routes to expert 1 (weight 1)
+    # interleaved: row 0 = gate f0, row 1 = linear f0.  gate col 0 = code 2 (1.0) scale 127;
+    # linear col 1 = high nibble code 4 (2.0) with scale 128 -> 4.0
+    L.w1_blocks[1, 0, 0] = 0x02
+    L.w1_blocks[1, 1, 0] = 0x40
+    L.w1_scales[1, 1, 0] = 128
+    # down: row d=3, col f=0 = code 7 (6.0) scale 126 -> 3.0
+    L.w2_blocks[1, 3, 0] = 0x07
+    L.w2_scales[1, 3, 0] = 126
+    L.b2_f32[1, 5] = 0.25
+    a, b = 0.7, -0.4
+    x = np.zeros((1, D), np.float32)
+    x[0, 0], x[0, 1], x[0, 3] = a, b, 2.0
+    y, idx, w = oracle.moe_forward(L, x, apply_rmsnorm=False, add_residual=True)
+    assert idx.tolist() == [[1]] and w.tolist() == [[1.0]]
+    g, l = a * 1.0, b * 4.0
+    act0 = g / (1 + math.exp(-1.702 * g)) * (l + 1)
+    exp = x.astype(np.float64).copy()
+    exp[0, 3] += act0 * 3.0
+    exp[0, 5] += 0.25
+    np.testing.assert_allclose(y, exp, rtol=1e-6, atol=1e-7)
+
+
+def test_reference_literal_quirk_and_agreement(oracle):
+    """F <= 256: one f-tile, the literal reference algorithm equals the build semantics (halves).
+    F > 256: the reference adds b2 once per f-tile; the excess is (ceil(F/256)-1) * sum_p w_p b2."""
+    S = synth()
+    L = S.make_layer(128, 256, 4, 2, seed=2, dtype="f32", gate_up_layout="halves")
+    x = S.make_tokens(9, 128, seed=2, dtype="f32")
+    y_b, _, _ = oracle.moe_forward(L, x, layout="halves")
+    assert oracle.max_abs_rel(oracle.moe_forward_reference(L, x), y_b) < 2e-6
+    L2 = S.make_layer(128, 600, 4, 2, seed=2, dtype="f32", gate_up_layout="halves")
+    y_b, idx, w = oracle.moe_forward(L2, x, layout="halves")
+    y_q = oracle.moe_forward_reference(L2, x, b2_per_ftile=True)
+    y_once = oracle.moe_forward_reference(L2, x, b2_per_ftile=False)
+    assert oracle.max_abs_rel(y_once, y_b) < 2e-6
+    extra = np.zeros_like(y_b, dtype=np.float64)
+    for t in range(x.shape[0]):
+        for p in range(2):
+            extra[t] += 2 * w[t, p] * L2.b2_f32[idx[t, p]]  # ceil(600/256) - 1 = 2 extra adds
+    np.testing.assert_allclose(y_q - y_b, extra, atol=2e-5)
+
+
+def test_golden_tiny_fixture(oracle):
+    """Committed config-1 vectors: the generator reproduces the inputs, the oracle the outputs."""
+    S = synth()
+    g = np.load(GOLDEN / "tiny_c1.npz")
+    L = S.make_layer(256, 256, 2, 2, seed=0, dtype="f32")
+    x = S.make_tokens(16, 256, seed=0, dtype="f32")
+    for k, v in (("x", x), ("w1_blocks", L.w1_blocks), ("w1_scales", L.w1_scales), ("w2_blocks", L.w2_blocks),
+                 ("w2_scales", L.w2_scales), ("b1", L.b1_f32), ("b2", L.b2_f32), ("router_w", L.router_w_f32)):
+        assert np.array_equal(g[k], v), k
+    y_int, idx, w = oracle.moe_forward(L, x, layout="interleaved")
+    y_hal, _, _ = oracle.moe_forward(L, x, layout="halves")
+    assert np.array_equal(g["y_interleaved"], y_int) and np.array_equal(g["y_halves"], y_hal)
+    assert np.array_equal(g["topk_idx"], idx) and np.array_equal(g["topk_w"], w)
+
+
+def test_golden_decode_routing_fixture(oracle):
+    S = synth()
+    g = np.load(GOLDEN / "decode_c2_routing.npz")
+    x = S.bf16_bits_to_f32(g["x_bf16_bits"])
+    rw = S.bf16_bits_to_f32(g["router_w_bf16_bits"])
+    lg = oracle.router(oracle.rmsnorm(x, None, 1e-5), rw, np.zeros(32, np.float32))
+    assert np.array_equal(lg.view(np.uint32), g["logits"].view(np.uint32))
+    idx, w = oracle.topk_softmax(lg, 4)
+    assert np.array_equal(idx, g["topk_idx"]) and np.array_equal(w, g["topk_w"])
