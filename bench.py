@@ -115,7 +115,7 @@ def main():
     kbytes = {
         "gate_up": touched * w1_bytes + T * D * 2 + nk * F * 4,
         "down": touched * w2_bytes + nk * F * 4 + nk * D * 4,
-        "route": E * D * 2 + E * 2 + T * D * 2 + T * D * 2 + nk * 8,
+        "router": E * D * 2 + E * 2 + T * D * 2 + T * D * 2 + T * E * 4,
         "combine": nk * D * 4 + touched * D * 2 + 2 * T * D * 2 + nk * 12,
     }
     kflops = {"gate_up": 2 * nk * 2 * F * D, "down": 2 * nk * D * F}

@@ -1,11 +1,15 @@
 // kernels.hip -- MI355X (gfx950) kernels of the GPT-OSS MoE feed-forward over MXFP4 experts.
 //
-// route_kernel      RmsNorm + router logits + top-k/softmax (+ dispatch for one-workgroup batches)
-//                   replaces src/moe/mod.rs:109-110,271-276 (Burn RmsNorm/Linear/topk ops)
+// router_kernel     RmsNorm + router logits, parallel over token blocks x expert groups
+//                   replaces src/moe/mod.rs:109-110 (Burn RmsNorm / Linear)
+// topk_kernel       top-k + softmax over the selected logits, one wave per token
+//                   replaces src/moe/mod.rs:271-276 (topk_with_indices, max/exp/sum/div)
 // dispatch_kernel   histogram / exclusive scan / stable scatter into expert segments
 //                   replaces the per-expert dense masks of src/moe/mod.rs:279-288
+// small_route       top-k/softmax/dispatch of a decode-sized batch by one workgroup
 // expert_gemv       MXFP4 x bf16 projection on MFMA 16x16x32 bf16, e2m1+e8m0 dequantised in
-//                   registers; gate_up epilogue fuses bias + clamped SwiGLU
+//                   registers; gate_up staging applies the RmsNorm and the epilogue fuses bias +
+//                   clamped SwiGLU
 //                   replaces w1_swiglu_dense_kernel / w2_scatter_dense_kernel (src/quant/gpu.rs:89-192)
 // combine_kernel    y = x + sum_p w_p * (down_p + b2), deterministic slot order
 //                   replaces the accumulate + residual of src/moe/mod.rs:405-411
@@ -21,10 +25,272 @@ __device__ __forceinline__ void store_val(float *p, size_t i, float v) { p[i] = 
 __device__ __forceinline__ void store_val(uint16_t *p, size_t i, float v) { p[i] = f32_to_bf16_bits(v); }
 
 // ---------------------------------------------------------------------------------------------
-// Dispatch by one workgroup.  Stable counting sort of the flat entries t*K+p by expert: the rank
-// of (t, e) inside expert e's segment is the number of earlier tokens that chose e, computed per
-// chunk of blockDim.x tokens from a per-expert token bitmap (order-independent atomicOr) and
-// popcount prefixes, so the result does not depend on thread timing.
+// 8-element chunks: raw register form between load and use, and guarded scalar loads.
+// ---------------------------------------------------------------------------------------------
+template <typename T> struct Chunk8;
+template <> struct Chunk8<float> {
+  float4 a, b;
+};
+template <> struct Chunk8<uint16_t> {
+  uint4 a;
+};
+__device__ __forceinline__ void chunk_load(Chunk8<float> &c, const float *p) {
+  c.a = *(const float4 *)p;
+  c.b = *(const float4 *)(p + 4);
+}
+__device__ __forceinline__ void chunk_load(Chunk8<uint16_t> &c, const uint16_t *p) { c.a = *(const uint4 *)p; }
+__device__ __forceinline__ void chunk_vals(const Chunk8<float> &c, float (&v)[8]) {
+  v[0] = c.a.x; v[1] = c.a.y; v[2] = c.a.z; v[3] = c.a.w; v[4] = c.b.x; v[5] = c.b.y; v[6] = c.b.z; v[7] = c.b.w;
+}
+__device__ __forceinline__ void chunk_vals(const Chunk8<uint16_t> &c, float (&v)[8]) {
+  const uint32_t w4[4] = {c.a.x, c.a.y, c.a.z, c.a.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(w4[j] << 16);
+    v[2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void load8_guarded(const T *p, uint32_t nvalid, float (&v)[8]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; ++j) v[j] = j < nvalid ? load_val(p, j) : 0.0f;
+}
+
+// Register chunks held per router row: 6 (3072 columns) for bf16 rows, 3 for f32 rows.
+template <typename WT> struct RouteChunks { static constexpr int value = sizeof(WT) == 2 ? 6 : 3; };
+
+// Lane-transposed LDS position of element c of a row: element 512 i + 8 l + j lives at
+// 512 i + 64 j + l, so lane l reading its chunk element j hits consecutive addresses across the
+// wave (conflict-free) in the fixed reduction order.
+__device__ __forceinline__ uint32_t tpos(uint32_t c) { return (c & ~511u) | ((c & 7u) << 6) | ((c & 511u) >> 3); }
+__device__ __forceinline__ uint32_t tpos_inv(uint32_t q) { return (q & ~511u) | ((q & 63u) << 3) | ((q >> 6) & 7u); }
+
+// ---------------------------------------------------------------------------------------------
+// Router kernel.  Grid (token blocks of tb <= 8, expert groups of 4 * epw); 4 waves.
+// Fixed reduction order of every dot product, mirrored by the oracle: lane l owns the
+// 8-element chunks c = 512 i + 8 l + j; its partial is fmaf over i ascending then j ascending;
+// then the xor butterfly over the 64 lanes.  With apply_norm the normalisation comes after the
+// dot product: logit = dot(x, gamma * w) / sqrt(dot(x, x) / D + eps) + b.
+//  1. each wave issues the loads of its router rows (registers) before anything else
+//  2. the workgroup stages its tokens into LDS (lane-transposed layout)
+//  3. dot products for all tokens of the block, butterflies interleaved across tokens
+//  4. sums of squares -> r per token (expert group 0 writes r for the expert GEMV staging)
+// ---------------------------------------------------------------------------------------------
+size_t router_lds_bytes(uint32_t tb, uint32_t Dpad) { return sizeof(float) * ((size_t)tb * Dpad + 8); }
+
+template <int N>
+__device__ __forceinline__ void wave_sum_butterfly_n(float (&v)[N]) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + __shfl_xor(v[i], off, 64);
+  }
+}
+
+template <typename XT, typename WT, bool VEC>
+__global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t D = a.D, Dpad = a.Dpad, E = a.E;
+  float *xs = (float *)smem;
+  float *rr = xs + (size_t)a.tb * Dpad;
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t t0 = blockIdx.x * a.tb;
+  const uint32_t nh = min(a.tb, a.n - t0);
+  const XT *x = (const XT *)a.x;
+  const WT *rw = (const WT *)a.rw;
+  constexpr int RC = RouteChunks<WT>::value;
+
+  // 1. router rows of this wave: experts eb + w and (epw == 2) eb + 4 + w
+  const uint32_t eb = blockIdx.y * 4u * a.epw;
+  const uint32_t e0 = eb + w, e1 = eb + 4u + w;
+  const bool has0 = e0 < E, has1 = a.epw == 2u && e1 < E;
+  Chunk8<WT> r0[RC], r1[RC];
+  if (VEC) {
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const uint32_t c0 = 512u * i + 8u * lane;
+      if (has0 && c0 < D) chunk_load(r0[i], rw + (size_t)e0 * D + c0);
+      if (has1 && c0 < D) chunk_load(r1[i], rw + (size_t)e1 * D + c0);
+    }
+  }
+
+  // 2. stage tokens (contiguous [nh, D])
+  if (VEC) {
+    const uint32_t nch = nh * D / 8u;
+    for (uint32_t base = threadIdx.x; base < nch; base += 4u * blockDim.x) {
+      Chunk8<XT> c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t ch = base + (uint32_t)u * blockDim.x;
+        if (ch < nch) chunk_load(c[u], x + (size_t)t0 * D + (size_t)ch * 8u);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t ch = base + (uint32_t)u * blockDim.x;
+        if (ch >= nch) continue;
+        const uint32_t f0 = ch * 8u, tt = f0 / D, c0 = f0 - tt * D;
+        float v[8];
+        chunk_vals(c[u], v);
+        float *dst = xs + (size_t)tt * Dpad + tpos(c0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[64 * j] = v[j];
+      }
+    }
+  } else {
+    for (uint32_t f = threadIdx.x; f < nh * D; f += blockDim.x) {
+      const uint32_t tt = f / D, c = f - tt * D;
+      xs[(size_t)tt * Dpad + tpos(c)] = load_val(x, (size_t)t0 * D + f);
+    }
+  }
+  __syncthreads();
+
+  // 4 (first, all waves): r per token, tokens w and w + 4 of the block
+  if (a.apply_norm) {
+    float ss[2] = {0.0f, 0.0f};
+    for (uint32_t c0 = 8u * lane; c0 < D; c0 += 512u) {
+      const uint32_t nv = min(8u, D - c0), q0 = tpos(c0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (w + 4u * h >= a.tb) continue;
+        const float *xq = xs + (size_t)(w + 4u * h) * Dpad + q0;
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j)
+          if (VEC || j < nv) ss[h] = fmaf(xq[64u * j], xq[64u * j], ss[h]);
+      }
+    }
+    wave_sum_butterfly_n<2>(ss);
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t tt = w + 4u * h;
+        if (tt < nh) {
+          rr[tt] = sqrtf(ss[h] / (float)D + a.eps);
+          if (a.rms && blockIdx.y == 0) a.rms[t0 + tt] = rr[tt];
+        }
+      }
+    }
+  }
+
+  // 3. dot products
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) acc0[tt] = acc1[tt] = 0.0f;
+  if (has0) {
+    for (uint32_t cg = 0; cg < D; cg += 512u * RC) {
+      if (VEC && cg > 0) {
+#pragma unroll
+        for (int i = 0; i < RC; ++i) {
+          const uint32_t c0 = cg + 512u * i + 8u * lane;
+          if (c0 < D) chunk_load(r0[i], rw + (size_t)e0 * D + c0);
+          if (has1 && c0 < D) chunk_load(r1[i], rw + (size_t)e1 * D + c0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        const uint32_t c0 = cg + 512u * i + 8u * lane;
+        if (c0 >= D) continue;
+        const uint32_t nv = min(8u, D - c0);
+        float w0[8], w1[8];
+        if (VEC) {
+          chunk_vals(r0[i], w0);
+          if (has1) chunk_vals(r1[i], w1);
+        } else {
+          load8_guarded(rw + (size_t)e0 * D + c0, nv, w0);
+          if (has1) load8_guarded(rw + (size_t)e1 * D + c0, nv, w1);
+        }
+        const uint32_t q0 = tpos(c0);
+#pragma unroll
+        for (uint32_t tt = 0; tt < 8u; ++tt) {
+          if (tt >= a.tb) break;
+          const float *xq = xs + (size_t)tt * Dpad + q0;  // rows in [nh, tb) hold stale data; unused
+#pragma unroll
+          for (uint32_t j = 0; j < 8u; ++j) {
+            if (VEC || j < nv) {
+              const float xv = xq[64u * j];
+              acc0[tt] = fmaf(xv, w0[j], acc0[tt]);
+              if (has1) acc1[tt] = fmaf(xv, w1[j], acc1[tt]);
+            }
+          }
+        }
+      }
+    }
+    wave_sum_butterfly_n<8>(acc0);
+    if (has1) wave_sum_butterfly_n<8>(acc1);
+  }
+  __syncthreads();  // rr visible
+  if (has0 && lane < nh) {
+    // lane tt writes token tt's logits (all lanes hold the reduced values)
+    float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+    for (uint32_t tt = 0; tt < 8u; ++tt)
+      if (lane == tt) {
+        v0 = acc0[tt];
+        v1 = acc1[tt];
+      }
+    const uint32_t t = t0 + lane;
+    const float r = a.apply_norm ? rr[lane] : 1.0f;
+    a.logits[(size_t)t * E + e0] = (a.apply_norm ? v0 / r : v0) + a.rb[e0];
+    if (has1) a.logits[(size_t)t * E + e1] = (a.apply_norm ? v1 / r : v1) + a.rb[e1];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Top-k by rank: the rank of expert e among a token's logits is the number of experts that beat
+// it under `beats` (larger value, NaN lowest, ties to the lower index); ranks < K are the
+// selection, in order.  Softmax over the selected logits: w_p = exp(v_p - v_0) / sum_q
+// exp(v_q - v_0), the sum taken q = 0..K-1 ascending from 0.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void rank_select(const float *lr, uint32_t E, uint32_t K, uint32_t e, int32_t *sel,
+                                            float *selv) {
+  const float v = lr[e];
+  uint32_t rank = 0;
+  for (uint32_t e2 = 0; e2 < E; ++e2) rank += beats(lr[e2], (int)e2, v, (int)e) ? 1u : 0u;
+  if (rank < K) {
+    sel[rank] = (int32_t)e;
+    selv[rank] = v;
+  }
+}
+
+__device__ __forceinline__ float softmax_weight(const float *selv, uint32_t K, uint32_t p) {
+  const float m = selv[0];
+  float s = 0.0f;
+  for (uint32_t q = 0; q < K; ++q) s += expf(selv[q] - m);
+  return expf(selv[p] - m) / s;
+}
+
+size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads) {
+  return (size_t)(threads / 64) * (sizeof(float) * E + 2 * sizeof(int32_t) * K);
+}
+
+// One wave per token; the workgroup's waves work on separate LDS rows, so only wave-level
+// ordering is needed between the phases (block barriers keep it simple and uniform).
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t t = blockIdx.x * (blockDim.x >> 6) + w;
+  float *lr = (float *)smem + (size_t)w * (a.E + 2 * a.K);
+  int32_t *sel = (int32_t *)(lr + a.E);
+  float *selv = (float *)(sel + a.K);
+  const bool live = t < a.n;
+  if (live)
+    for (uint32_t e = lane; e < a.E; e += 64) lr[e] = a.logits[(size_t)t * a.E + e];
+  __syncthreads();
+  if (live)
+    for (uint32_t e = lane; e < a.E; e += 64) rank_select(lr, a.E, a.K, e, sel, selv);
+  __syncthreads();
+  if (live) {
+    for (uint32_t p = lane; p < a.K; p += 64) {
+      a.topk_idx[(size_t)t * a.K + p] = sel[p];
+      a.topk_w[(size_t)t * a.K + p] = softmax_weight(selv, a.K, p);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dispatch by one workgroup (any batch size).  Stable counting sort of the flat entries t*K+p by
+// expert: the rank of (t, e) inside expert e's segment is the number of earlier tokens that chose
+// e, computed per chunk of blockDim.x tokens from a per-expert token bitmap (order-independent
+// atomicOr) and popcount prefixes, so the result does not depend on thread timing.
 // LDS: cnt[E], base[E], bm[E * words], wpre[E * words] (words = blockDim.x / 32).
 // ---------------------------------------------------------------------------------------------
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
@@ -41,17 +307,22 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
     if (e >= 0 && (uint32_t)e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int32_t run = 0, na = 0;
-    for (uint32_t e = 0; e < E; ++e) {
-      seg_off[e] = run;
-      base[e] = run;
-      if (cnt[e] > 0) active[na++] = (int32_t)e;
-      run += cnt[e];
+  // exclusive scan and active list, each expert's thread summing the counts below it
+  for (uint32_t e = tid; e < E; e += nth) {
+    int32_t off = 0, ra = 0;
+    for (uint32_t e2 = 0; e2 < e; ++e2) {
+      off += cnt[e2];
+      ra += cnt[e2] > 0;
     }
-    seg_off[E] = run;
-    for (uint32_t e = (uint32_t)na; e < E; ++e) active[e] = -1;
-    *num_active = na;
+    seg_off[e] = off;
+    base[e] = off;
+    if (cnt[e] > 0) active[ra] = (int32_t)e;
+    if (e + 1 == E) {
+      seg_off[E] = off + cnt[e];
+      const int32_t na = ra + (cnt[e] > 0);
+      *num_active = na;
+      for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) active[e3] = -1;
+    }
   }
   __syncthreads();
   for (uint32_t c0 = 0; c0 < n; c0 += nth) {
@@ -91,153 +362,74 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
 
 size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) { return sizeof(int32_t) * (size_t)E * (2 + 2 * (threads / 32)); }
 
-size_t route_lds_bytes(uint32_t tpb, uint32_t D, uint32_t E, uint32_t K, uint32_t threads) {
-  size_t b = sizeof(float) * (size_t)tpb * D + sizeof(float) * (size_t)tpb * E + 2 * sizeof(int32_t) * (size_t)tpb * K;
-  return b + dispatch_lds_bytes(E, threads);
-}
-
-// ---------------------------------------------------------------------------------------------
-// Route kernel: one workgroup of 8 waves per block of tpb (<= 8) tokens.
-//  phase 0  wave w loads token w, optional RmsNorm (sum of squares in the fixed lane/butterfly
-//           order), keeps xn in LDS and writes its bf16 terms for the expert GEMVs
-//  phase 1  logits: wave w computes experts w, w+8, ... for all tokens of the block; per logit
-//           lane partials fmaf over c = lane + 64 i, then the butterfly, then + bias
-//  phase 2  top-k: wave w selects token w's experts by repeated wave arg-max under `beats`
-//           (ties -> lower index), softmax over the selected logits (lane 0, ascending order)
-//  phase 3  (fuse_dispatch) the same workgroup builds the expert segments
-// ---------------------------------------------------------------------------------------------
-template <typename XT, typename WT>
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const uint32_t tpb = a.tpb, D = a.D, E = a.E, K = a.K;
-  float *xs = (float *)smem;
-  float *lg = xs + (size_t)tpb * D;
-  int32_t *sel = (int32_t *)(lg + (size_t)tpb * E);
-  float *selv = (float *)(sel + (size_t)tpb * K);
-  int32_t *dlds = (int32_t *)(selv + (size_t)tpb * K);
-
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  const uint32_t t0 = blockIdx.x * tpb;
-  const uint32_t nh = min(tpb, a.n - t0);
-  const XT *x = (const XT *)a.x;
-
-  // phase 0
-  if (w < nh) {
-    const uint32_t t = t0 + w;
-    float *xr = xs + (size_t)w * D;
-    float p = 0.0f;
-    for (uint32_t c = lane; c < D; c += 64) {
-      const float v = load_val(x, (size_t)t * D + c);
-      xr[c] = v;
-      p = fmaf(v, v, p);
-    }
-    if (a.apply_norm) {
-      p = wave_sum_butterfly(p);
-      const float ms = p / (float)D;
-      const float r = sqrtf(ms + a.eps);
-      for (uint32_t c = lane; c < D; c += 64) xr[c] = (xr[c] / r) * a.gamma[c];
-    }
-    if (a.xn_terms) {
-      uint16_t *dst = a.xn_terms + (size_t)t * a.nt * a.Dp;
-      for (uint32_t c = lane; c < a.Dp; c += 64) {
-        float v = c < D ? xr[c] : 0.0f;
-        for (uint32_t i = 0; i < a.nt; ++i) {
-          const uint16_t b = f32_to_bf16_bits(v);
-          dst[(size_t)i * a.Dp + c] = b;
-          v = v - bf16_bits_to_f32(b);
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // phase 1
-  const WT *rw = (const WT *)a.rw;
-  for (uint32_t e = w; e < E; e += nwaves) {
-    float acc[8];
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) acc[tt] = 0.0f;
-    const WT *wr = rw + (size_t)e * D;
-    for (uint32_t c = lane; c < D; c += 64) {
-      const float wv = load_val(wr, c);
-#pragma unroll
-      for (uint32_t tt = 0; tt < 8; ++tt)
-        if (tt < nh) acc[tt] = fmaf(xs[(size_t)tt * D + c], wv, acc[tt]);
-    }
-#pragma unroll
-    for (uint32_t tt = 0; tt < 8; ++tt) {
-      if (tt < nh) {
-        const float s = wave_sum_butterfly(acc[tt]);
-        if (lane == 0) lg[tt * E + e] = s + a.rb[e];
-      }
-    }
-  }
-  __syncthreads();
-
-  // phase 2
-  if (w < nh) {
-    const uint32_t t = t0 + w;
-    const float *lr = lg + (size_t)w * E;
-    float v[4];
-    bool tk[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t e = lane + 64u * j;
-      v[j] = e < E ? lr[e] : 0.0f;
-      tk[j] = e >= E;
-    }
-    for (uint32_t p = 0; p < K; ++p) {
-      float bv = 0.0f;
-      int bi = -1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = (int)(lane + 64u * j);
-        if (!tk[j] && (bi < 0 || beats(v[j], e, bv, bi))) {
-          bv = v[j];
-          bi = e;
-        }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (oi >= 0 && (bi < 0 || beats(ov, oi, bv, bi))) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (bi == (int)(lane + 64u * j)) tk[j] = true;
-      if (lane == 0) {
-        sel[w * K + p] = bi;
-        selv[w * K + p] = bv;
-      }
-    }
-    if (lane == 0) {
-      const float m = selv[w * K];
-      float s = 0.0f;
-      for (uint32_t p = 0; p < K; ++p) s += expf(selv[w * K + p] - m);
-      for (uint32_t p = 0; p < K; ++p) {
-        a.topk_idx[(size_t)t * K + p] = sel[w * K + p];
-        a.topk_w[(size_t)t * K + p] = expf(selv[w * K + p] - m) / s;
-      }
-    }
-    if (a.logits)
-      for (uint32_t e = lane; e < E; e += 64) a.logits[(size_t)t * E + e] = lr[e];
-  }
-
-  // phase 3
-  if (a.fuse_dispatch) {
-    __syncthreads();
-    block_dispatch(sel, a.n, K, E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, dlds);
-  }
-}
-
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active,
-                 (int32_t *)smem);
+  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, (int32_t *)smem);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Routing of a decode-sized batch (T <= 16) by one workgroup, all in LDS, no serial loops over
+// tokens: top-k by rank, softmax, histogram by counting, exclusive scan by per-expert sums, and
+// segment positions pos(t, e) = seg_off[e] + #{t' < t : t' chose e}.  Same results as
+// topk_kernel + block_dispatch.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kSmallRouteThreads) void small_route_kernel(SmallRouteArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t T = a.n, E = a.E, K = a.K;
+  const uint32_t tid = threadIdx.x, nth = blockDim.x;
+  float *lg = (float *)smem;
+  int32_t *sel = (int32_t *)(lg + T * E);
+  float *selv = (float *)(sel + T * K);
+  int32_t *cnt = (int32_t *)(selv + T * K);
+  int32_t *seg = cnt + E;
+  for (uint32_t i = tid; i < T * E; i += nth) lg[i] = a.logits[i];
+  __syncthreads();
+  for (uint32_t i = tid; i < T * E; i += nth) {
+    const uint32_t t = i / E, e = i - t * E;
+    rank_select(lg + t * E, E, K, e, sel + t * K, selv + t * K);
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < T * K; i += nth) {
+    const uint32_t t = i / K, p = i - t * K;
+    a.topk_idx[i] = sel[i];
+    a.topk_w[i] = softmax_weight(selv + t * K, K, p);
+  }
+  for (uint32_t e = tid; e < E; e += nth) {
+    int32_t c = 0;
+#pragma unroll 8
+    for (uint32_t i = 0; i < T * K; ++i) c += sel[i] == (int32_t)e;
+    cnt[e] = c;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < E; e += nth) {
+    int32_t off = 0, ra = 0;
+#pragma unroll 8
+    for (uint32_t e2 = 0; e2 < e; ++e2) {
+      const int32_t c2 = cnt[e2];
+      off += c2;
+      ra += c2 > 0;
+    }
+    seg[e] = off;
+    a.seg_off[e] = off;
+    if (cnt[e] > 0) a.active[ra] = (int32_t)e;
+    if (e + 1 == E) {
+      const int32_t na = ra + (cnt[e] > 0);
+      a.seg_off[E] = off + cnt[e];
+      *a.num_active = na;
+      for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) a.active[e3] = -1;
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < T * K; i += nth) {
+    const uint32_t t = i / K;
+    const int32_t e = sel[i];
+    int32_t rk = 0;
+#pragma unroll 8
+    for (uint32_t i2 = 0; i2 < t * K; ++i2) rk += sel[i2] == e;
+    const int32_t pos = seg[e] + rk;
+    a.perm[pos] = (int32_t)i;
+    a.pos_of[i] = pos;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -253,9 +445,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 // (row, token, k) exactly once.  Output: lane holds C[rows 4q..4q+3][token j].
 // f32 activations are split into NT bf16 terms (NT MFMAs per step).
 // ---------------------------------------------------------------------------------------------
-size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
-  return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
-}
 
 __device__ __forceinline__ float swiglu_clamp(float g, float l, float alpha, float limit) {
   const float xg = fminf(g, limit);
@@ -264,107 +453,189 @@ __device__ __forceinline__ float swiglu_clamp(float g, float l, float alpha, flo
   return (xg * sig) * (xl + 1.0f);
 }
 
-template <int NT, bool GATE_UP>
-__global__ __launch_bounds__(kGemvThreads) void expert_gemv_kernel(GemvArgs a) {
-  const int ai = (int)blockIdx.y;
-  if (ai >= *a.num_active) return;
-  const uint32_t rt_begin = blockIdx.x * a.tiles_per_wg;
-  if (rt_begin >= a.nrt) return;
-  const int e = a.active[ai];
-  const int seg0 = a.seg_off[e];
-  const int M = a.seg_off[e + 1] - seg0;
-
+// Grid of G workgroups (as many as stay resident).  Each active expert gets wpe = G / num_active
+// workgroups, each owning a contiguous range of that expert's row tiles, so every workgroup
+// stages one expert's B operand once.  The B operand (xn = x * (1/r) * gamma split into NT bf16
+// terms, or the f32 act rows of the down projection) is staged into LDS with every global load of
+// a batch issued before any is consumed; the first weight chunk is requested before staging.
+// Each wave then streams its tiles with the next chunk's loads -- also across tile boundaries --
+// in flight while the current chunk is on the matrix cores.
+template <int NT, bool GATE_UP, typename XT>
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t *bs = (uint16_t *)smem;
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
+  const uint32_t mtm = a.mt_max;
+  uint16_t *bs = (uint16_t *)smem;
+  int32_t *tok_l = (int32_t *)(smem + gemv_lds_bytes(NT, mtm, a.nb));  // [mtm]
+  float *r_l = (float *)(tok_l + mtm);                                    // [mtm]
+  const uint32_t nrt = a.nrt;
+  const uint32_t na = (uint32_t)*a.num_active;
+  if (na == 0) return;
+  const uint32_t wpe = max(1u, gridDim.x / na);
+  const uint32_t ai = blockIdx.x / wpe, part = blockIdx.x % wpe;
+  if (ai >= na) return;
+  const uint32_t tpw = (nrt + wpe - 1) / wpe;  // tiles per workgroup
+  const uint32_t rt_lo = part * tpw;
+  const uint32_t rt_hi = min(nrt, rt_lo + tpw);
+  if (rt_lo >= rt_hi) return;
+
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
-  const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
-  const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
   const uint32_t nkg = (a.nb + 3u) >> 2;
   const uint32_t tail = a.nb - 4u * (nkg - 1u);
-  const uint32_t mtm = a.mt_max;
+  const uint32_t nch = (nkg + 3u) >> 2;  // 4-K-group chunks per tile
 
-  for (int m0 = 0; m0 < M; m0 += (int)mtm) {
-    const uint32_t mt = (uint32_t)min((int)mtm, M - m0);
-    __syncthreads();
-    // stage B: mt tokens x Kp, NT bf16 terms, zero beyond the true K
-    const uint32_t k8n = Kp >> 3;
-    for (uint32_t id = threadIdx.x; id < mt * k8n; id += blockDim.x) {
-      const uint32_t j = id / k8n, kb = (id % k8n) * 8u;
-      if constexpr (GATE_UP) {
-        const uint32_t tok = (uint32_t)a.perm[seg0 + m0 + (int)j] / a.topk;
+  // Unconditional loads: a lane whose (K-group, block) lies outside the tile reads the tile's
+  // first 16 bytes instead (always valid memory) and is neutralised at use time (scale 1.0 and a
+  // zero B operand).  No branch surrounds a load, so the compiler keeps the next chunk's loads
+  // in flight (partial vmcnt waits) while the current chunk is on the matrix cores.
+  auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
+  auto load_chunk = [&](const uint8_t *wt, const uint8_t *st, uint32_t c0, uint4(&av)[4], uint32_t(&sv)[4]) {
 #pragma unroll
-        for (int term = 0; term < NT; ++term) {
-          uint4 v = *(const uint4 *)(a.bterms + ((size_t)tok * NT + term) * Kp + kb);
-          if (kb + 8u > a.kt) {
-            uint16_t *h = (uint16_t *)&v;
-            for (uint32_t u = 0; u < 8u; ++u)
-              if (kb + u >= a.kt) h[u] = 0;
-          }
-          *(uint4 *)(bs + ((size_t)term * mtm + j) * ldk + kb) = v;
-        }
-      } else {
-        const float *src = a.bf32 + (size_t)(seg0 + m0 + (int)j) * Kp + kb;
-        const float4 lo = *(const float4 *)src, hi = *(const float4 *)(src + 4);
-        const float vals[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t kg = c0 + (uint32_t)u;
+      const bool ok = lane_ok(kg);
+      av[u] = *(const uint4 *)(wt + (ok ? kg * 1024u + lane * 16u : 0u));
+      sv[u] = (uint32_t)st[ok ? kg * 64u + lane : 0u];
+    }
+  };
+
+  {
+    const int e = a.active[ai];
+    const int seg0 = a.seg_off[e];
+    const int M = a.seg_off[e + 1] - seg0;
+    const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
+    const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
+    // this wave's tiles: rt_lo + wv, rt_lo + wv + 4, ...
+    const uint32_t my_first = rt_lo + wv;
+    const uint32_t my_tiles = my_first < rt_hi ? (rt_hi - my_first + 3u) / 4u : 0u;
+
+    for (int m0 = 0; m0 < M; m0 += (int)mtm) {
+      const uint32_t mt = (uint32_t)min((int)mtm, M - m0);
+      // first weight chunk requested before the staging
+      uint4 acur[4];
+      uint32_t scur[4];
+      if (my_tiles > 0)
+        load_chunk(wexp + (size_t)my_first * a.nb * 256u, sexp + (size_t)my_first * a.nb * 16u, 0u, acur, scur);
+      __syncthreads();
+      if (GATE_UP && threadIdx.x < mt) {
+        const int32_t tk = a.perm[seg0 + m0 + (int)threadIdx.x] / (int32_t)a.topk;
+        tok_l[threadIdx.x] = tk;
+        r_l[threadIdx.x] = a.apply_norm ? 1.0f / a.rms[tk] : 1.0f;  // within 1 ulp of dividing by r
+      }
+      __syncthreads();
+      // stage B: mt tokens x Kp, NT bf16 terms, zero beyond the true K; batches of SB items with
+      // all of a batch's global loads issued before any is consumed
+      constexpr int SB = 2;
+      const uint32_t k8n = Kp >> 3, nitems = mt * k8n;
+      auto store_item = [&](uint32_t id, const float (&v8)[8]) {
+        const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
         uint32_t pk[NT][4];
 #pragma unroll
-        for (int u = 0; u < 8; u += 2) {
+        for (int v = 0; v < 8; v += 2) {
           uint16_t t0[NT], t1[NT];
-          split_bf16<NT>(kb + (uint32_t)u < a.kt ? vals[u] : 0.0f, t0);
-          split_bf16<NT>(kb + (uint32_t)u + 1u < a.kt ? vals[u + 1] : 0.0f, t1);
+          split_bf16<NT>(v8[v], t0);
+          split_bf16<NT>(v8[v + 1], t1);
 #pragma unroll
-          for (int term = 0; term < NT; ++term) pk[term][u >> 1] = (uint32_t)t0[term] | ((uint32_t)t1[term] << 16);
+          for (int term = 0; term < NT; ++term) pk[term][v >> 1] = (uint32_t)t0[term] | ((uint32_t)t1[term] << 16);
         }
 #pragma unroll
         for (int term = 0; term < NT; ++term)
           *(uint4 *)(bs + ((size_t)term * mtm + j) * ldk + kb) = make_uint4(pk[term][0], pk[term][1], pk[term][2], pk[term][3]);
-      }
-    }
-    __syncthreads();
-
-    const bool bval = i16 < mt;
-    const uint16_t *brow = bs + (size_t)i16 * ldk;
-    for (uint32_t rt = rt_begin + wv; rt < min(rt_begin + a.tiles_per_wg, a.nrt); rt += 4u) {
-      const uint8_t *wt = wexp + (size_t)rt * a.nb * 256u;
-      const uint8_t *st = sexp + (size_t)rt * a.nb * 16u;
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      uint4 acur[4];
-      uint32_t scur[4];
+      };
+      for (uint32_t base = threadIdx.x; base < nitems; base += SB * blockDim.x) {
+        if constexpr (GATE_UP) {
+          Chunk8<XT> cx[SB];
+          Chunk8<float> cg[SB];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t kg = (uint32_t)u;
-        const bool ok = kg < nkg && q < (kg + 1u == nkg ? tail : 4u);
-        acur[u] = ok ? *(const uint4 *)(wt + kg * 1024u + lane * 16u) : make_uint4(0u, 0u, 0u, 0u);
-        scur[u] = ok ? (uint32_t)st[kg * 64u + lane] : 0u;
+          for (int u = 0; u < SB; ++u) {
+            const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitems - 1u);
+            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+            if (a.x_vec && kb + 8u <= a.kt) {
+              chunk_load(cx[u], (const XT *)a.x + (size_t)tok_l[j] * a.kt + kb);
+              if (a.apply_norm) chunk_load(cg[u], a.gamma + kb);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < SB; ++u) {
+            const uint32_t id = base + (uint32_t)u * blockDim.x;
+            if (id >= nitems) continue;
+            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+            const uint32_t nv = kb < a.kt ? min(8u, a.kt - kb) : 0u;
+            float v8[8], g8[8];
+            if (a.x_vec && nv == 8u) {
+              chunk_vals(cx[u], v8);
+              if (a.apply_norm) chunk_vals(cg[u], g8);
+            } else {
+              load8_guarded((const XT *)a.x + (size_t)tok_l[j] * a.kt + kb, nv, v8);
+              if (a.apply_norm) load8_guarded(a.gamma + kb, nv, g8);
+            }
+            const float ir = r_l[j];
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+              v8[v] = (uint32_t)v < nv ? (a.apply_norm ? (v8[v] * ir) * g8[v] : v8[v]) : 0.0f;
+            store_item(id, v8);
+          }
+        } else {
+          float4 lo[SB], hi[SB];
+#pragma unroll
+          for (int u = 0; u < SB; ++u) {
+            const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitems - 1u);
+            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+            const float *src = a.act + (size_t)(seg0 + m0 + (int)j) * Kp + kb;
+            lo[u] = *(const float4 *)src;
+            hi[u] = *(const float4 *)(src + 4);
+          }
+#pragma unroll
+          for (int u = 0; u < SB; ++u) {
+            const uint32_t id = base + (uint32_t)u * blockDim.x;
+            if (id >= nitems) continue;
+            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+            const float t8[8] = {lo[u].x, lo[u].y, lo[u].z, lo[u].w, hi[u].x, hi[u].y, hi[u].z, hi[u].w};
+            float v8[8];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) v8[v] = kb + (uint32_t)v < a.kt ? t8[v] : 0.0f;
+            store_item(id, v8);
+          }
+        }
       }
-      for (uint32_t c0 = 0; c0 < nkg; c0 += 4u) {
+      __syncthreads();
+
+      const bool bval = i16 < mt;
+      const uint16_t *brow = bs + (size_t)i16 * ldk;
+      const uint32_t nsteps = my_tiles * nch;
+      uint32_t ti = 0, c = 0;  // tile ordinal and chunk inside the tile of the current step
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (uint32_t g = 0; g < nsteps; ++g) {
+        const uint32_t rt = my_first + 4u * ti;
+        // prefetch the next step (next chunk of this tile, or chunk 0 of the next tile)
         uint4 anx[4];
         uint32_t snx[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t kg = c0 + 4u + (uint32_t)u;
-          const bool ok = kg < nkg && q < (kg + 1u == nkg ? tail : 4u);
-          anx[u] = ok ? *(const uint4 *)(wt + kg * 1024u + lane * 16u) : make_uint4(0u, 0u, 0u, 0u);
-          snx[u] = ok ? (uint32_t)st[kg * 64u + lane] : 0u;
+        {
+          // next step: next chunk of this tile, chunk 0 of the next tile, or (last step) the
+          // current chunk again -- a cache hit that keeps the load count static
+          const bool last_c = c + 1u == nch;
+          const bool more = g + 1u < nsteps;
+          const uint32_t nrt_ = (last_c && more) ? rt + 4u : rt;
+          const uint32_t nc = more ? (last_c ? 0u : c + 1u) : c;
+          load_chunk(wexp + (size_t)nrt_ * a.nb * 256u, sexp + (size_t)nrt_ * a.nb * 16u, 4u * nc, anx, snx);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const uint32_t kg = c0 + (uint32_t)u;
-          if (kg >= nkg) break;
-          const bool ok = q < (kg + 1u == nkg ? tail : 4u);
+          const uint32_t kg = 4u * c + (uint32_t)u;
+          const bool ok = lane_ok(kg);
           const bool bok = bval && ok;
-          const float sc = e8m0_to_f32(scur[u]);
-          const uint32_t kb = 32u * (4u * kg + q);
+          const float sc = ok ? e8m0_to_f32(scur[u]) : 1.0f;
+          const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
           const uint32_t wd[4] = {acur[u].x, acur[u].y, acur[u].z, acur[u].w};
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
 #pragma unroll
             for (int term = 0; term < NT; ++term) {
-              bf16x8_t B = {};
-              if (bok) B = *(const bf16x8_t *)(brow + (size_t)term * mtm * ldk + kb + 8u * s);
+              const u32x4_t raw = *(const u32x4_t *)(brow + (size_t)term * mtm * ldk + kb + 8u * s);
+              const u32x4_t z = {0u, 0u, 0u, 0u};
+              const bf16x8_t B = __builtin_bit_cast(bf16x8_t, bok ? raw : z);
               acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, acc, 0, 0, 0);
             }
           }
@@ -374,30 +645,37 @@ __global__ __launch_bounds__(kGemvThreads) void expert_gemv_kernel(GemvArgs a) {
           acur[u] = anx[u];
           scur[u] = snx[u];
         }
-      }
-      // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
-      if (bval) {
-        const int pos = seg0 + m0 + (int)i16;
-        const uint32_t r0 = rt * 16u + 4u * q;
-        if constexpr (GATE_UP) {
-          const float *bb = a.bias + (size_t)e * a.bias_estride + r0;
-          const uint32_t f0 = r0 >> 1;
-          const float o0 = swiglu_clamp(acc[0] + bb[0], acc[1] + bb[1], a.alpha, a.limit);
-          const float o1 = swiglu_clamp(acc[2] + bb[2], acc[3] + bb[3], a.alpha, a.limit);
-          float *o = a.out + (size_t)pos * a.out_stride + f0;
-          if (f0 + 1u < a.out_rows) {
-            *(float2 *)o = make_float2(o0, o1);
-          } else if (f0 < a.out_rows) {
-            o[0] = o0;
+        if (c + 1u == nch) {
+          // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
+          if (bval) {
+            const int pos = seg0 + m0 + (int)i16;
+            const uint32_t r0 = rt * 16u + 4u * q;
+            if constexpr (GATE_UP) {
+              const float *bb = a.bias + (size_t)e * a.bias_estride + r0;
+              const uint32_t f0 = r0 >> 1;
+              const float o0 = swiglu_clamp(acc[0] + bb[0], acc[1] + bb[1], a.alpha, a.limit);
+              const float o1 = swiglu_clamp(acc[2] + bb[2], acc[3] + bb[3], a.alpha, a.limit);
+              float *o = a.out + (size_t)pos * a.out_stride + f0;
+              if (f0 + 1u < a.out_rows) {
+                *(float2 *)o = make_float2(o0, o1);
+              } else if (f0 < a.out_rows) {
+                o[0] = o0;
+              }
+            } else {
+              float *o = a.out + (size_t)pos * a.out_stride + r0;
+              if (r0 + 3u < a.out_rows) {
+                *(float4 *)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+              } else {
+                for (uint32_t r = 0; r < 4u; ++r)
+                  if (r0 + r < a.out_rows) o[r] = acc[r];
+              }
+            }
           }
+          acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          c = 0;
+          ++ti;
         } else {
-          float *o = a.out + (size_t)pos * a.out_stride + r0;
-          if (r0 + 3u < a.out_rows) {
-            *(float4 *)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
-          } else {
-            for (uint32_t r = 0; r < 4u; ++r)
-              if (r0 + r < a.out_rows) o[r] = acc[r];
-          }
+          ++c;
         }
       }
     }
@@ -406,23 +684,58 @@ __global__ __launch_bounds__(kGemvThreads) void expert_gemv_kernel(GemvArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Combine: y[t, d] = (add_residual ? x[t, d] : 0) + sum_{p asc} (ypart[pos(t,p), d] + b2[e_p, d]) * w_p
+// Four outputs per thread; the token's routing loads are issued together.
 // ---------------------------------------------------------------------------------------------
 template <typename XT>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const uint32_t t = blockIdx.y;
-  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d >= a.D) return;
-  float acc = 0.0f;
-  for (uint32_t p = 0; p < a.K; ++p) {
-    const int32_t e = a.topk_idx[(size_t)t * a.K + p];
-    if (e < 0 || (uint32_t)e >= a.E) continue;
-    const float w = a.topk_w[(size_t)t * a.K + p];
-    const int32_t pos = a.pos_of[(size_t)t * a.K + p];
-    acc = acc + (a.ypart[(size_t)pos * a.Dp + d] + a.b2[(size_t)e * a.D + d]) * w;
+  const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4u;
+  if (d0 >= a.D) return;
+  const uint32_t nv = min(4u, a.D - d0);
+  const bool vec4 = (a.D % 4u) == 0u;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t p0 = 0; p0 < a.K; p0 += 8u) {
+    int32_t ev[8], pv[8];
+    float wv[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t p = p0 + u;
+      const bool in = p < a.K;
+      ev[u] = in ? a.topk_idx[(size_t)t * a.K + p] : -1;
+      wv[u] = in ? a.topk_w[(size_t)t * a.K + p] : 0.0f;
+      pv[u] = in ? a.pos_of[(size_t)t * a.K + p] : 0;
+    }
+    float4 yv[8], bv[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const bool ok = ev[u] >= 0 && (uint32_t)ev[u] < a.E;
+      const float *yp = a.ypart + (size_t)pv[u] * a.Dp + d0;
+      const float *bp = a.b2 + (size_t)(ok ? ev[u] : 0) * a.D + d0;
+      if (ok && vec4) {
+        yv[u] = *(const float4 *)yp;
+        bv[u] = *(const float4 *)bp;
+      } else if (ok) {
+        yv[u] = make_float4(yp[0], nv > 1 ? yp[1] : 0.f, nv > 2 ? yp[2] : 0.f, nv > 3 ? yp[3] : 0.f);
+        bv[u] = make_float4(bp[0], nv > 1 ? bp[1] : 0.f, nv > 2 ? bp[2] : 0.f, nv > 3 ? bp[3] : 0.f);
+      } else {
+        yv[u] = bv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      if (!(ev[u] >= 0 && (uint32_t)ev[u] < a.E)) continue;
+      acc[0] = acc[0] + (yv[u].x + bv[u].x) * wv[u];
+      acc[1] = acc[1] + (yv[u].y + bv[u].y) * wv[u];
+      acc[2] = acc[2] + (yv[u].z + bv[u].z) * wv[u];
+      acc[3] = acc[3] + (yv[u].w + bv[u].w) * wv[u];
+    }
   }
   const XT *x = (const XT *)a.x;
-  const float r = (a.add_residual ? load_val(x, (size_t)t * a.D + d) : 0.0f) + acc;
-  store_val((XT *)a.y, (size_t)t * a.D + d, r);
+  XT *y = (XT *)a.y;
+  for (uint32_t j = 0; j < nv; ++j) {
+    const size_t i = (size_t)t * a.D + d0 + j;
+    store_val(y, i, (a.add_residual ? load_val(x, i) : 0.0f) + acc[j]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -463,33 +776,64 @@ hipError_t configure_kernels() {
     hipError_t e_ = hipFuncSetAttribute((const void *)(f), hipFuncAttributeMaxDynamicSharedMemorySize, big);       \
     if (e_ != hipSuccess && err == hipSuccess) err = e_;                                                             \
   } while (0)
-  BX_ATTR((route_kernel<float, float>));
-  BX_ATTR((route_kernel<float, uint16_t>));
-  BX_ATTR((route_kernel<uint16_t, float>));
-  BX_ATTR((route_kernel<uint16_t, uint16_t>));
+  BX_ATTR((router_kernel<float, float, true>));
+  BX_ATTR((router_kernel<float, uint16_t, true>));
+  BX_ATTR((router_kernel<uint16_t, float, true>));
+  BX_ATTR((router_kernel<uint16_t, uint16_t, true>));
+  BX_ATTR((router_kernel<float, float, false>));
+  BX_ATTR((router_kernel<float, uint16_t, false>));
+  BX_ATTR((router_kernel<uint16_t, float, false>));
+  BX_ATTR((router_kernel<uint16_t, uint16_t, false>));
+  BX_ATTR(small_route_kernel);
+  BX_ATTR(topk_kernel);
   BX_ATTR(dispatch_kernel);
-  BX_ATTR((expert_gemv_kernel<1, true>));
-  BX_ATTR((expert_gemv_kernel<1, false>));
-  BX_ATTR((expert_gemv_kernel<3, true>));
-  BX_ATTR((expert_gemv_kernel<3, false>));
+  BX_ATTR((expert_gemv_kernel<1, true, uint16_t>));
+  BX_ATTR((expert_gemv_kernel<1, true, float>));
+  BX_ATTR((expert_gemv_kernel<1, false, float>));
+  BX_ATTR((expert_gemv_kernel<3, true, uint16_t>));
+  BX_ATTR((expert_gemv_kernel<3, true, float>));
+  BX_ATTR((expert_gemv_kernel<3, false, float>));
 #undef BX_ATTR
   return err;
 }
 
-hipError_t launch_route(const RouteArgs &a, bool x_bf16, bool w_bf16, hipStream_t s) {
-  const dim3 grid((a.n + a.tpb - 1) / a.tpb), block(kRouteThreads);
-  const size_t lds = route_lds_bytes(a.tpb, a.D, a.E, a.K, kRouteThreads);
+template <typename XT, typename WT>
+static void router_launch(const RouterArgs &a, bool vec, dim3 grid, size_t lds, hipStream_t s) {
+  if (vec)
+    router_kernel<XT, WT, true><<<grid, dim3(kRouterThreads), lds, s>>>(a);
+  else
+    router_kernel<XT, WT, false><<<grid, dim3(kRouterThreads), lds, s>>>(a);
+}
+
+hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s) {
+  const dim3 grid((a.n + a.tb - 1) / a.tb, (a.E + 4 * a.epw - 1) / (4 * a.epw));
+  const size_t lds = router_lds_bytes(a.tb, a.Dpad);
   if (x_bf16) {
     if (w_bf16)
-      route_kernel<uint16_t, uint16_t><<<grid, block, lds, s>>>(a);
+      router_launch<uint16_t, uint16_t>(a, vec, grid, lds, s);
     else
-      route_kernel<uint16_t, float><<<grid, block, lds, s>>>(a);
+      router_launch<uint16_t, float>(a, vec, grid, lds, s);
   } else {
     if (w_bf16)
-      route_kernel<float, uint16_t><<<grid, block, lds, s>>>(a);
+      router_launch<float, uint16_t>(a, vec, grid, lds, s);
     else
-      route_kernel<float, float><<<grid, block, lds, s>>>(a);
+      router_launch<float, float>(a, vec, grid, lds, s);
   }
+  return hipGetLastError();
+}
+
+size_t small_route_kernel_lds(uint32_t T, uint32_t E, uint32_t K) {
+  return sizeof(int32_t) * ((size_t)T * E + 2 * (size_t)T * K + 2 * (size_t)E);
+}
+
+hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
+  small_route_kernel<<<dim3(1), dim3(kSmallRouteThreads), small_route_kernel_lds(a.n, a.E, a.K), s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const TopkArgs &a, hipStream_t s) {
+  const uint32_t wpb = kTopkThreads / 64;
+  topk_kernel<<<dim3((a.n + wpb - 1) / wpb), dim3(kTopkThreads), topk_lds_bytes(a.E, a.K, kTopkThreads), s>>>(a);
   return hipGetLastError();
 }
 
@@ -498,19 +842,23 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, uint32_t grid_x, uint32_t grid_y, hipStream_t s) {
-  const dim3 grid(grid_x, grid_y), block(kGemvThreads);
-  const size_t lds = gemv_lds_bytes(nt, a.mt_max, a.nb);
+hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
+  const dim3 g(grid), block(kGemvThreads);
+  const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb);
   if (nt == 1) {
-    if (gate_up)
-      expert_gemv_kernel<1, true><<<grid, block, lds, s>>>(a);
+    if (!gate_up)
+      expert_gemv_kernel<1, false, float><<<g, block, lds, s>>>(a);
+    else if (x_bf16)
+      expert_gemv_kernel<1, true, uint16_t><<<g, block, lds, s>>>(a);
     else
-      expert_gemv_kernel<1, false><<<grid, block, lds, s>>>(a);
+      expert_gemv_kernel<1, true, float><<<g, block, lds, s>>>(a);
   } else if (nt == 3) {
-    if (gate_up)
-      expert_gemv_kernel<3, true><<<grid, block, lds, s>>>(a);
+    if (!gate_up)
+      expert_gemv_kernel<3, false, float><<<g, block, lds, s>>>(a);
+    else if (x_bf16)
+      expert_gemv_kernel<3, true, uint16_t><<<g, block, lds, s>>>(a);
     else
-      expert_gemv_kernel<3, false><<<grid, block, lds, s>>>(a);
+      expert_gemv_kernel<3, true, float><<<g, block, lds, s>>>(a);
   } else {
     return hipErrorInvalidValue;
   }
@@ -518,7 +866,7 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, uint32_t grid_x,
 }
 
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
-  const dim3 grid((a.D + 255) / 256, a.n), block(256);
+  const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
   if (x_bf16)
     combine_kernel<uint16_t><<<grid, block, 0, s>>>(a);
   else

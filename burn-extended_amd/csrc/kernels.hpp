@@ -5,22 +5,26 @@
 
 namespace burnext {
 
-// Route: optional RmsNorm, router logits, top-k + softmax, bf16 activation terms for the
-// expert GEMVs, and (single-workgroup batches) the dispatch into expert segments.
-struct RouteArgs {
+// Router logits for a block of tokens x a group of experts.  With apply_norm the rows are the
+// gamma-folded router weights and logit = dot(x, gw) / r + b, r = sqrt(mean(x^2) + eps); the
+// workgroups of expert group 0 also write r per token for the expert GEMV staging.
+struct RouterArgs {
   const void *x;
-  const void *rw;  // router weight [E, D] (f32 or bf16 bits)
-  const float *rb; // router bias [E]
-  const float *gamma;
-  uint16_t *xn_terms; // [n, nt, Dp] bf16 bits, nullable
-  float *logits;      // [n, E], nullable
-  int32_t *topk_idx;  // [n, K]
-  float *topk_w;      // [n, K]
-  int32_t *seg_off, *perm, *pos_of, *active, *num_active; // fused dispatch outputs
-  uint32_t n, D, Dp, E, K, tpb, nt;
+  const void *rw;     // router weight [E, D] (f32 or bf16 bits), gamma-folded when apply_norm
+  const float *rb;    // router bias [E]
+  float *logits;      // [n, E]
+  float *rms;         // [n] (written when apply_norm), nullable
+  uint32_t n, D, Dpad, E, tb, epw;
   float eps;
   int apply_norm;
-  int fuse_dispatch;
+};
+
+// Top-k + softmax per token (one wave per token) from logits [n, E].
+struct TopkArgs {
+  const float *logits;
+  int32_t *topk_idx;
+  float *topk_w;
+  uint32_t n, E, K;
 };
 
 struct DispatchArgs {
@@ -29,7 +33,8 @@ struct DispatchArgs {
   uint32_t n, K, E;
 };
 
-// One expert projection over the tiled MXFP4 layout (see layer.hip, "tiled layout").
+// One expert projection over the tiled MXFP4 layout (see the expert_gemv comment in kernels.hip).
+// Persistent-style: gridDim.x workgroups split the flattened (active expert, row tile) items.
 struct GemvArgs {
   const uint8_t *wb;      // tiled e2m1 blocks, expert stride wb_estride bytes
   const uint8_t *ws;      // tiled e8m0 scales, expert stride ws_estride bytes
@@ -40,15 +45,29 @@ struct GemvArgs {
   uint32_t nb;            // 32-wide K blocks (K padded = 32 * nb)
   uint32_t kt;            // true K
   uint32_t out_rows;      // gate_up: F output features; down: D
-  uint32_t tiles_per_wg;  // row tiles per workgroup (multiple of the 4 waves)
   uint32_t mt_max;        // tokens staged per pass (<= 16)
   const int32_t *seg_off, *active, *num_active, *perm;
   uint32_t topk;
-  const uint16_t *bterms; // gate_up B operand: xn terms [n, NT, Kp]
-  const float *bf32;      // down B operand: act [n*k, Kp] f32
+  // gate_up B operand: xn = apply_norm ? (x / rms[t]) * gamma : x, from x [n, kt] (x dtype)
+  const void *x;
+  const float *rms, *gamma;
+  int apply_norm;
+  int x_vec;              // x rows 16-byte aligned (base aligned, kt % 8 == 0): 128-bit loads
+  // down B operand: act [n*k, Kp] f32
+  const float *act;
   float *out;             // gate_up: act [n*k, Fp]; down: ypart [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
+};
+
+// Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,
+// dispatch, all outputs to global.
+struct SmallRouteArgs {
+  const float *logits;
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  uint32_t n, E, K;
 };
 
 struct CombineArgs {
@@ -71,20 +90,32 @@ struct DequantArgs {
   int out_bf16;
 };
 
-// LDS bytes the route kernel needs for a given token block.
-size_t route_lds_bytes(uint32_t tpb, uint32_t D, uint32_t E, uint32_t K, uint32_t threads);
+size_t router_lds_bytes(uint32_t tb, uint32_t Dpad);
+size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads);
 size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
-size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb);
+__host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
+  return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
+}
+// B staging plus the per-token row index and RmsNorm denominator.
+__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
+  return gemv_lds_bytes(nt, mt_max, nb) + 8u * (size_t)mt_max + 16u;
+}
+size_t small_route_kernel_lds(uint32_t T, uint32_t E, uint32_t K);
 
-constexpr uint32_t kRouteThreads = 512;
+constexpr uint32_t kRouterThreads = 256;
+constexpr uint32_t kTopkThreads = 512;
 constexpr uint32_t kDispatchThreads = 1024;
 constexpr uint32_t kGemvThreads = 256;
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
+constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
+constexpr uint32_t kSmallRouteThreads = 256;
 
-hipError_t launch_route(const RouteArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
+hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
+hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);
+hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
-hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, uint32_t grid_x, uint32_t grid_y, hipStream_t s);
+hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s);
 hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t configure_kernels();

@@ -80,10 +80,13 @@ struct burnext_moe_layer {
   TiledMx w1, w2;
   float *b1 = nullptr;  // [E, w1.rows_p], interleaved (gate, linear) order
   float *b2 = nullptr;  // [E, D]
-  void *router_w = nullptr;
+  void *router_w = nullptr;   // [E, D] as given (routing without RmsNorm)
   bool router_bf16 = false;
+  void *router_wg = nullptr;  // [E, D] gamma-folded rows (routing with RmsNorm); may alias router_w
+  bool router_wg_bf16 = false;
   float *router_b = nullptr;  // [E]
   float *gamma = nullptr;     // [D]
+  int num_cus = 256;
   std::mutex prof_mu;
   bool profiling = false;
   std::vector<ProfPair> prof;
@@ -181,8 +184,9 @@ burnext_status upload_vec(T **dst, const std::vector<T> &v) {
 void free_layer(burnext_moe_layer *L) {
   if (!L) return;
   DeviceGuard g(L->device);
+  if (L->router_wg == L->router_w) L->router_wg = nullptr;
   for (void *p : {(void *)L->w1.blocks, (void *)L->w1.scales, (void *)L->w2.blocks, (void *)L->w2.scales,
-                  (void *)L->b1, (void *)L->b2, L->router_w, (void *)L->router_b, (void *)L->gamma})
+                  (void *)L->b1, (void *)L->b2, L->router_w, L->router_wg, (void *)L->router_b, (void *)L->gamma})
     if (p) (void)hipFree(p);
   for (auto &pp : L->prof) {
     (void)hipEventDestroy(pp.a);
@@ -211,10 +215,8 @@ bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t
 
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t xn, logits, topk_idx, topk_w, meta, perm, pos_of, act, ypart, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, perm, pos_of, act, ypart, total;
 };
-
-constexpr uint32_t kMaxTerms = 3;
 
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   WsLayout w{};
@@ -225,7 +227,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     return o;
   };
   const uint64_t nk = n * L.K;
-  w.xn = take(n * kMaxTerms * L.Dp * 2);
+  w.rms = take(n * 4);
   w.logits = take(n * L.E * 4);
   w.topk_idx = take(nk * 4);
   w.topk_w = take(nk * 4);
@@ -239,7 +241,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
 }
 
 struct WsPtrs {
-  uint16_t *xn;
+  float *rms;
   float *logits;
   int32_t *topk_idx;
   float *topk_w;
@@ -250,7 +252,7 @@ struct WsPtrs {
 WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   uint8_t *b = (uint8_t *)base;
   WsPtrs p{};
-  p.xn = (uint16_t *)(b + w.xn);
+  p.rms = (float *)(b + w.rms);
   p.logits = (float *)(b + w.logits);
   p.topk_idx = (int32_t *)(b + w.topk_idx);
   p.topk_w = (float *)(b + w.topk_w);
@@ -266,10 +268,12 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
 
 constexpr size_t kLdsBudget = 160 * 1024;
 
-uint32_t route_tpb(const burnext_moe_layer &L) {
-  uint32_t tpb = 8;
-  while (tpb > 1 && route_lds_bytes(tpb, L.D, L.E, L.K, kRouteThreads) > kLdsBudget) tpb >>= 1;
-  return tpb;
+// Router token block: up to 8 tokens whose f32 rows (padded to 512) fit in LDS.
+uint32_t router_tb(const burnext_moe_layer &L) {
+  const uint32_t Dpad = (uint32_t)align_up(L.D, 512);
+  uint32_t tb = 8;
+  while (tb > 1 && router_lds_bytes(tb, Dpad) > kLdsBudget) tb >>= 1;
+  return tb;
 }
 
 // Records a HIP event pair around a launch when profiling is on.
@@ -294,59 +298,79 @@ struct ProfScope {
   }
 };
 
+enum KernelId { kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5 };
+
 burnext_status check_launch(hipError_t e, const char *what) {
   if (e != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
   return BURNEXT_OK;
 }
 
-// Routing (+ dispatch) into the workspace; shared by forward, route and dispatch entry points.
-burnext_status run_route(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, const WsPtrs &p,
-                         bool want_terms, bool want_dispatch, hipStream_t s) {
-  RouteArgs ra{};
+// Router logits (and r per token when normalising) into the workspace.
+burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
+                          float *logits, hipStream_t s) {
+  RouterArgs ra{};
   ra.x = x;
-  ra.rw = L->router_w;
+  ra.rw = norm ? L->router_wg : L->router_w;
+  const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
   ra.rb = L->router_b;
-  ra.gamma = L->gamma;
-  ra.xn_terms = want_terms ? p.xn : nullptr;
-  ra.logits = p.logits;
-  ra.topk_idx = p.topk_idx;
-  ra.topk_w = p.topk_w;
-  ra.seg_off = p.seg_off;
-  ra.perm = p.perm;
-  ra.pos_of = p.pos_of;
-  ra.active = p.active;
-  ra.num_active = p.num_active;
+  ra.logits = logits;
+  ra.rms = rms;
   ra.n = (uint32_t)n;
   ra.D = L->D;
-  ra.Dp = L->Dp;
+  ra.Dpad = (uint32_t)align_up(L->D, 512);
   ra.E = L->E;
-  ra.K = L->K;
-  ra.tpb = route_tpb(*L);
-  ra.nt = x_bf16 ? 1 : 3;
+  ra.tb = router_tb(*L);
+  ra.epw = n <= 64 ? 1 : 2;
   ra.eps = L->eps;
   ra.apply_norm = norm ? 1 : 0;
-  ra.fuse_dispatch = (want_dispatch && n <= ra.tpb) ? 1 : 0;
-  {
-    ProfScope ps(L, s, 0);
-    burnext_status st = check_launch(launch_route(ra, x_bf16, L->router_bf16, s), "route kernel launch");
-    if (st != BURNEXT_OK) return st;
-  }
-  if (want_dispatch && !ra.fuse_dispatch) {
-    DispatchArgs da{};
-    da.topk_idx = p.topk_idx;
-    da.seg_off = p.seg_off;
-    da.perm = p.perm;
-    da.pos_of = p.pos_of;
-    da.active = p.active;
-    da.num_active = p.num_active;
-    da.n = (uint32_t)n;
-    da.K = L->K;
-    da.E = L->E;
-    ProfScope ps(L, s, 1);
-    burnext_status st = check_launch(launch_dispatch(da, s), "dispatch kernel launch");
-    if (st != BURNEXT_OK) return st;
-  }
-  return BURNEXT_OK;
+  const bool vec = L->D % 8 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)ra.rw & 15u) == 0;
+  ProfScope ps(L, s, kKRouter);
+  return check_launch(launch_router(ra, x_bf16, w_bf16, vec, s), "router kernel launch");
+}
+
+burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, hipStream_t s) {
+  SmallRouteArgs a{};
+  a.logits = p.logits;
+  a.topk_idx = p.topk_idx;
+  a.topk_w = p.topk_w;
+  a.seg_off = p.seg_off;
+  a.perm = p.perm;
+  a.pos_of = p.pos_of;
+  a.active = p.active;
+  a.num_active = p.num_active;
+  a.n = (uint32_t)n;
+  a.E = L->E;
+  a.K = L->K;
+  ProfScope ps(L, s, kKTopk);
+  return check_launch(launch_small_route(a, s), "small-batch routing kernel launch");
+}
+
+burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, int32_t *idx, float *w, hipStream_t s) {
+  TopkArgs ta{};
+  ta.logits = logits;
+  ta.topk_idx = idx;
+  ta.topk_w = w;
+  ta.n = (uint32_t)n;
+  ta.E = L->E;
+  ta.K = L->K;
+  ProfScope ps(L, s, kKTopk);
+  return check_launch(launch_topk(ta, s), "top-k kernel launch");
+}
+
+burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
+                            int32_t *pos_of, int32_t *active, int32_t *num_active, hipStream_t s) {
+  DispatchArgs da{};
+  da.topk_idx = idx;
+  da.seg_off = seg_off;
+  da.perm = perm;
+  da.pos_of = pos_of;
+  da.active = active;
+  da.num_active = num_active;
+  da.n = (uint32_t)n;
+  da.K = L->K;
+  da.E = L->E;
+  ProfScope ps(L, s, kKDispatch);
+  return check_launch(launch_dispatch(da, s), "dispatch kernel launch");
 }
 
 burnext_status check_ws(burnext_moe_layer *L, uint64_t n, void *ws, uint64_t ws_bytes, WsLayout &w) {
@@ -451,6 +475,30 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
     else if (hipMemcpy(L->router_w, router_w, rbytes, hipMemcpyHostToDevice) != hipSuccess)
       st = fail(BURNEXT_DEVICE_ERROR, "hipMemcpy failed for router weight");
   }
+  if (st == BURNEXT_OK) {
+    // RmsNorm routing uses gamma-folded rows gw[e, c] = gamma[c] * w[e, c] (f32); with gamma all
+    // ones they equal the given rows, which are then shared.
+    bool ones = true;
+    for (uint32_t d = 0; d < D; ++d) ones = ones && hg[d] == 1.0f;
+    if (ones) {
+      L->router_wg = L->router_w;
+      L->router_wg_bf16 = L->router_bf16;
+    } else {
+      std::vector<float> gw((size_t)E * D);
+      for (uint32_t e = 0; e < E; ++e)
+        for (uint32_t d = 0; d < D; ++d)
+          gw[(size_t)e * D + d] = hg[d] * read_scalar(router_w, router_dtype, (size_t)e * D + d);
+      float *dgw = nullptr;
+      st = upload_vec(&dgw, gw);
+      L->router_wg = dgw;
+      L->router_wg_bf16 = false;
+    }
+  }
+  if (st == BURNEXT_OK) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+      L->num_cus = cus;
+  }
   if (st != BURNEXT_OK) {
     free_layer(L);
     return st;
@@ -490,11 +538,19 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_route(L, x, xb, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p, true, true, s);
+  const bool norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
+  st = run_router(L, x, xb, n, norm, p.rms, p.logits, s);
+  if (st != BURNEXT_OK) return st;
+  if (n <= kSmallRouteMaxTokens) {
+    st = run_small_route(L, n, p, s);
+  } else {
+    st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
+    if (st == BURNEXT_OK) st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, s);
+  }
   if (st != BURNEXT_OK) return st;
 
   const int nt = xb ? 1 : 3;
-  const uint32_t max_active = (uint32_t)std::min<uint64_t>(L->E, n * L->K);
+  const uint64_t max_active = std::min<uint64_t>(L->E, n * L->K);
   auto gemv = [&](bool gate_up) -> burnext_status {
     const TiledMx &t = gate_up ? L->w1 : L->w2;
     GemvArgs g{};
@@ -508,7 +564,6 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.nb = t.nb;
     g.kt = t.cols;
     g.out_rows = gate_up ? L->F : L->D;
-    g.tiles_per_wg = 8;
     const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
     uint32_t mt = (uint32_t)std::min<uint64_t>(16, n);
     mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
@@ -518,15 +573,25 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.num_active = p.num_active;
     g.perm = p.perm;
     g.topk = L->K;
-    g.bterms = p.xn;
-    g.bf32 = p.act;
+    g.x = x;
+    g.rms = p.rms;
+    g.gamma = L->gamma;
+    g.apply_norm = norm ? 1 : 0;
+    g.x_vec = (L->D % 8 == 0 && ((uintptr_t)x & 15u) == 0) ? 1 : 0;
+    g.act = p.act;
     g.out = gate_up ? p.act : p.ypart;
     g.out_stride = gate_up ? L->Fp : L->Dp;
     g.alpha = L->alpha;
     g.limit = L->limit;
-    const uint32_t gx = (uint32_t)cdiv(t.nrt, g.tiles_per_wg);
-    ProfScope ps(L, s, gate_up ? 2 : 3);
-    return check_launch(launch_gemv(g, nt, gate_up, gx, max_active, s), gate_up ? "gate_up launch" : "down launch");
+    // persistent grid: as many workgroups as stay resident at once (LDS-limited, at most 4 per CU)
+    // persistent grid: as many workgroups as stay resident at once (LDS-limited, at most 4 per
+    // CU), at least one per possible active expert (the kernel gives each active expert
+    // grid / num_active workgroups)
+    const size_t lds = gemv_total_lds_bytes(nt, mt, t.nb);
+    const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kLdsBudget / std::max<size_t>(lds, 1)));
+    const uint64_t grid = std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L->num_cus * per_cu, max_active * t.nrt));
+    ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
+    return check_launch(launch_gemv(g, nt, gate_up, xb, (uint32_t)grid, s), gate_up ? "gate_up launch" : "down launch");
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
@@ -548,7 +613,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   c.K = L->K;
   c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
   {
-    ProfScope ps(L, s, 4);
+    ProfScope ps(L, s, kKCombine);
     st = check_launch(launch_combine(c, xb, s), "combine launch");
   }
   return st == BURNEXT_OK ? ok() : st;
@@ -569,11 +634,10 @@ burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_d
   WsLayout w;
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
-  WsPtrs p = ws_ptrs(*L, w, workspace);
-  p.topk_idx = topk_idx;
-  p.topk_w = topk_w;
-  if (logits) p.logits = logits;
-  st = run_route(L, x, x_dtype == BURNEXT_BF16, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p, false, false, s);
+  const WsPtrs p = ws_ptrs(*L, w, workspace);
+  float *lg = logits ? logits : p.logits;
+  st = run_router(L, x, x_dtype == BURNEXT_BF16, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p.rms, lg, s);
+  if (st == BURNEXT_OK) st = run_topk(L, n, lg, topk_idx, topk_w, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 
@@ -589,17 +653,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  DispatchArgs da{};
-  da.topk_idx = topk_idx;
-  da.seg_off = seg_offsets;
-  da.perm = perm;
-  da.pos_of = p.pos_of;
-  da.active = p.active;
-  da.num_active = p.num_active;
-  da.n = (uint32_t)n;
-  da.K = L->K;
-  da.E = L->E;
-  st = check_launch(launch_dispatch(da, s), "dispatch kernel launch");
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 

@@ -10,7 +10,8 @@
  *   fp4 LUT / dequant ......... src/loader/mxfp4.rs:10-13, :56-79 (exact powi form)
  *   element addressing ........ src/quant/gpu.rs:124-131 (byte = blocks[row*bpr + c/2],
  *                               low nibble for even c; scale = scales[row*gpr + c/32])
- *   RMSNorm + router Linear ... src/moe/mod.rs:109-110 (Burn RmsNorm: x / sqrt(mean(x^2)+eps) * gamma)
+ *   RMSNorm + router Linear ... src/moe/mod.rs:109-110 (Burn RmsNorm: x / sqrt(mean(x^2)+eps) * gamma;
+ *                               routing applies 1/r after the dot product, see oracle_route_logits)
  *   top-k + softmax ........... src/moe/mod.rs:271-276 (softmax over the k selected logits)
  *   W1 + clamped SwiGLU ....... src/quant/gpu.rs:89-146, src/activation/mod.rs:5-45
  *   W2 + weighted accumulate .. src/quant/gpu.rs:148-192, src/moe/mod.rs:405-411
@@ -18,7 +19,8 @@
  *
  * Fixed reduction orders.  Routing (RMSNorm sum of squares and router logits) uses the
  * order the GPU route kernel uses, so indices and logits can be compared bit-exactly:
- *   lane partials  p[l] = fmaf(a[c], b[c], p[l]) for c = l, l+64, l+128, ... (l = 0..63)
+ *   lane partials  p[l] = fmaf(a[c], b[c], p[l]) over c = 512 i + 8 l + j, i ascending, then
+ *                  j = 0..7 ascending (lane l owns 8-element chunks; l = 0..63)
  *   butterfly      for off in 32,16,8,4,2,1:  p'[l] = p[l] + p[l ^ off]
  * IEEE addition is commutative, so every lane ends with the same value; lane 0 is used.
  *
@@ -26,8 +28,8 @@
  *   oracle_fp4_value / oracle_e8m0_scale / dequant: the reference KATs of
  *     tests/mxfp4_dequant_tests.rs:4-25, exhaustive 16 codes x 256 scale bytes against
  *     numpy.ldexp, and the e2m1 bit-field closed form.
- *   oracle_rmsnorm / oracle_router: float64 brute force (tolerance) and the butterfly
- *     order restated independently in numpy (bit-exact).
+ *   oracle_rmsnorm / oracle_router / oracle_route_logits: float64 brute force (tolerance) and
+ *     the lane order restated with exact rational arithmetic in Python (bit-exact).
  *   oracle_topk_softmax: brute-force stable sort by (value desc, index asc); ties and
  *     -inf special cases; sum of weights.
  *   oracle_dispatch: permutation / histogram / stability invariants.
@@ -92,12 +94,13 @@ void oracle_dequant_matrix(const uint8_t *blocks, const uint8_t *scales, int64_t
   }
 }
 
-/* One 64-lane strided dot product in the GPU route kernel's order (see header). */
+/* One 64-lane dot product in the GPU route kernel's order (see header). */
 static float lane_dot(const float *a, const float *b, int64_t n) {
   float p[64];
   for (int l = 0; l < 64; ++l) {
     float acc = 0.0f;
-    for (int64_t c = l; c < n; c += 64) acc = fmaf(a[c], b[c], acc);
+    for (int64_t c0 = 8 * l; c0 < n; c0 += 512)
+      for (int64_t c = c0; c < c0 + 8 && c < n; ++c) acc = fmaf(a[c], b[c], acc);
     p[l] = acc;
   }
   for (int off = 32; off >= 1; off >>= 1) {
@@ -132,6 +135,34 @@ void oracle_router(const float *xn, int64_t n, int64_t d, const float *w, const 
       const float s = lane_dot(xn + t * d, w + j * d, d);
       logits[t * e + j] = s + (b ? b[j] : 0.0f);
     }
+}
+
+/* Routing logits as the GPU router computes them.  With apply_rmsnorm the normalisation is
+ * applied after the dot product:
+ *   r_t = sqrt(lane_dot(x_t, x_t) / D + eps)          (Burn RmsNorm denominator)
+ *   logit[t,e] = lane_dot(x_t, gw_e) / r_t + b[e],    gw_e[c] = gamma[c] * W[e,c] (f32)
+ * which equals Linear(RmsNorm(x)) (src/moe/mod.rs:109-110) up to f32 rounding (Burn's own
+ * order is unpinned); gamma NULL means ones, and then gw_e = W[e] exactly.  Without
+ * apply_rmsnorm: logit[t,e] = lane_dot(x_t, W[e]) + b[e]. */
+void oracle_route_logits(const float *x, int64_t n, int64_t d, const float *gamma, float eps, int apply_rmsnorm,
+                         const float *w, const float *b, int64_t e, float *logits) {
+  float *gw = (float *)malloc(sizeof(float) * (size_t)(d > 0 ? d : 1));
+  for (int64_t j = 0; j < e; ++j) {
+    for (int64_t c = 0; c < d; ++c) gw[c] = (apply_rmsnorm && gamma) ? gamma[c] * w[j * d + c] : w[j * d + c];
+    for (int64_t t = 0; t < n; ++t) {
+      const float *xr = x + t * d;
+      const float u = lane_dot(xr, gw, d);
+      float lgt;
+      if (apply_rmsnorm) {
+        const float r = sqrtf(lane_dot(xr, xr, d) / (float)d + eps);
+        lgt = u / r;
+      } else {
+        lgt = u;
+      }
+      logits[t * e + j] = lgt + (b ? b[j] : 0.0f);
+    }
+  }
+  free(gw);
 }
 
 /* Strict total order used for selection: larger value first, NaN below everything,
@@ -276,7 +307,7 @@ int oracle_moe_forward(const float *x, int64_t n, const oracle_cfg *cfg, const u
     oracle_rmsnorm(x, n, D, gamma, cfg->eps, xn);
   else
     memcpy(xn, x, sizeof(float) * (size_t)(n * D));
-  oracle_router(xn, n, D, router_w, router_b, E, lg);
+  oracle_route_logits(x, n, D, gamma, cfg->eps, apply_rmsnorm, router_w, router_b, E, lg);
   oracle_topk_softmax(lg, n, E, K, idx, wt);
   for (int64_t e = 0; e < E; ++e) {
     int used = 0;
@@ -370,7 +401,7 @@ int oracle_moe_forward_reference(const float *x, int64_t n, const oracle_cfg *cf
   float *wt = (float *)malloc(sizeof(float) * (size_t)(n * K + 1));
   init_scale_table();
   oracle_rmsnorm(x, n, D, gamma, cfg->eps, xn);
-  oracle_router(xn, n, D, router_w, router_b, E, lg);
+  oracle_route_logits(x, n, D, gamma, cfg->eps, 1, router_w, router_b, E, lg);
   oracle_topk_softmax(lg, n, E, K, idx, wt);
   const int64_t tile_n = n < 256 ? (n < 1 ? 1 : n) : 256;
   const int64_t tile_f = F < 256 ? F : 256;

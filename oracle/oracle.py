@@ -45,6 +45,8 @@ def lib():
         L.oracle_dequant_matrix.argtypes = [_u8p, _u8p, _i64, _i64, _i64, _i64, ctypes.c_int, _f32p]
         L.oracle_rmsnorm.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_float, _f32p]
         L.oracle_router.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p]
+        L.oracle_route_logits.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_float, ctypes.c_int, _f32p, _f32p,
+                                          _i64, _f32p]
         L.oracle_topk_softmax.argtypes = [_f32p, _i64, _i64, _i64, _i32p, _f32p]
         L.oracle_dispatch.argtypes = [_i32p, _i64, _i64, _i64, _i32p, _i32p, _i32p]
         L.oracle_swiglu.restype = ctypes.c_float
@@ -113,6 +115,17 @@ def router(xn, w, b=None) -> np.ndarray:
     e = w.shape[0]
     out = np.empty((n, e), np.float32)
     lib().oracle_router(_p(xn, _f32p), n, d, _p(w, _f32p), _p(b, _f32p), e, _p(out, _f32p))
+    return out
+
+
+def route_logits(x, w, b=None, gamma=None, eps=1e-5, apply_rmsnorm=True) -> np.ndarray:
+    """Router logits in the GPU router's order (see oracle_route_logits)."""
+    x, w, b, g = _c(x, np.float32), _c(w, np.float32), _c(b, np.float32), _c(gamma, np.float32)
+    n, d = x.shape
+    e = w.shape[0]
+    out = np.empty((n, e), np.float32)
+    lib().oracle_route_logits(_p(x, _f32p), n, d, _p(g, _f32p), eps, int(apply_rmsnorm), _p(w, _f32p),
+                              _p(b, _f32p), e, _p(out, _f32p))
     return out
 
 

@@ -31,8 +31,7 @@ def main():
 
     L = synth.make_layer(256, 256, 2, 2, seed=0, dtype="f32")
     x = synth.make_tokens(16, 256, seed=0, dtype="f32")
-    xn = O.rmsnorm(x, None, L.rms_eps)
-    lg = O.router(xn, L.router_w_f32, L.router_b_f32)
+    lg = O.route_logits(x, L.router_w_f32, L.router_b_f32, None, L.rms_eps, True)
     idx, w = O.topk_softmax(lg, 2)
     y_int, _, _ = O.moe_forward(L, x, layout="interleaved")
     y_hal, _, _ = O.moe_forward(L, x, layout="halves")
@@ -43,8 +42,7 @@ def main():
 
     L2 = synth.make_layer(2880, 2880, 32, 4, seed=0, dtype="bf16")
     x2 = synth.make_tokens(8, 2880, seed=0, dtype="bf16")
-    xn2 = O.rmsnorm(x2, None, L2.rms_eps)
-    lg2 = O.router(xn2, L2.router_w_f32, L2.router_b_f32)
+    lg2 = O.route_logits(x2, L2.router_w_f32, L2.router_b_f32, None, L2.rms_eps, True)
     idx2, w2 = O.topk_softmax(lg2, 4)
     np.savez_compressed(HERE / "decode_c2_routing.npz", x_bf16_bits=synth.f32_to_bf16_bits(x2),
                         router_w_bf16_bits=L2.router_w_bits, logits=lg2, topk_idx=idx2, topk_w=w2)

@@ -106,8 +106,9 @@ def _exact_lane_dot(a, b):
     p = []
     for lane in range(64):
         acc = 0.0
-        for c in range(lane, len(a), 64):
-            acc = _exact_fma(float(a[c]), float(b[c]), acc)
+        for c0 in range(8 * lane, len(a), 512):
+            for c in range(c0, min(c0 + 8, len(a))):
+                acc = _exact_fma(float(a[c]), float(b[c]), acc)
         p.append(acc)
     for off in (32, 16, 8, 4, 2, 1):
         p = [_f32(p[i] + p[i ^ off]) for i in range(64)]
@@ -117,7 +118,7 @@ def _exact_lane_dot(a, b):
 
 def test_router_order_exact_rational(oracle):
     rng = np.random.default_rng(2)
-    D, E, n = 200, 5, 3
+    D, E, n = 1100, 5, 3  # two 512-element rounds plus a partial chunk
     x = rng.standard_normal((n, D)).astype(np.float32)
     w = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
     b = (rng.standard_normal(E) * 0.1).astype(np.float32)
@@ -126,6 +127,30 @@ def test_router_order_exact_rational(oracle):
         for e in range(E):
             assert lg[t, e] == _f32(_exact_lane_dot(x[t], w[e]) + float(b[e]))
     np.testing.assert_allclose(lg, x.astype(np.float64) @ w.T.astype(np.float64) + b, rtol=1e-5, atol=1e-6)
+
+
+def test_route_logits_exact_rational(oracle):
+    """Normalised routing: lane_dot(x, g*w) / sqrt(lane_dot(x, x)/D + eps) + b, exactly rounded."""
+    rng = np.random.default_rng(12)
+    D, E, n = 600, 3, 2
+    x = rng.standard_normal((n, D)).astype(np.float32)
+    w = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    g = rng.standard_normal(D).astype(np.float32)
+    lg = oracle.route_logits(x, w, b, g, 1e-5, True)
+    for t in range(n):
+        ss = np.float32(_exact_lane_dot(x[t], x[t]))
+        r = np.sqrt(np.float32(ss / np.float32(D)) + np.float32(1e-5), dtype=np.float32)
+        for e in range(E):
+            gw = (g * w[e]).astype(np.float32)
+            u = np.float32(_exact_lane_dot(x[t], gw))
+            assert lg[t, e] == np.float32(np.float32(u / r) + b[e])
+    # same values as Linear(RmsNorm(x)) up to f32 rounding
+    x64 = x.astype(np.float64)
+    ref = (x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-5) * g) @ w.T.astype(np.float64) + b
+    np.testing.assert_allclose(lg, ref, rtol=1e-4, atol=1e-6)
+    # without normalisation it is the plain Linear
+    assert np.array_equal(oracle.route_logits(x, w, b, g, 1e-5, False), oracle.router(x, w, b))
 
 
 def test_rmsnorm_exact_and_f64(oracle):
@@ -385,7 +410,7 @@ def test_golden_decode_routing_fixture(oracle):
     g = np.load(GOLDEN / "decode_c2_routing.npz")
     x = S.bf16_bits_to_f32(g["x_bf16_bits"])
     rw = S.bf16_bits_to_f32(g["router_w_bf16_bits"])
-    lg = oracle.router(oracle.rmsnorm(x, None, 1e-5), rw, np.zeros(32, np.float32))
+    lg = oracle.route_logits(x, rw, np.zeros(32, np.float32), None, 1e-5, True)
     assert np.array_equal(lg.view(np.uint32), g["logits"].view(np.uint32))
     idx, w = oracle.topk_softmax(lg, 4)
     assert np.array_equal(idx, g["topk_idx"]) and np.array_equal(w, g["topk_w"])
