@@ -114,18 +114,19 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     }
   }
 
-  // 2. stage tokens (contiguous [nh, D])
+  // 2. stage tokens (contiguous [nh, D]); one batch of SU chunk loads per thread in flight
   if (VEC) {
+    constexpr int SU = sizeof(XT) == 2 ? 12 : 6;
     const uint32_t nch = nh * D / 8u;
-    for (uint32_t base = threadIdx.x; base < nch; base += 4u * blockDim.x) {
-      Chunk8<XT> c[4];
+    for (uint32_t base = threadIdx.x; base < nch; base += SU * blockDim.x) {
+      Chunk8<XT> c[SU];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t ch = base + (uint32_t)u * blockDim.x;
-        if (ch < nch) chunk_load(c[u], x + (size_t)t0 * D + (size_t)ch * 8u);
+      for (int u = 0; u < SU; ++u) {
+        const uint32_t ch = min(base + (uint32_t)u * blockDim.x, nch - 1u);
+        chunk_load(c[u], x + (size_t)t0 * D + (size_t)ch * 8u);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < SU; ++u) {
         const uint32_t ch = base + (uint32_t)u * blockDim.x;
         if (ch >= nch) continue;
         const uint32_t f0 = ch * 8u, tt = f0 / D, c0 = f0 - tt * D;
@@ -243,8 +244,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 __device__ __forceinline__ void rank_select(const float *lr, uint32_t E, uint32_t K, uint32_t e, int32_t *sel,
                                             float *selv) {
   const float v = lr[e];
+  const uint64_t ke = topk_key(v, e);
   uint32_t rank = 0;
-  for (uint32_t e2 = 0; e2 < E; ++e2) rank += beats(lr[e2], (int)e2, v, (int)e) ? 1u : 0u;
+  for (uint32_t e2 = 0; e2 < E; ++e2) rank += topk_key(lr[e2], e2) > ke ? 1u : 0u;
   if (rank < K) {
     sel[rank] = (int32_t)e;
     selv[rank] = v;
@@ -295,11 +297,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 // ---------------------------------------------------------------------------------------------
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
                                int32_t *perm, int32_t *pos_of, int32_t *active, int32_t *num_active,
-                               int32_t *lds) {
+                               int32_t *exrec, const float *rms, int32_t *lds) {
   const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;
   int32_t *cnt = lds, *base = lds + E;
   uint32_t *bm = (uint32_t *)(lds + 2 * E);
   int32_t *wpre = lds + 2 * E + E * words;
+  int32_t *aidx = wpre + E * words;  // active slot of each expert
+  int32_t *segs = aidx + E;          // segment start of each expert
   for (uint32_t e = tid; e < E; e += nth) cnt[e] = 0;
   __syncthreads();
   for (uint32_t i = tid; i < n * K; i += nth) {
@@ -316,7 +320,14 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
     }
     seg_off[e] = off;
     base[e] = off;
-    if (cnt[e] > 0) active[ra] = (int32_t)e;
+    segs[e] = off;
+    aidx[e] = ra;
+    if (cnt[e] > 0) {
+      active[ra] = (int32_t)e;
+      exrec[ra * kRecWords + 0] = (int32_t)e;
+      exrec[ra * kRecWords + 1] = off;
+      exrec[ra * kRecWords + 2] = cnt[e];
+    }
     if (e + 1 == E) {
       seg_off[E] = off + cnt[e];
       const int32_t na = ra + (cnt[e] > 0);
@@ -352,6 +363,12 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
         const int32_t pos = base[e] + r;
         perm[pos] = (int32_t)(t * K + p);
         pos_of[t * K + p] = pos;
+        const int32_t j = pos - segs[e];  // entry index inside the expert's segment
+        if (j < (int32_t)kRecTokens) {
+          int32_t *rec = exrec + aidx[e] * kRecWords;
+          rec[4 + j] = (int32_t)(t * K + p);
+          rec[4 + kRecTokens + j] = __float_as_int(rms ? 1.0f / rms[t] : 1.0f);
+        }
       }
     }
     __syncthreads();
@@ -360,75 +377,143 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
   }
 }
 
-size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) { return sizeof(int32_t) * (size_t)E * (2 + 2 * (threads / 32)); }
+size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) { return sizeof(int32_t) * (size_t)E * (4 + 2 * (threads / 32)); }
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, (int32_t *)smem);
+  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec, a.rms,
+                 (int32_t *)smem);
 }
 
 // ---------------------------------------------------------------------------------------------
-// Routing of a decode-sized batch (T <= 16) by one workgroup, all in LDS, no serial loops over
-// tokens: top-k by rank, softmax, histogram by counting, exclusive scan by per-expert sums, and
-// segment positions pos(t, e) = seg_off[e] + #{t' < t : t' chose e}.  Same results as
-// topk_kernel + block_dispatch.
+// Routing of a decode-sized batch (T <= 16, E <= 256) by one workgroup of T waves.
+//  phase 1 (wave t = token t): lane l holds experts l + 64 j (j < J); the rank of each is the
+//    number of experts whose packed key (topk_key, the `beats` order) is larger, counted over
+//    readlane broadcasts; ranks < K are the selection; softmax over the selected logits
+//    (q ascending) by lanes p < K.
+//  phase 2 (wave 0): per-expert counts, exclusive scan and active list by a readlane loop, and
+//    segment positions in token order from per-lane running counters.
+// Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kSmallRouteThreads) void small_route_kernel(SmallRouteArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
+}
+
+template <int J>
+__global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
+  __shared__ int8_t rank_l[kSmallRouteMaxTokens][kMaxExperts];
+  __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
+  __shared__ int32_t invr_l[kSmallRouteMaxTokens];
   const uint32_t T = a.n, E = a.E, K = a.K;
-  const uint32_t tid = threadIdx.x, nth = blockDim.x;
-  float *lg = (float *)smem;
-  int32_t *sel = (int32_t *)(lg + T * E);
-  float *selv = (float *)(sel + T * K);
-  int32_t *cnt = (int32_t *)(selv + T * K);
-  int32_t *seg = cnt + E;
-  for (uint32_t i = tid; i < T * E; i += nth) lg[i] = a.logits[i];
-  __syncthreads();
-  for (uint32_t i = tid; i < T * E; i += nth) {
-    const uint32_t t = i / E, e = i - t * E;
-    rank_select(lg + t * E, E, K, e, sel + t * K, selv + t * K);
-  }
-  __syncthreads();
-  for (uint32_t i = tid; i < T * K; i += nth) {
-    const uint32_t t = i / K, p = i - t * K;
-    a.topk_idx[i] = sel[i];
-    a.topk_w[i] = softmax_weight(selv + t * K, K, p);
-  }
-  for (uint32_t e = tid; e < E; e += nth) {
-    int32_t c = 0;
-#pragma unroll 8
-    for (uint32_t i = 0; i < T * K; ++i) c += sel[i] == (int32_t)e;
-    cnt[e] = c;
-  }
-  __syncthreads();
-  for (uint32_t e = tid; e < E; e += nth) {
-    int32_t off = 0, ra = 0;
-#pragma unroll 8
-    for (uint32_t e2 = 0; e2 < e; ++e2) {
-      const int32_t c2 = cnt[e2];
-      off += c2;
-      ra += c2 > 0;
+  const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
+  if (t < T && lane == 0) invr_l[t] = __float_as_int(a.rms ? 1.0f / a.rms[t] : 1.0f);
+  if (t < T) {
+    float v[J];
+    uint64_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t e = lane + 64u * j;
+      v[j] = e < E ? a.logits[(size_t)t * E + e] : 0.0f;
+      key[j] = topk_key(v[j], e);
     }
-    seg[e] = off;
-    a.seg_off[e] = off;
-    if (cnt[e] > 0) a.active[ra] = (int32_t)e;
-    if (e + 1 == E) {
-      const int32_t na = ra + (cnt[e] > 0);
-      a.seg_off[E] = off + cnt[e];
-      *a.num_active = na;
-      for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) a.active[e3] = -1;
+    uint32_t rank[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) rank[j] = 0u;
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj) {
+      const uint32_t kn = min(64u, E - 64u * jj);
+      const uint32_t khi = (uint32_t)(key[jj] >> 32), klo = (uint32_t)key[jj];
+      for (uint32_t kk = 0; kk < kn; ++kk) {
+        const uint64_t kb = ((uint64_t)readlane_u(khi, kk) << 32) | readlane_u(klo, kk);
+#pragma unroll
+        for (int j = 0; j < J; ++j) rank[j] += kb > key[j] ? 1u : 0u;
+      }
     }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t e = lane + 64u * j;
+      if (e >= E) continue;
+      const bool s = rank[j] < K;
+      rank_l[t][e] = s ? (int8_t)rank[j] : (int8_t)-1;
+      if (s) {
+        selv_l[t][rank[j]] = v[j];
+        a.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t p = lane; p < K; p += 64u) a.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
   __syncthreads();
-  for (uint32_t i = tid; i < T * K; i += nth) {
-    const uint32_t t = i / K;
-    const int32_t e = sel[i];
-    int32_t rk = 0;
-#pragma unroll 8
-    for (uint32_t i2 = 0; i2 < t * K; ++i2) rk += sel[i2] == e;
-    const int32_t pos = seg[e] + rk;
-    a.perm[pos] = (int32_t)i;
-    a.pos_of[i] = pos;
+  if (t != 0) return;
+  int cnt[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    int c = 0;
+    for (uint32_t t2 = 0; t2 < T; ++t2) c += (e < E && rank_l[t2][e] >= 0) ? 1 : 0;
+    cnt[j] = c;
+  }
+  int off[J], ra[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) off[j] = ra[j] = 0;
+  int total = 0, nact = 0;
+#pragma unroll
+  for (int jj = 0; jj < J; ++jj) {
+    const uint32_t kn = min(64u, E - 64u * jj);
+    for (uint32_t kk = 0; kk < kn; ++kk) {
+      const int c = (int)readlane_u((uint32_t)cnt[jj], kk);
+      const uint32_t ek = 64u * jj + kk;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const bool before = ek < lane + 64u * j;
+        off[j] += before ? c : 0;
+        ra[j] += (before && c > 0) ? 1 : 0;
+      }
+      total += c;
+      nact += c > 0 ? 1 : 0;
+    }
+  }
+  // seg_off, active[0..nact) from the experts with tokens, active[nact..E) = -1 (disjoint writes)
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    if (e >= E) continue;
+    a.seg_off[e] = off[j];
+    if (cnt[j] > 0) {
+      a.active[ra[j]] = (int32_t)e;
+      int32_t *rec = a.exrec + ra[j] * kRecWords;
+      rec[0] = (int32_t)e;
+      rec[1] = off[j];
+      rec[2] = cnt[j];
+    }
+    if ((int)e >= nact) a.active[e] = -1;
+  }
+  if (lane == 0) {
+    a.seg_off[E] = total;
+    *a.num_active = nact;
+  }
+  int seen[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) seen[j] = 0;
+  for (uint32_t t2 = 0; t2 < T; ++t2) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t e = lane + 64u * j;
+      if (e >= E) continue;
+      const int r = rank_l[t2][e];
+      if (r >= 0) {
+        const int pos = off[j] + seen[j];
+        a.perm[pos] = (int32_t)(t2 * K + (uint32_t)r);
+        a.pos_of[t2 * K + (uint32_t)r] = pos;
+        if (seen[j] < (int)kRecTokens) {
+          int32_t *rec = a.exrec + ra[j] * kRecWords;
+          rec[4 + seen[j]] = (int32_t)(t2 * K + (uint32_t)r);
+          rec[4 + kRecTokens + seen[j]] = invr_l[t2];
+        }
+        seen[j] += 1;
+      }
+    }
   }
 }
 
@@ -455,7 +540,8 @@ __device__ __forceinline__ float swiglu_clamp(float g, float l, float alpha, flo
 
 // Grid of G workgroups (as many as stay resident).  Each active expert gets wpe = G / num_active
 // workgroups, each owning a contiguous range of that expert's row tiles, so every workgroup
-// stages one expert's B operand once.  The B operand (xn = x * (1/r) * gamma split into NT bf16
+// stages one expert's B operand once.  A workgroup learns num_active, its expert, segment and
+// first tokens from one round trip (num_active plus the record table).  The B operand (xn = x * (1/r) * gamma split into NT bf16
 // terms, or the f32 act rows of the down projection) is staged into LDS with every global load of
 // a batch issued before any is consumed; the first weight chunk is requested before staging.
 // Each wave then streams its tiles with the next chunk's loads -- also across tile boundaries --
@@ -466,18 +552,28 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
   const uint32_t mtm = a.mt_max;
   uint16_t *bs = (uint16_t *)smem;
-  int32_t *tok_l = (int32_t *)(smem + gemv_lds_bytes(NT, mtm, a.nb));  // [mtm]
-  float *r_l = (float *)(tok_l + mtm);                                    // [mtm]
+  int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec));  // [kRecWords]
+  int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
+  float *r_l = (float *)(tok_l + mtm);                                            // [mtm]
   const uint32_t nrt = a.nrt;
+  // one round trip: num_active and the record table (staged through the B area)
+  {
+    const uint4 *src = (const uint4 *)a.exrec;
+    uint4 *dst = (uint4 *)smem;
+    const uint32_t nv = a.nrec * (kRecWords / 4u);
+    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
+  }
   const uint32_t na = (uint32_t)*a.num_active;
-  if (na == 0) return;
-  const uint32_t wpe = max(1u, gridDim.x / na);
+  __syncthreads();
+  if (na == 0u) return;
+  const uint32_t wpe = max(1u, min(gridDim.x / na, nrt));
   const uint32_t ai = blockIdx.x / wpe, part = blockIdx.x % wpe;
   if (ai >= na) return;
-  const uint32_t tpw = (nrt + wpe - 1) / wpe;  // tiles per workgroup
-  const uint32_t rt_lo = part * tpw;
-  const uint32_t rt_hi = min(nrt, rt_lo + tpw);
-  if (rt_lo >= rt_hi) return;
+  if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = ((const int32_t *)smem)[ai * kRecWords + threadIdx.x];
+  // even split of the expert's row tiles over its wpe workgroups (wpe <= nrt: none is empty)
+  const uint32_t rt_lo = (uint32_t)(((uint64_t)part * nrt) / wpe);
+  const uint32_t rt_hi = (uint32_t)(((uint64_t)(part + 1u) * nrt) / wpe);
+  __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
@@ -501,9 +597,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   };
 
   {
-    const int e = a.active[ai];
-    const int seg0 = a.seg_off[e];
-    const int M = a.seg_off[e + 1] - seg0;
+    const int e = rec_l[0];
+    const int seg0 = rec_l[1];
+    const int M = rec_l[2];
     const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
     const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
     // this wave's tiles: rt_lo + wv, rt_lo + wv + 4, ...
@@ -518,10 +614,23 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       if (my_tiles > 0)
         load_chunk(wexp + (size_t)my_first * a.nb * 256u, sexp + (size_t)my_first * a.nb * 16u, 0u, acur, scur);
       __syncthreads();
-      if (GATE_UP && threadIdx.x < mt) {
-        const int32_t tk = a.perm[seg0 + m0 + (int)threadIdx.x] / (int32_t)a.topk;
-        tok_l[threadIdx.x] = tk;
-        r_l[threadIdx.x] = a.apply_norm ? 1.0f / a.rms[tk] : 1.0f;  // within 1 ulp of dividing by r
+      if (threadIdx.x < mt) {
+        // token, 1/r (within 1 ulp of dividing by r) and slot t * topk + p of segment entry jj:
+        // from the record for the first kRecTokens entries, else from the global segment list
+        const uint32_t jj = (uint32_t)m0 + threadIdx.x;
+        int32_t slot, tk;
+        float ir;
+        if (jj < kRecTokens) {
+          slot = rec_l[4 + jj];
+          tk = slot / (int32_t)a.topk;
+          ir = __int_as_float(rec_l[4 + kRecTokens + jj]);
+        } else {
+          slot = a.perm[seg0 + (int)jj];
+          tk = slot / (int32_t)a.topk;
+          ir = a.apply_norm ? 1.0f / a.rms[tk] : 1.0f;
+        }
+        tok_l[threadIdx.x] = GATE_UP ? tk : slot;
+        r_l[threadIdx.x] = ir;
       }
       __syncthreads();
       // stage B: mt tokens x Kp, NT bf16 terms, zero beyond the true K; batches of SB items with
@@ -662,12 +771,14 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
                 o[0] = o0;
               }
             } else {
-              float *o = a.out + (size_t)pos * a.out_stride + r0;
+              // token-major slot row t * topk + p, expert bias b2 added once
+              const float *bb = a.bias + (size_t)e * a.bias_estride + r0;
+              float *o = a.out + (size_t)tok_l[i16] * a.out_stride + r0;
               if (r0 + 3u < a.out_rows) {
-                *(float4 *)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                *(float4 *)o = make_float4(acc[0] + bb[0], acc[1] + bb[1], acc[2] + bb[2], acc[3] + bb[3]);
               } else {
                 for (uint32_t r = 0; r < 4u; ++r)
-                  if (r0 + r < a.out_rows) o[r] = acc[r];
+                  if (r0 + r < a.out_rows) o[r] = acc[r] + bb[r];
               }
             }
           }
@@ -683,8 +794,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Combine: y[t, d] = (add_residual ? x[t, d] : 0) + sum_{p asc} (ypart[pos(t,p), d] + b2[e_p, d]) * w_p
-// Four outputs per thread; the token's routing loads are issued together.
+// Combine: y[t, d] = (add_residual ? x[t, d] : 0) + sum_{p asc} yslot[t*K + p, d] * w_p, where the
+// down projection already wrote yslot = down_p + b2[e_p] token-major.  Every load of a thread is
+// independent of the others (one memory round trip); four outputs per thread.
 // ---------------------------------------------------------------------------------------------
 template <typename XT>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
@@ -692,50 +804,31 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4u;
   if (d0 >= a.D) return;
   const uint32_t nv = min(4u, a.D - d0);
-  const bool vec4 = (a.D % 4u) == 0u;
+  const XT *x = (const XT *)a.x;
+  float xv[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4u; ++j) xv[j] = (a.add_residual && j < nv) ? load_val(x, (size_t)t * a.D + d0 + j) : 0.0f;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (uint32_t p0 = 0; p0 < a.K; p0 += 8u) {
-    int32_t ev[8], pv[8];
     float wv[8];
+    float4 yv[8];
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
-      const uint32_t p = p0 + u;
-      const bool in = p < a.K;
-      ev[u] = in ? a.topk_idx[(size_t)t * a.K + p] : -1;
-      wv[u] = in ? a.topk_w[(size_t)t * a.K + p] : 0.0f;
-      pv[u] = in ? a.pos_of[(size_t)t * a.K + p] : 0;
-    }
-    float4 yv[8], bv[8];
-#pragma unroll
-    for (uint32_t u = 0; u < 8u; ++u) {
-      const bool ok = ev[u] >= 0 && (uint32_t)ev[u] < a.E;
-      const float *yp = a.ypart + (size_t)pv[u] * a.Dp + d0;
-      const float *bp = a.b2 + (size_t)(ok ? ev[u] : 0) * a.D + d0;
-      if (ok && vec4) {
-        yv[u] = *(const float4 *)yp;
-        bv[u] = *(const float4 *)bp;
-      } else if (ok) {
-        yv[u] = make_float4(yp[0], nv > 1 ? yp[1] : 0.f, nv > 2 ? yp[2] : 0.f, nv > 3 ? yp[3] : 0.f);
-        bv[u] = make_float4(bp[0], nv > 1 ? bp[1] : 0.f, nv > 2 ? bp[2] : 0.f, nv > 3 ? bp[3] : 0.f);
-      } else {
-        yv[u] = bv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      const uint32_t p = min(p0 + u, a.K - 1u);
+      wv[u] = a.topk_w[(size_t)t * a.K + p];
+      yv[u] = *(const float4 *)(a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 4 == 0, d0 < Dp
     }
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
-      if (!(ev[u] >= 0 && (uint32_t)ev[u] < a.E)) continue;
-      acc[0] = acc[0] + (yv[u].x + bv[u].x) * wv[u];
-      acc[1] = acc[1] + (yv[u].y + bv[u].y) * wv[u];
-      acc[2] = acc[2] + (yv[u].z + bv[u].z) * wv[u];
-      acc[3] = acc[3] + (yv[u].w + bv[u].w) * wv[u];
+      if (p0 + u >= a.K) break;
+      acc[0] = acc[0] + yv[u].x * wv[u];
+      acc[1] = acc[1] + yv[u].y * wv[u];
+      acc[2] = acc[2] + yv[u].z * wv[u];
+      acc[3] = acc[3] + yv[u].w * wv[u];
     }
   }
-  const XT *x = (const XT *)a.x;
   XT *y = (XT *)a.y;
-  for (uint32_t j = 0; j < nv; ++j) {
-    const size_t i = (size_t)t * a.D + d0 + j;
-    store_val(y, i, (a.add_residual ? load_val(x, i) : 0.0f) + acc[j]);
-  }
+  for (uint32_t j = 0; j < nv; ++j) store_val(y, (size_t)t * a.D + d0 + j, xv[j] + acc[j]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -784,7 +877,6 @@ hipError_t configure_kernels() {
   BX_ATTR((router_kernel<float, uint16_t, false>));
   BX_ATTR((router_kernel<uint16_t, float, false>));
   BX_ATTR((router_kernel<uint16_t, uint16_t, false>));
-  BX_ATTR(small_route_kernel);
   BX_ATTR(topk_kernel);
   BX_ATTR(dispatch_kernel);
   BX_ATTR((expert_gemv_kernel<1, true, uint16_t>));
@@ -822,12 +914,15 @@ hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec
   return hipGetLastError();
 }
 
-size_t small_route_kernel_lds(uint32_t T, uint32_t E, uint32_t K) {
-  return sizeof(int32_t) * ((size_t)T * E + 2 * (size_t)T * K + 2 * (size_t)E);
-}
-
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
-  small_route_kernel<<<dim3(1), dim3(kSmallRouteThreads), small_route_kernel_lds(a.n, a.E, a.K), s>>>(a);
+  if (a.n == 0 || a.n > kSmallRouteMaxTokens || a.E > kMaxExperts || a.K > kMaxTopK) return hipErrorInvalidValue;
+  const dim3 block(64 * a.n);
+  if (a.E <= 64)
+    small_route_kernel<1><<<dim3(1), block, 0, s>>>(a);
+  else if (a.E <= 128)
+    small_route_kernel<2><<<dim3(1), block, 0, s>>>(a);
+  else
+    small_route_kernel<4><<<dim3(1), block, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -844,7 +939,7 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
 
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
   const dim3 g(grid), block(kGemvThreads);
-  const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb);
+  const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
   if (nt == 1) {
     if (!gate_up)
       expert_gemv_kernel<1, false, float><<<g, block, lds, s>>>(a);

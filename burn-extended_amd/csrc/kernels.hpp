@@ -27,9 +27,19 @@ struct TopkArgs {
   uint32_t n, E, K;
 };
 
+// Per-active-expert record written by the routing kernels: [0] expert, [1] segment offset,
+// [2] segment size M, [3] unused, [4 + j] slot t*K + p of the j-th segment entry and
+// [4 + kRecTokens + j] its 1/r (f32 bits, 1.0 without RmsNorm), for j < min(M, kRecTokens).
+// The expert GEMVs load the records of every possible active slot together with num_active in
+// one round trip and map themselves onto the active experts from that.
+constexpr uint32_t kRecWords = 32;
+constexpr uint32_t kRecTokens = 14;
+
 struct DispatchArgs {
   const int32_t *topk_idx;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;     // [E, kRecWords]
+  const float *rms;   // [n] or null (no RmsNorm)
   uint32_t n, K, E;
 };
 
@@ -39,7 +49,7 @@ struct GemvArgs {
   const uint8_t *wb;      // tiled e2m1 blocks, expert stride wb_estride bytes
   const uint8_t *ws;      // tiled e8m0 scales, expert stride ws_estride bytes
   uint64_t wb_estride, ws_estride;
-  const float *bias;      // gate_up: b1 [E, rows_p] (interleaved order); unused for down
+  const float *bias;      // gate_up: b1 [E, rows_p] (interleaved order); down: b2 [E, D]
   uint32_t bias_estride;
   uint32_t nrt;           // 16-row tiles per expert
   uint32_t nb;            // 32-wide K blocks (K padded = 32 * nb)
@@ -47,6 +57,8 @@ struct GemvArgs {
   uint32_t out_rows;      // gate_up: F output features; down: D
   uint32_t mt_max;        // tokens staged per pass (<= 16)
   const int32_t *seg_off, *active, *num_active, *perm;
+  const int32_t *exrec;   // [E, kRecWords] per-active-expert records
+  uint32_t nrec;          // records loaded: min(E, n * topk), every slot that can be active
   uint32_t topk;
   // gate_up B operand: xn = apply_norm ? (x / rms[t]) * gamma : x, from x [n, kt] (x dtype)
   const void *x;
@@ -55,7 +67,7 @@ struct GemvArgs {
   int x_vec;              // x rows 16-byte aligned (base aligned, kt % 8 == 0): 128-bit loads
   // down B operand: act [n*k, Kp] f32
   const float *act;
-  float *out;             // gate_up: act [n*k, Fp]; down: ypart [n*k, Dp]
+  float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
 };
@@ -64,21 +76,20 @@ struct GemvArgs {
 // dispatch, all outputs to global.
 struct SmallRouteArgs {
   const float *logits;
+  const float *rms;  // [n] or null (no RmsNorm)
   int32_t *topk_idx;
   float *topk_w;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;    // [E, kRecWords]
   uint32_t n, E, K;
 };
 
 struct CombineArgs {
   const void *x;
   void *y;
-  const float *ypart;
-  const float *b2;
-  const int32_t *topk_idx;
+  const float *ypart;  // token-major slot rows [n*K, Dp], expert bias included
   const float *topk_w;
-  const int32_t *pos_of;
-  uint32_t n, D, Dp, E, K;
+  uint32_t n, D, Dp, K;
   int add_residual;
 };
 
@@ -96,11 +107,15 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
 }
-// B staging plus the per-token row index and RmsNorm denominator.
-__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
-  return gemv_lds_bytes(nt, mt_max, nb) + 8u * (size_t)mt_max + 16u;
+// B staging (which first holds the record table), the chosen record, the per-token row index
+// and RmsNorm denominator.
+__host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = 4u * (size_t)nrec * 32u;
+  return b > t ? b : t;
 }
-size_t small_route_kernel_lds(uint32_t T, uint32_t E, uint32_t K);
+__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 8u * (size_t)mt_max + 16u;
+}
 
 constexpr uint32_t kRouterThreads = 256;
 constexpr uint32_t kTopkThreads = 512;
@@ -109,7 +124,6 @@ constexpr uint32_t kGemvThreads = 256;
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
-constexpr uint32_t kSmallRouteThreads = 256;
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);

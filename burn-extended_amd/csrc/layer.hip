@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -215,7 +216,7 @@ bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t
 
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t rms, logits, topk_idx, topk_w, meta, perm, pos_of, act, ypart, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, act, ypart, total;
 };
 
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
@@ -232,6 +233,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   w.topk_idx = take(nk * 4);
   w.topk_w = take(nk * 4);
   w.meta = take((2ull * L.E + 2) * 4);
+  w.exrec = take((uint64_t)L.E * kRecWords * 4);
   w.perm = take(nk * 4);
   w.pos_of = take(nk * 4);
   w.act = take(nk * L.Fp * 4);
@@ -246,6 +248,7 @@ struct WsPtrs {
   int32_t *topk_idx;
   float *topk_w;
   int32_t *seg_off, *active, *num_active, *perm, *pos_of;
+  int32_t *exrec;
   float *act, *ypart;
 };
 
@@ -259,6 +262,7 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.seg_off = (int32_t *)(b + w.meta);
   p.active = p.seg_off + L.E + 1;
   p.num_active = p.active + L.E;
+  p.exrec = (int32_t *)(b + w.exrec);
   p.perm = (int32_t *)(b + w.perm);
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
@@ -328,9 +332,12 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
   return check_launch(launch_router(ra, x_bf16, w_bf16, vec, s), "router kernel launch");
 }
 
-burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, hipStream_t s) {
+// rms: per-token r when RmsNorm is applied (the records then carry 1/r), else null.
+burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *rms, hipStream_t s) {
   SmallRouteArgs a{};
   a.logits = p.logits;
+  a.rms = rms;
+  a.exrec = p.exrec;
   a.topk_idx = p.topk_idx;
   a.topk_w = p.topk_w;
   a.seg_off = p.seg_off;
@@ -358,8 +365,11 @@ burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, i
 }
 
 burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
-                            int32_t *pos_of, int32_t *active, int32_t *num_active, hipStream_t s) {
+                            int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec,
+                            const float *rms, hipStream_t s) {
   DispatchArgs da{};
+  da.exrec = exrec;
+  da.rms = rms;
   da.topk_idx = idx;
   da.seg_off = seg_off;
   da.perm = perm;
@@ -542,10 +552,12 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   st = run_router(L, x, xb, n, norm, p.rms, p.logits, s);
   if (st != BURNEXT_OK) return st;
   if (n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, s);
+    st = run_small_route(L, n, p, norm ? p.rms : nullptr, s);
   } else {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
-    if (st == BURNEXT_OK) st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, s);
+    if (st == BURNEXT_OK)
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec,
+                        norm ? p.rms : nullptr, s);
   }
   if (st != BURNEXT_OK) return st;
 
@@ -558,8 +570,8 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.ws = t.scales;
     g.wb_estride = t.blocks_per_expert;
     g.ws_estride = t.scales_per_expert;
-    g.bias = L->b1;
-    g.bias_estride = L->w1.rows_p;
+    g.bias = gate_up ? L->b1 : L->b2;
+    g.bias_estride = gate_up ? L->w1.rows_p : L->D;
     g.nrt = t.nrt;
     g.nb = t.nb;
     g.kt = t.cols;
@@ -572,6 +584,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.active = p.active;
     g.num_active = p.num_active;
     g.perm = p.perm;
+    g.exrec = p.exrec;
     g.topk = L->K;
     g.x = x;
     g.rms = p.rms;
@@ -583,11 +596,11 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.out_stride = gate_up ? L->Fp : L->Dp;
     g.alpha = L->alpha;
     g.limit = L->limit;
-    // persistent grid: as many workgroups as stay resident at once (LDS-limited, at most 4 per CU)
     // persistent grid: as many workgroups as stay resident at once (LDS-limited, at most 4 per
     // CU), at least one per possible active expert (the kernel gives each active expert
     // grid / num_active workgroups)
-    const size_t lds = gemv_total_lds_bytes(nt, mt, t.nb);
+    g.nrec = (uint32_t)max_active;
+    const size_t lds = gemv_total_lds_bytes(nt, mt, t.nb, g.nrec);
     const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kLdsBudget / std::max<size_t>(lds, 1)));
     const uint64_t grid = std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L->num_cus * per_cu, max_active * t.nrt));
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
@@ -602,14 +615,10 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   c.x = x;
   c.y = y;
   c.ypart = p.ypart;
-  c.b2 = L->b2;
-  c.topk_idx = p.topk_idx;
   c.topk_w = p.topk_w;
-  c.pos_of = p.pos_of;
   c.n = (uint32_t)n;
   c.D = L->D;
   c.Dp = L->Dp;
-  c.E = L->E;
   c.K = L->K;
   c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
   {
@@ -653,7 +662,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, s);
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, nullptr, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 

@@ -53,6 +53,21 @@ __device__ __forceinline__ float wave_sum_butterfly(float p) {
   return p;
 }
 
+// Packed top-k key with the same strict total order as `beats`: a beats b iff key(a) > key(b)
+// (unsigned).  High word: order-preserving map of the float with NaN -> 0 (lowest) and -0 -> +0;
+// low word: ~index, so equal values rank the lower index first.
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
+  const uint32_t u = __float_as_uint(v);
+  uint32_t k;
+  if (v != v)
+    k = 0u;
+  else if (v == 0.0f)
+    k = 0x80000000u;
+  else
+    k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+
 // Strict total order for top-k: larger value first, NaN lowest, ties to the lower index.
 __device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
   const bool na = va != va, nb = vb != vb;
