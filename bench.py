@@ -45,11 +45,30 @@ def parse():
     ap.add_argument("--copies", type=int, default=4, help="device copies of the layer rotated per step")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     return ap.parse_args()
+
+
+def copy_probe(mib):
+    """A plain device-to-device copy of known size: under `rocprofv3 --pmc FETCH_SIZE` /
+    `WRITE_SIZE` its per-dispatch counter values give the factor that turns those counters into
+    HBM bytes on this GPU."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}), flush=True)
 
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (one MI355X per run); "
               "run with --gpus 1", file=sys.stderr)
@@ -121,17 +140,18 @@ def main():
     kflops = {"gate_up": 2 * nk * 2 * F * D, "down": 2 * nk * D * F}
     layer_bytes = synth.decode_bytes(data, touched, T, 2)
     dominant = max(kavg_us, key=kavg_us.get)
+    traffic = measured_traffic(args.workload, dominant)
     if T >= 1024:
         fl = kflops.get(dominant, 0)
         ach = fl / (kavg_us[dominant] * 1e-6) / 1e12
         roof = {"bound": "mfma", "kernel": dominant, "achieved": round(ach, 2), "peak": FP4_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / FP4_PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(ach / FP4_PEAK_TFLOPS, 4), "traffic": traffic,
                 "algorithmic_flops_per_launch": fl, "avg_launch_us": round(kavg_us[dominant], 2)}
     else:
         b = kbytes.get(dominant, 0)
         ach = b / (kavg_us[dominant] * 1e-6) / 1e9
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes_per_launch": b,
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes_per_launch": b,
                 "avg_launch_us": round(kavg_us[dominant], 2)}
 
     out = {
@@ -168,6 +188,21 @@ def main():
     for L in layers:
         L.close()
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (profiles/hbm_traffic_<workload>.txt: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a plain
+    copy's counter readings); None when no summary covers it."""
+    path = ROOT / "profiles" / f"hbm_traffic_{workload}.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if len(f) >= 3 and f[0] == "traffic" and f[1] == workload and f[2] == kernel:
+            kv = dict(x.split("=", 1) for x in f[3:] if "=" in x)
+            return int(float(kv["bytes"])) if "bytes" in kv else None
+    return None
 
 
 def cpu_baseline(data, x_np, budget_s):
