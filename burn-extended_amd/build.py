@@ -15,8 +15,10 @@ SOURCES = ["kernels.hip", "layer.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops off: hipcc forms packed fp32 ops from plain float code on its own; they are
 # kept out of every kernel here.  The host pass warns that it does not know the feature.
+# atomic optimizer off: it turns the expert GEMV's single-lane ticket atomic into a wave-reduced
+# one whose result is consumed at once, i.e. a full vmcnt(0) drain of the weight prefetch.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-Wall", "-Wno-unused-result"]
+         "-packed-fp32-ops", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None", "-Wall", "-Wno-unused-result"]
 
 
 def build(verbose: bool = False) -> pathlib.Path:

@@ -6,6 +6,8 @@
 //                   replaces src/moe/mod.rs:271-276 (topk_with_indices, max/exp/sum/div)
 // dispatch_kernel   histogram / exclusive scan / stable scatter into expert segments
 //                   replaces the per-expert dense masks of src/moe/mod.rs:279-288
+// router_small      decode-sized router (n <= 16): one wave per (expert, token pair), also
+//                   writes the normalised token rows for the expert GEMV
 // small_route       top-k/softmax/dispatch of a decode-sized batch by one workgroup
 // expert_gemv       MXFP4 x bf16 projection on MFMA 16x16x32 bf16, e2m1+e8m0 dequantised in
 //                   registers; gate_up staging applies the RmsNorm and the epilogue fuses bias +
@@ -23,6 +25,18 @@ __device__ __forceinline__ float load_val(const float *p, size_t i) { return p[i
 __device__ __forceinline__ float load_val(const uint16_t *p, size_t i) { return bf16_bits_to_f32(p[i]); }
 __device__ __forceinline__ void store_val(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void store_val(uint16_t *p, size_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+
+__device__ __forceinline__ void store8(uint16_t *p, const float (&v)[8]) {
+  uint32_t w4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w4[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+  *(uint4 *)p = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+}
+__device__ __forceinline__ void store8(float *p, const float (&v)[8]) {
+  *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4 *)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
 
 // ---------------------------------------------------------------------------------------------
 // 8-element chunks: raw register form between load and use, and guarded scalar loads.
@@ -219,6 +233,28 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     if (has1) wave_sum_butterfly_n<8>(acc1);
   }
   __syncthreads();  // rr visible
+  if (blockIdx.y == 0 && a.xn) {
+    // normalised rows for the expert GEMV: xn = x * (1/r) * gamma (x without RmsNorm) in the
+    // x dtype, zero padded to Dp
+    XT *xn = (XT *)a.xn;
+    const uint32_t cpr = a.Dp / 8u;  // Dp is a multiple of 32
+    for (uint32_t ch = threadIdx.x; ch < nh * cpr; ch += blockDim.x) {
+      const uint32_t tt = ch / cpr, c0 = (ch - tt * cpr) * 8u;
+      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
+      float v[8];
+#pragma unroll
+      for (uint32_t j = 0; j < 8u; ++j) {
+        const uint32_t c = c0 + j;
+        float u = 0.0f;
+        if (c < D) {
+          u = xs[(size_t)tt * Dpad + tpos(c)];
+          if (a.apply_norm) u = (u * ir) * a.gamma[c];
+        }
+        v[j] = u;
+      }
+      store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
+    }
+  }
   if (has0 && lane < nh) {
     // lane tt writes token tt's logits (all lanes hold the reduced values)
     float v0 = 0.0f, v1 = 0.0f;
@@ -297,7 +333,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 // ---------------------------------------------------------------------------------------------
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
                                int32_t *perm, int32_t *pos_of, int32_t *active, int32_t *num_active,
-                               int32_t *exrec, const float *rms, int32_t *lds) {
+                               int32_t *exrec, int32_t *lds) {
   const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;
   int32_t *cnt = lds, *base = lds + E;
   uint32_t *bm = (uint32_t *)(lds + 2 * E);
@@ -364,11 +400,7 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
         perm[pos] = (int32_t)(t * K + p);
         pos_of[t * K + p] = pos;
         const int32_t j = pos - segs[e];  // entry index inside the expert's segment
-        if (j < (int32_t)kRecTokens) {
-          int32_t *rec = exrec + aidx[e] * kRecWords;
-          rec[4 + j] = (int32_t)(t * K + p);
-          rec[4 + kRecTokens + j] = __float_as_int(rms ? 1.0f / rms[t] : 1.0f);
-        }
+        if (j < (int32_t)kRecTokens) exrec[aidx[e] * kRecWords + 4 + j] = (int32_t)(t * K + p);
       }
     }
     __syncthreads();
@@ -381,7 +413,7 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) { return sizeof(int32_t)
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec, a.rms,
+  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec,
                  (int32_t *)smem);
 }
 
@@ -399,21 +431,27 @@ __device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
 }
 
+// Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
+struct RouteOut {
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;
+};
+
+// Routing of T <= 16 tokens over E <= 64 * J experts from logits lg[t * E + e] (global or LDS) by
+// a workgroup of at least T waves.  Every wave of the workgroup must call it (it has a barrier).
 template <int J>
-__global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
-  __shared__ int8_t rank_l[kSmallRouteMaxTokens][kMaxExperts];
-  __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
-  __shared__ int32_t invr_l[kSmallRouteMaxTokens];
-  const uint32_t T = a.n, E = a.E, K = a.K;
+__device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+                                 int8_t (*rank_l)[kMaxExperts], float (*selv_l)[kMaxTopK]) {
   const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
-  if (t < T && lane == 0) invr_l[t] = __float_as_int(a.rms ? 1.0f / a.rms[t] : 1.0f);
   if (t < T) {
     float v[J];
     uint64_t key[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const uint32_t e = lane + 64u * j;
-      v[j] = e < E ? a.logits[(size_t)t * E + e] : 0.0f;
+      v[j] = e < E ? lg[(size_t)t * E + e] : 0.0f;
       key[j] = topk_key(v[j], e);
     }
     uint32_t rank[J];
@@ -433,16 +471,16 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
     for (int j = 0; j < J; ++j) {
       const uint32_t e = lane + 64u * j;
       if (e >= E) continue;
-      const bool s = rank[j] < K;
-      rank_l[t][e] = s ? (int8_t)rank[j] : (int8_t)-1;
-      if (s) {
+      const bool sel = rank[j] < K;
+      rank_l[t][e] = sel ? (int8_t)rank[j] : (int8_t)-1;
+      if (sel) {
         selv_l[t][rank[j]] = v[j];
-        a.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
+        o.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    for (uint32_t p = lane; p < K; p += 64u) a.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
+    for (uint32_t p = lane; p < K; p += 64u) o.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
   __syncthreads();
   if (t != 0) return;
@@ -479,19 +517,19 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
   for (int j = 0; j < J; ++j) {
     const uint32_t e = lane + 64u * j;
     if (e >= E) continue;
-    a.seg_off[e] = off[j];
+    o.seg_off[e] = off[j];
     if (cnt[j] > 0) {
-      a.active[ra[j]] = (int32_t)e;
-      int32_t *rec = a.exrec + ra[j] * kRecWords;
+      o.active[ra[j]] = (int32_t)e;
+      int32_t *rec = o.exrec + ra[j] * kRecWords;
       rec[0] = (int32_t)e;
       rec[1] = off[j];
       rec[2] = cnt[j];
     }
-    if ((int)e >= nact) a.active[e] = -1;
+    if ((int)e >= nact) o.active[e] = -1;
   }
   if (lane == 0) {
-    a.seg_off[E] = total;
-    *a.num_active = nact;
+    o.seg_off[E] = total;
+    *o.num_active = nact;
   }
   int seen[J];
 #pragma unroll
@@ -504,16 +542,116 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
       const int r = rank_l[t2][e];
       if (r >= 0) {
         const int pos = off[j] + seen[j];
-        a.perm[pos] = (int32_t)(t2 * K + (uint32_t)r);
-        a.pos_of[t2 * K + (uint32_t)r] = pos;
-        if (seen[j] < (int)kRecTokens) {
-          int32_t *rec = a.exrec + ra[j] * kRecWords;
-          rec[4 + seen[j]] = (int32_t)(t2 * K + (uint32_t)r);
-          rec[4 + kRecTokens + seen[j]] = invr_l[t2];
-        }
+        const int32_t slot = (int32_t)(t2 * K + (uint32_t)r);
+        o.perm[pos] = slot;
+        o.pos_of[slot] = pos;
+        if (seen[j] < (int)kRecTokens) o.exrec[ra[j] * kRecWords + 4 + seen[j]] = slot;
         seen[j] += 1;
       }
     }
+  }
+}
+
+template <int J>
+__global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
+  __shared__ int8_t rank_l[kSmallRouteMaxTokens][kMaxExperts];
+  __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
+  const RouteOut o{a.topk_idx, a.topk_w, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec};
+  route_small_body<J>(a.logits, a.n, a.E, a.K, o, rank_l, selv_l);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Decode router (n <= 16 tokens, D % 8 == 0, D <= 512 * kFrontChunks, 16-byte aligned rows):
+// workgroup e = expert e, wave w = tokens 2w and 2w + 1.  Every lane issues all of its loads
+// at once (router row chunks and both tokens' chunks; workgroup 0 also gamma), then computes the
+// two dot products and sums of squares in the fixed lane order (lane l owns chunks
+// c = 512 i + 8 l + j, fmaf over i then j, xor butterfly) -- no LDS, no barrier.
+// logit = dot / r + b with r = sqrt(sum(x^2) / D + eps) (r = 1 without RmsNorm).  Workgroup 0
+// writes r and the normalised rows xn_t = x_t * (1/r_t) * gamma (x_t without RmsNorm) in the x
+// dtype, zero padded to Dp, for the expert GEMV.  Results equal router_kernel bit for bit.
+// ---------------------------------------------------------------------------------------------
+template <typename XT, typename WT>
+__global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
+  constexpr int RC = kFrontChunks;
+  const uint32_t D = a.D, E = a.E, n = a.n;
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t e = blockIdx.x;
+  const uint32_t t0 = 2u * w, t1 = min(2u * w + 1u, n - 1u);
+  const bool has1 = 2u * w + 1u < n;
+  const XT *x = (const XT *)a.x;
+  const WT *rw = (const WT *)a.rw + (size_t)e * D;
+  const bool xn_wg = blockIdx.x == 0 && a.xn;
+
+  Chunk8<WT> wc[RC];
+  Chunk8<XT> xc0[RC], xc1[RC];
+  Chunk8<float> gc[RC];
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const uint32_t c0 = min(512u * i + 8u * lane, D - 8u);  // clamped: lanes past D reload a valid chunk
+    chunk_load(wc[i], rw + c0);
+    chunk_load(xc0[i], x + (size_t)t0 * D + c0);
+    chunk_load(xc1[i], x + (size_t)t1 * D + c0);
+    if (xn_wg && a.apply_norm) chunk_load(gc[i], a.gamma + c0);
+  }
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // dot t0, dot t1, sumsq t0, sumsq t1
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    if (512u * i + 8u * lane >= D) continue;
+    float wv[8], x0[8], x1[8];
+    chunk_vals(wc[i], wv);
+    chunk_vals(xc0[i], x0);
+    chunk_vals(xc1[i], x1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[0] = fmaf(x0[j], wv[j], acc[0]);
+      acc[1] = fmaf(x1[j], wv[j], acc[1]);
+      acc[2] = fmaf(x0[j], x0[j], acc[2]);
+      acc[3] = fmaf(x1[j], x1[j], acc[3]);
+    }
+  }
+  wave_sum_butterfly_n<4>(acc);
+  const float r0 = a.apply_norm ? sqrtf(acc[2] / (float)D + a.eps) : 1.0f;
+  const float r1 = a.apply_norm ? sqrtf(acc[3] / (float)D + a.eps) : 1.0f;
+  if (lane == 0) {
+    a.logits[(size_t)t0 * E + e] = (a.apply_norm ? acc[0] / r0 : acc[0]) + a.rb[e];
+    if (has1) a.logits[(size_t)t1 * E + e] = (a.apply_norm ? acc[1] / r1 : acc[1]) + a.rb[e];
+    if (blockIdx.x == 0 && a.rms) {
+      a.rms[t0] = r0;
+      if (has1) a.rms[t1] = r1;
+    }
+  }
+  if (!xn_wg) return;
+  const float ir0 = 1.0f / r0, ir1 = 1.0f / r1;
+  XT *xn0 = (XT *)a.xn + (size_t)t0 * a.Dp;
+  XT *xn1 = (XT *)a.xn + (size_t)t1 * a.Dp;
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const uint32_t c0 = 512u * i + 8u * lane;
+    if (c0 >= a.Dp) continue;  // Dp is a multiple of 32, D of 8: a chunk is all data or all padding
+    float x0[8], x1[8], g[8];
+    if (c0 < D) {
+      chunk_vals(xc0[i], x0);
+      chunk_vals(xc1[i], x1);
+      if (a.apply_norm) {
+        chunk_vals(gc[i], g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          x0[j] = (x0[j] * ir0) * g[j];
+          x1[j] = (x1[j] * ir1) * g[j];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x0[j] = x1[j] = 0.0f;
+    }
+    store8(xn0 + c0, x0);
+    if (has1) store8(xn1 + c0, x1);
+  }
+  // rows beyond RC chunks of padding (Dp > 512 * RC cannot happen: Dp <= D + 31 <= 512 * RC + 31)
+  for (uint32_t c0 = 512u * RC + 8u * lane; c0 < a.Dp; c0 += 512u) {
+    const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    store8(xn0 + c0, z);
+    if (has1) store8(xn1 + c0, z);
   }
 }
 
@@ -538,23 +676,28 @@ __device__ __forceinline__ float swiglu_clamp(float g, float l, float alpha, flo
   return (xg * sig) * (xl + 1.0f);
 }
 
-// Grid of G workgroups (as many as stay resident).  Each active expert gets wpe = G / num_active
-// workgroups, each owning a contiguous range of that expert's row tiles, so every workgroup
-// stages one expert's B operand once.  A workgroup learns num_active, its expert, segment and
-// first tokens from one round trip (num_active plus the record table).  The B operand (xn = x * (1/r) * gamma split into NT bf16
-// terms, or the f32 act rows of the down projection) is staged into LDS with every global load of
-// a batch issued before any is consumed; the first weight chunk is requested before staging.
-// Each wave then streams its tiles with the next chunk's loads -- also across tile boundaries --
-// in flight while the current chunk is on the matrix cores.
+// Work split.  Grid of G workgroups (as many as stay resident); each active expert gets
+// wpe = G / num_active of them, each owning a contiguous range of that expert's row tiles
+// (wave w of a workgroup: tiles rt_lo + w, rt_lo + w + 4, ...), so every workgroup stages its
+// expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
+// one pass at decode sizes).  A workgroup learns num_active, its expert, segment and first tokens
+// from one round trip (num_active plus the record table).
+// Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups; the next step's
+// loads (also across tile and pass boundaries) are issued before the current step goes to the
+// matrix cores, into the other of two register buffers, so no register copy has to wait for
+// them.  Everything a step consumes besides the weights (bias, B from LDS) is requested before
+// that prefetch: loads complete in order, so waiting for those never waits for the prefetch.
+// At start-up the B operand's staging loads are issued before the first weight loads for the same
+// reason.  No branch surrounds a weight load.
 template <int NT, bool GATE_UP, typename XT>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
+  constexpr uint32_t CJ = kGemvKgPerWave;
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
   const uint32_t mtm = a.mt_max;
   uint16_t *bs = (uint16_t *)smem;
   int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec));  // [kRecWords]
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
-  float *r_l = (float *)(tok_l + mtm);                                            // [mtm]
   const uint32_t nrt = a.nrt;
   // one round trip: num_active and the record table (staged through the B area)
   {
@@ -570,75 +713,82 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t ai = blockIdx.x / wpe, part = blockIdx.x % wpe;
   if (ai >= na) return;
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = ((const int32_t *)smem)[ai * kRecWords + threadIdx.x];
+  __syncthreads();
+  const int e = rec_l[0];
+  const int seg0 = rec_l[1];
+  const int M = rec_l[2];
+  const uint32_t npass = ((uint32_t)M + mtm - 1u) / mtm;
   // even split of the expert's row tiles over its wpe workgroups (wpe <= nrt: none is empty)
   const uint32_t rt_lo = (uint32_t)(((uint64_t)part * nrt) / wpe);
   const uint32_t rt_hi = (uint32_t)(((uint64_t)(part + 1u) * nrt) / wpe);
-  __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2;
   const uint32_t tail = a.nb - 4u * (nkg - 1u);
-  const uint32_t nch = (nkg + 3u) >> 2;  // 4-K-group chunks per tile
+  const uint32_t nst = (nkg + CJ - 1u) / CJ;  // steps per tile
+  const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
+  const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
 
-  // Unconditional loads: a lane whose (K-group, block) lies outside the tile reads the tile's
-  // first 16 bytes instead (always valid memory) and is neutralised at use time (scale 1.0 and a
-  // zero B operand).  No branch surrounds a load, so the compiler keeps the next chunk's loads
-  // in flight (partial vmcnt waits) while the current chunk is on the matrix cores.
+  // K-group of slot j of step st; lanes outside the tile load the tile's first 16 bytes instead
+  // (valid memory) and are neutralised at use (scale 1.0, zero B): no branch surrounds a load, so
+  // partial vmcnt waits keep later loads in flight.
+  auto kg_of = [&](uint32_t st, uint32_t j) { return CJ * st + j; };
   auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
-  auto load_chunk = [&](const uint8_t *wt, const uint8_t *st, uint32_t c0, uint4(&av)[4], uint32_t(&sv)[4]) {
+  auto load_step = [&](uint32_t rt, uint32_t st, uint4(&av)[CJ], uint32_t(&sv)[CJ]) {
+    const uint8_t *wt = wexp + (size_t)rt * a.nb * 256u;
+    const uint8_t *stp = sexp + (size_t)rt * a.nb * 16u;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t kg = c0 + (uint32_t)u;
+    for (uint32_t j = 0; j < CJ; ++j) {
+      const uint32_t kg = kg_of(st, j);
       const bool ok = lane_ok(kg);
-      av[u] = *(const uint4 *)(wt + (ok ? kg * 1024u + lane * 16u : 0u));
-      sv[u] = (uint32_t)st[ok ? kg * 64u + lane : 0u];
+      av[j] = *(const uint4 *)(wt + (ok ? kg * 1024u + lane * 16u : 0u));
+      // the dword holding this lane's scale byte (byte lane & 3), kept raw until use: a byte load
+      // would be re-extended at the loop back-edge, which waits for the prefetch to land
+      sv[j] = *(const uint32_t *)(stp + (ok ? kg * 64u + (lane & ~3u) : 0u));
     }
   };
+  const uint32_t sshift = 8u * (lane & 3u);
 
-  {
-    const int e = rec_l[0];
-    const int seg0 = rec_l[1];
-    const int M = rec_l[2];
-    const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
-    const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
-    // this wave's tiles: rt_lo + wv, rt_lo + wv + 4, ...
-    const uint32_t my_first = rt_lo + wv;
-    const uint32_t my_tiles = my_first < rt_hi ? (rt_hi - my_first + 3u) / 4u : 0u;
-
-    for (int m0 = 0; m0 < M; m0 += (int)mtm) {
-      const uint32_t mt = (uint32_t)min((int)mtm, M - m0);
-      // first weight chunk requested before the staging
-      uint4 acur[4];
-      uint32_t scur[4];
-      if (my_tiles > 0)
-        load_chunk(wexp + (size_t)my_first * a.nb * 256u, sexp + (size_t)my_first * a.nb * 16u, 0u, acur, scur);
-      __syncthreads();
-      if (threadIdx.x < mt) {
-        // token, 1/r (within 1 ulp of dividing by r) and slot t * topk + p of segment entry jj:
-        // from the record for the first kRecTokens entries, else from the global segment list
-        const uint32_t jj = (uint32_t)m0 + threadIdx.x;
-        int32_t slot, tk;
-        float ir;
-        if (jj < kRecTokens) {
-          slot = rec_l[4 + jj];
-          tk = slot / (int32_t)a.topk;
-          ir = __int_as_float(rec_l[4 + kRecTokens + jj]);
-        } else {
-          slot = a.perm[seg0 + (int)jj];
-          tk = slot / (int32_t)a.topk;
-          ir = a.apply_norm ? 1.0f / a.rms[tk] : 1.0f;
-        }
-        tok_l[threadIdx.x] = GATE_UP ? tk : slot;
-        r_l[threadIdx.x] = ir;
-      }
-      __syncthreads();
-      // stage B: mt tokens x Kp, NT bf16 terms, zero beyond the true K; batches of SB items with
-      // all of a batch's global loads issued before any is consumed
-      constexpr int SB = 2;
-      const uint32_t k8n = Kp >> 3, nitems = mt * k8n;
-      auto store_item = [&](uint32_t id, const float (&v8)[8]) {
+  // Staging of the B operand for token pass `pass_`: mt rows x Kp, NT bf16 terms, zero beyond the
+  // true K.  Rows: gate_up the routed tokens' xn rows, down the segment's act rows (both
+  // [*, Kp] in XT).  `first_loads` runs once, after the first batch's global loads are issued.
+  uint32_t mt = 0, m0 = 0;
+  auto stage = [&](uint32_t pass_, auto &&first_loads) {
+    m0 = pass_ * mtm;
+    mt = min(mtm, (uint32_t)M - m0);
+    if (threadIdx.x < mt) {
+      // slot t * topk + p of segment entry jj: from the record for the first kRecTokens entries,
+      // else from the global segment list
+      const uint32_t jj = m0 + threadIdx.x;
+      const int32_t slot = jj < kRecTokens ? rec_l[4 + jj] : a.perm[seg0 + (int)jj];
+      tok_l[threadIdx.x] = GATE_UP ? slot / (int32_t)a.topk : slot;
+    }
+    __syncthreads();
+    constexpr int SB = NT == 1 ? 3 : 2;
+    const XT *src = (const XT *)a.brows;
+    const uint32_t k8n = Kp >> 3, nitm = mt * k8n;
+    bool first = true;
+    for (uint32_t base = threadIdx.x; base < nitm; base += SB * blockDim.x) {
+      Chunk8<XT> cx[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitm - 1u);
         const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+        const size_t row = GATE_UP ? (size_t)tok_l[j] : (size_t)(seg0 + (int)(m0 + j));
+        chunk_load(cx[u], src + row * Kp + kb);
+      }
+      if (first) first_loads();
+      first = false;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const uint32_t id = base + (uint32_t)u * blockDim.x;
+        if (id >= nitm) continue;
+        const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+        float v8[8];
+        chunk_vals(cx[u], v8);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) v8[v] = kb + (uint32_t)v < a.kt ? v8[v] : 0.0f;
         uint32_t pk[NT][4];
 #pragma unroll
         for (int v = 0; v < 8; v += 2) {
@@ -651,144 +801,102 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
         for (int term = 0; term < NT; ++term)
           *(uint4 *)(bs + ((size_t)term * mtm + j) * ldk + kb) = make_uint4(pk[term][0], pk[term][1], pk[term][2], pk[term][3]);
-      };
-      for (uint32_t base = threadIdx.x; base < nitems; base += SB * blockDim.x) {
-        if constexpr (GATE_UP) {
-          Chunk8<XT> cx[SB];
-          Chunk8<float> cg[SB];
-#pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitems - 1u);
-            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
-            if (a.x_vec && kb + 8u <= a.kt) {
-              chunk_load(cx[u], (const XT *)a.x + (size_t)tok_l[j] * a.kt + kb);
-              if (a.apply_norm) chunk_load(cg[u], a.gamma + kb);
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            const uint32_t id = base + (uint32_t)u * blockDim.x;
-            if (id >= nitems) continue;
-            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
-            const uint32_t nv = kb < a.kt ? min(8u, a.kt - kb) : 0u;
-            float v8[8], g8[8];
-            if (a.x_vec && nv == 8u) {
-              chunk_vals(cx[u], v8);
-              if (a.apply_norm) chunk_vals(cg[u], g8);
-            } else {
-              load8_guarded((const XT *)a.x + (size_t)tok_l[j] * a.kt + kb, nv, v8);
-              if (a.apply_norm) load8_guarded(a.gamma + kb, nv, g8);
-            }
-            const float ir = r_l[j];
-#pragma unroll
-            for (int v = 0; v < 8; ++v)
-              v8[v] = (uint32_t)v < nv ? (a.apply_norm ? (v8[v] * ir) * g8[v] : v8[v]) : 0.0f;
-            store_item(id, v8);
-          }
-        } else {
-          float4 lo[SB], hi[SB];
-#pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitems - 1u);
-            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
-            const float *src = a.act + (size_t)(seg0 + m0 + (int)j) * Kp + kb;
-            lo[u] = *(const float4 *)src;
-            hi[u] = *(const float4 *)(src + 4);
-          }
-#pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            const uint32_t id = base + (uint32_t)u * blockDim.x;
-            if (id >= nitems) continue;
-            const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
-            const float t8[8] = {lo[u].x, lo[u].y, lo[u].z, lo[u].w, hi[u].x, hi[u].y, hi[u].z, hi[u].w};
-            float v8[8];
-#pragma unroll
-            for (int v = 0; v < 8; ++v) v8[v] = kb + (uint32_t)v < a.kt ? t8[v] : 0.0f;
-            store_item(id, v8);
-          }
-        }
       }
-      __syncthreads();
+    }
+    if (first) first_loads();
+    __syncthreads();
+  };
 
-      const bool bval = i16 < mt;
-      const uint16_t *brow = bs + (size_t)i16 * ldk;
-      const uint32_t nsteps = my_tiles * nch;
-      uint32_t ti = 0, c = 0;  // tile ordinal and chunk inside the tile of the current step
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (uint32_t g = 0; g < nsteps; ++g) {
-        const uint32_t rt = my_first + 4u * ti;
-        // prefetch the next step (next chunk of this tile, or chunk 0 of the next tile)
-        uint4 anx[4];
-        uint32_t snx[4];
-        {
-          // next step: next chunk of this tile, chunk 0 of the next tile, or (last step) the
-          // current chunk again -- a cache hit that keeps the load count static
-          const bool last_c = c + 1u == nch;
-          const bool more = g + 1u < nsteps;
-          const uint32_t nrt_ = (last_c && more) ? rt + 4u : rt;
-          const uint32_t nc = more ? (last_c ? 0u : c + 1u) : c;
-          load_chunk(wexp + (size_t)nrt_ * a.nb * 256u, sexp + (size_t)nrt_ * a.nb * 16u, 4u * nc, anx, snx);
-        }
+  // this wave's tiles: rt_lo + wv, rt_lo + wv + 4, ... < rt_hi (first tile clamped into the expert
+  // for the start-up loads of a wave without tiles)
+  const uint32_t my_first = rt_lo + wv;
+  const uint32_t my_tiles = my_first < rt_hi ? (rt_hi - my_first + 3u) / 4u : 0u;
+  const uint32_t first_c = min(my_first, nrt - 1u);
+  const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
+  uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
+  uint4 abuf0[CJ], abuf1[CJ];
+  uint32_t sbuf0[CJ], sbuf1[CJ];
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+
+  // One step: prefetch the next step into (an, sn), run the current one from (ac, scv), and at
+  // the end of a tile run the epilogue.  Returns false when the wave's steps are done.
+  auto do_step = [&](uint4(&ac)[CJ], uint32_t(&scv)[CJ], uint4(&an)[CJ], uint32_t(&sn)[CJ]) -> bool {
+    if (g >= total) return false;
+    const uint32_t rt = my_first + 4u * ti;
+    // the bias of this lane's 4 epilogue rows, requested before the prefetch
+    const f32x4_t bias4 = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + rt * 16u + 4u * q);
+    {
+      // next step: next step of this tile, step 0 of the next tile, or (last step of the pass)
+      // the current step again -- a cache hit that keeps the load count static
+      const bool more_st = st + 1u < nst;
+      const bool more_t = ti + 1u < my_tiles;
+      const uint32_t nrt_ = more_st ? rt : (more_t ? rt + 4u : rt);
+      const uint32_t nst_ = more_st ? st + 1u : (more_t ? 0u : st);
+      load_step(nrt_, nst_, an, sn);
+    }
+    const bool bval = i16 < mt;
+    const uint16_t *brow = bs + (size_t)min(i16, mtm - 1u) * ldk;  // rows >= mt: zeroed at use
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t kg = 4u * c + (uint32_t)u;
-          const bool ok = lane_ok(kg);
-          const bool bok = bval && ok;
-          const float sc = ok ? e8m0_to_f32(scur[u]) : 1.0f;
-          const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
-          const uint32_t wd[4] = {acur[u].x, acur[u].y, acur[u].z, acur[u].w};
+    for (uint32_t j = 0; j < CJ; ++j) {
+      const uint32_t kg = kg_of(st, j);
+      const bool ok = lane_ok(kg);
+      const bool bok = bval && ok;
+      const float sc = ok ? e8m0_to_f32((scv[j] >> sshift) & 0xFFu) : 1.0f;
+      const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
+      const uint32_t wd[4] = {ac[j].x, ac[j].y, ac[j].z, ac[j].w};
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
 #pragma unroll
-            for (int term = 0; term < NT; ++term) {
-              const u32x4_t raw = *(const u32x4_t *)(brow + (size_t)term * mtm * ldk + kb + 8u * s);
-              const u32x4_t z = {0u, 0u, 0u, 0u};
-              const bf16x8_t B = __builtin_bit_cast(bf16x8_t, bok ? raw : z);
-              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, acc, 0, 0, 0);
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          acur[u] = anx[u];
-          scur[u] = snx[u];
-        }
-        if (c + 1u == nch) {
-          // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
-          if (bval) {
-            const int pos = seg0 + m0 + (int)i16;
-            const uint32_t r0 = rt * 16u + 4u * q;
-            if constexpr (GATE_UP) {
-              const float *bb = a.bias + (size_t)e * a.bias_estride + r0;
-              const uint32_t f0 = r0 >> 1;
-              const float o0 = swiglu_clamp(acc[0] + bb[0], acc[1] + bb[1], a.alpha, a.limit);
-              const float o1 = swiglu_clamp(acc[2] + bb[2], acc[3] + bb[3], a.alpha, a.limit);
-              float *o = a.out + (size_t)pos * a.out_stride + f0;
-              if (f0 + 1u < a.out_rows) {
-                *(float2 *)o = make_float2(o0, o1);
-              } else if (f0 < a.out_rows) {
-                o[0] = o0;
-              }
-            } else {
-              // token-major slot row t * topk + p, expert bias b2 added once
-              const float *bb = a.bias + (size_t)e * a.bias_estride + r0;
-              float *o = a.out + (size_t)tok_l[i16] * a.out_stride + r0;
-              if (r0 + 3u < a.out_rows) {
-                *(float4 *)o = make_float4(acc[0] + bb[0], acc[1] + bb[1], acc[2] + bb[2], acc[3] + bb[3]);
-              } else {
-                for (uint32_t r = 0; r < 4u; ++r)
-                  if (r0 + r < a.out_rows) o[r] = acc[r] + bb[r];
-              }
-            }
-          }
-          acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          c = 0;
-          ++ti;
-        } else {
-          ++c;
+        for (int term = 0; term < NT; ++term) {
+          const u32x4_t raw = *(const u32x4_t *)(brow + (size_t)term * mtm * ldk + kb + 8u * s);
+          const u32x4_t z = {0u, 0u, 0u, 0u};
+          const bf16x8_t B = __builtin_bit_cast(bf16x8_t, bok ? raw : z);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, acc, 0, 0, 0);
         }
       }
+      // keep each K-group's LDS reads next to its MFMAs (bounds the live B registers)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    ++g;
+    if (++st < nst) return true;
+    st = 0;
+    // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
+    if (bval) {
+      const uint32_t r0 = rt * 16u + 4u * q;
+      if constexpr (GATE_UP) {
+        const int pos = seg0 + (int)(m0 + i16);
+        const uint32_t f0 = r0 >> 1;
+        const float o0 = swiglu_clamp(acc[0] + bias4[0], acc[1] + bias4[1], a.alpha, a.limit);
+        const float o1 = swiglu_clamp(acc[2] + bias4[2], acc[3] + bias4[3], a.alpha, a.limit);
+        float *o = a.out + (size_t)pos * a.out_stride + f0;
+        if (f0 + 1u < a.out_rows) {
+          *(float2 *)o = make_float2(o0, o1);
+        } else if (f0 < a.out_rows) {
+          o[0] = o0;
+        }
+      } else {
+        // token-major slot row t * topk + p, expert bias b2 added once
+        float *o = a.out + (size_t)tok_l[i16] * a.out_stride + r0;
+        if (r0 + 3u < a.out_rows) {
+          *(float4 *)o = make_float4(acc[0] + bias4[0], acc[1] + bias4[1], acc[2] + bias4[2], acc[3] + bias4[3]);
+        } else {
+          for (uint32_t r = 0; r < 4u; ++r)
+            if (r0 + r < a.out_rows) o[r] = acc[r] + bias4[r];
+        }
+      }
+    }
+    acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    return ++ti < my_tiles;
+  };
+  for (uint32_t pass = 0; pass < npass; ++pass) {
+    // every wave (also one without tiles) reaches the staging barriers of every pass
+    if (pass > 0) __syncthreads();  // all waves done with the previous pass's B
+    stage(pass, [&] { load_step(first_c, 0u, abuf0, sbuf0); });
+    ti = 0;
+    st = 0;
+    g = 0;
+    while (do_step(abuf0, sbuf0, abuf1, sbuf1) && do_step(abuf1, sbuf1, abuf0, sbuf0)) {
     }
   }
 }
@@ -923,6 +1031,21 @@ hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
     small_route_kernel<2><<<dim3(1), block, 0, s>>>(a);
   else
     small_route_kernel<4><<<dim3(1), block, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hipStream_t s) {
+  if (a.n == 0 || a.n > kSmallRouteMaxTokens || a.D % 8u != 0 || a.D > 512u * kFrontChunks || !a.logits)
+    return hipErrorInvalidValue;
+  const dim3 g(a.E), b(64 * ((a.n + 1) / 2));
+  if (x_bf16 && w_bf16)
+    router_small_kernel<uint16_t, uint16_t><<<g, b, 0, s>>>(a);
+  else if (x_bf16)
+    router_small_kernel<uint16_t, float><<<g, b, 0, s>>>(a);
+  else if (w_bf16)
+    router_small_kernel<float, uint16_t><<<g, b, 0, s>>>(a);
+  else
+    router_small_kernel<float, float><<<g, b, 0, s>>>(a);
   return hipGetLastError();
 }
 

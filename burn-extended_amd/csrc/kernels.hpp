@@ -14,7 +14,9 @@ struct RouterArgs {
   const float *rb;    // router bias [E]
   float *logits;      // [n, E]
   float *rms;         // [n] (written when apply_norm), nullable
-  uint32_t n, D, Dpad, E, tb, epw;
+  void *xn;           // [n, Dp] normalised rows in the x dtype (expert group 0 writes), nullable
+  const float *gamma; // [D]
+  uint32_t n, D, Dpad, Dp, E, tb, epw;
   float eps;
   int apply_norm;
 };
@@ -28,18 +30,16 @@ struct TopkArgs {
 };
 
 // Per-active-expert record written by the routing kernels: [0] expert, [1] segment offset,
-// [2] segment size M, [3] unused, [4 + j] slot t*K + p of the j-th segment entry and
-// [4 + kRecTokens + j] its 1/r (f32 bits, 1.0 without RmsNorm), for j < min(M, kRecTokens).
-// The expert GEMVs load the records of every possible active slot together with num_active in
-// one round trip and map themselves onto the active experts from that.
+// [2] segment size M, [3] unused, [4 + j] slot t*K + p of the j-th segment entry, for
+// j < min(M, kRecTokens).  The expert GEMVs load the records of every possible active slot
+// together with num_active in one round trip and map themselves onto the active experts.
 constexpr uint32_t kRecWords = 32;
-constexpr uint32_t kRecTokens = 14;
+constexpr uint32_t kRecTokens = 28;
 
 struct DispatchArgs {
   const int32_t *topk_idx;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;     // [E, kRecWords]
-  const float *rms;   // [n] or null (no RmsNorm)
   uint32_t n, K, E;
 };
 
@@ -49,7 +49,7 @@ struct GemvArgs {
   const uint8_t *wb;      // tiled e2m1 blocks, expert stride wb_estride bytes
   const uint8_t *ws;      // tiled e8m0 scales, expert stride ws_estride bytes
   uint64_t wb_estride, ws_estride;
-  const float *bias;      // gate_up: b1 [E, rows_p] (interleaved order); down: b2 [E, D]
+  const float *bias;      // [E, rows_p] (zero padded): gate_up b1 (interleaved order), down b2
   uint32_t bias_estride;
   uint32_t nrt;           // 16-row tiles per expert
   uint32_t nb;            // 32-wide K blocks (K padded = 32 * nb)
@@ -60,13 +60,8 @@ struct GemvArgs {
   const int32_t *exrec;   // [E, kRecWords] per-active-expert records
   uint32_t nrec;          // records loaded: min(E, n * topk), every slot that can be active
   uint32_t topk;
-  // gate_up B operand: xn = apply_norm ? (x / rms[t]) * gamma : x, from x [n, kt] (x dtype)
-  const void *x;
-  const float *rms, *gamma;
-  int apply_norm;
-  int x_vec;              // x rows 16-byte aligned (base aligned, kt % 8 == 0): 128-bit loads
-  // down B operand: act [n*k, Kp] f32
-  const float *act;
+  // B operand rows: gate_up xn [n, Kp] (x dtype), down act [n*k, Kp] f32 (segment order)
+  const void *brows;
   float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
@@ -76,13 +71,28 @@ struct GemvArgs {
 // dispatch, all outputs to global.
 struct SmallRouteArgs {
   const float *logits;
-  const float *rms;  // [n] or null (no RmsNorm)
   int32_t *topk_idx;
   float *topk_w;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;    // [E, kRecWords]
   uint32_t n, E, K;
 };
+
+// Decode-sized router (router_small_kernel, n <= kSmallRouteMaxTokens, D % 8 == 0, aligned rows):
+// logits, r and the normalised rows xn for the gate_up GEMV.
+struct FrontArgs {
+  const void *x;
+  const void *rw;      // router weight [E, D], gamma-folded when apply_norm
+  const float *rb;     // [E]
+  const float *gamma;  // [D]
+  void *xn;            // [n, Dp] x dtype, or null
+  float *logits;       // [n, E]
+  float *rms;          // [n] or null
+  uint32_t n, D, Dp, E;
+  float eps;
+  int apply_norm;
+};
+constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 
 struct CombineArgs {
   const void *x;
@@ -107,15 +117,15 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
 }
-// B staging (which first holds the record table), the chosen record, the per-token row index
-// and RmsNorm denominator.
+// B staging (which first holds the record table), the chosen record and the per-token row index.
 __host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
   const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = 4u * (size_t)nrec * 32u;
   return b > t ? b : t;
 }
 __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
-  return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 8u * (size_t)mt_max + 16u;
+  return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
+constexpr uint32_t kGemvKgPerWave = 4;  // K-groups per wave per step (6 KiB of weights in flight)
 
 constexpr uint32_t kRouterThreads = 256;
 constexpr uint32_t kTopkThreads = 512;
@@ -127,6 +137,7 @@ constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-work
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);
+hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
 hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);

@@ -80,7 +80,7 @@ struct burnext_moe_layer {
   uint32_t Dp = 0, Fp = 0;
   TiledMx w1, w2;
   float *b1 = nullptr;  // [E, w1.rows_p], interleaved (gate, linear) order
-  float *b2 = nullptr;  // [E, D]
+  float *b2 = nullptr;  // [E, w2.rows_p] (rows padded to the 16-row tile, zeros)
   void *router_w = nullptr;   // [E, D] as given (routing without RmsNorm)
   bool router_bf16 = false;
   void *router_wg = nullptr;  // [E, D] gamma-folded rows (routing with RmsNorm); may alias router_w
@@ -216,7 +216,7 @@ bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t
 
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, act, ypart, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, xn, act, ypart, total;
 };
 
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
@@ -236,6 +236,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   w.exrec = take((uint64_t)L.E * kRecWords * 4);
   w.perm = take(nk * 4);
   w.pos_of = take(nk * 4);
+  w.xn = take(n * L.Dp * 4);  // normalised rows, x dtype (f32 size covers both)
   w.act = take(nk * L.Fp * 4);
   w.ypart = take(nk * L.Dp * 4);
   w.total = off;
@@ -249,6 +250,7 @@ struct WsPtrs {
   float *topk_w;
   int32_t *seg_off, *active, *num_active, *perm, *pos_of;
   int32_t *exrec;
+  void *xn;
   float *act, *ypart;
 };
 
@@ -263,6 +265,7 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.active = p.seg_off + L.E + 1;
   p.num_active = p.active + L.E;
   p.exrec = (int32_t *)(b + w.exrec);
+  p.xn = b + w.xn;
   p.perm = (int32_t *)(b + w.perm);
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
@@ -311,8 +314,11 @@ burnext_status check_launch(hipError_t e, const char *what) {
 
 // Router logits (and r per token when normalising) into the workspace.
 burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
-                          float *logits, hipStream_t s) {
+                          float *logits, void *xn, hipStream_t s) {
   RouterArgs ra{};
+  ra.xn = xn;
+  ra.gamma = L->gamma;
+  ra.Dp = L->Dp;
   ra.x = x;
   ra.rw = norm ? L->router_wg : L->router_w;
   const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
@@ -332,14 +338,13 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
   return check_launch(launch_router(ra, x_bf16, w_bf16, vec, s), "router kernel launch");
 }
 
-// rms: per-token r when RmsNorm is applied (the records then carry 1/r), else null.
-burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *rms, hipStream_t s) {
+burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *logits,
+                               int32_t *topk_idx, float *topk_w, hipStream_t s) {
   SmallRouteArgs a{};
-  a.logits = p.logits;
-  a.rms = rms;
+  a.logits = logits;
   a.exrec = p.exrec;
-  a.topk_idx = p.topk_idx;
-  a.topk_w = p.topk_w;
+  a.topk_idx = topk_idx;
+  a.topk_w = topk_w;
   a.seg_off = p.seg_off;
   a.perm = p.perm;
   a.pos_of = p.pos_of;
@@ -365,11 +370,9 @@ burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, i
 }
 
 burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
-                            int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec,
-                            const float *rms, hipStream_t s) {
+                            int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec, hipStream_t s) {
   DispatchArgs da{};
   da.exrec = exrec;
-  da.rms = rms;
   da.topk_idx = idx;
   da.seg_off = seg_off;
   da.perm = perm;
@@ -381,6 +384,35 @@ burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx
   da.E = L->E;
   ProfScope ps(L, s, kKDispatch);
   return check_launch(launch_dispatch(da, s), "dispatch kernel launch");
+}
+
+// The decode-sized router (one wave per expert and token pair) covers n <= 16 tokens with
+// D % 8 == 0, D <= 3072 and 16-byte aligned x and router rows; otherwise router_kernel runs.
+bool router_small_ok(const burnext_moe_layer &L, uint64_t n, const void *x, bool norm) {
+  const void *rw = norm ? L.router_wg : L.router_w;
+  return n >= 1 && n <= kSmallRouteMaxTokens && L.D % 8 == 0 && L.D <= 512u * kFrontChunks &&
+         ((uintptr_t)x & 15u) == 0 && ((uintptr_t)rw & 15u) == 0;
+}
+
+burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
+                                float *logits, void *xn, hipStream_t s) {
+  FrontArgs a{};
+  a.x = x;
+  a.rw = norm ? L->router_wg : L->router_w;
+  const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
+  a.rb = L->router_b;
+  a.gamma = L->gamma;
+  a.xn = xn;
+  a.logits = logits;
+  a.rms = rms;
+  a.n = (uint32_t)n;
+  a.D = L->D;
+  a.Dp = L->Dp;
+  a.E = L->E;
+  a.eps = L->eps;
+  a.apply_norm = norm ? 1 : 0;
+  ProfScope ps(L, s, kKRouter);
+  return check_launch(launch_router_small(a, x_bf16, w_bf16, s), "router kernel launch");
 }
 
 burnext_status check_ws(burnext_moe_layer *L, uint64_t n, void *ws, uint64_t ws_bytes, WsLayout &w) {
@@ -464,11 +496,12 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
     return st;
   }
   // biases (f32 on device), b1 permuted to the interleaved internal row order
-  std::vector<float> hb1((size_t)E * L->w1.rows_p, 0.0f), hb2((size_t)E * D), hrb(E, 0.0f), hg(D, 1.0f);
+  std::vector<float> hb1((size_t)E * L->w1.rows_p, 0.0f), hb2((size_t)E * L->w2.rows_p, 0.0f), hrb(E, 0.0f),
+      hg(D, 1.0f);
   for (uint32_t e = 0; e < E; ++e) {
     for (uint32_t r = 0; r < 2 * F; ++r)
       hb1[(size_t)e * L->w1.rows_p + r] = read_scalar(b1, bias_dtype, (size_t)e * 2 * F + w1_src_row(r, F, gate_up_layout));
-    for (uint32_t d = 0; d < D; ++d) hb2[(size_t)e * D + d] = read_scalar(b2, bias_dtype, (size_t)e * D + d);
+    for (uint32_t d = 0; d < D; ++d) hb2[(size_t)e * L->w2.rows_p + d] = read_scalar(b2, bias_dtype, (size_t)e * D + d);
     if (router_b) hrb[e] = read_scalar(router_b, router_dtype, e);
   }
   if (norm_gamma)
@@ -549,15 +582,14 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
   const bool norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
-  st = run_router(L, x, xb, n, norm, p.rms, p.logits, s);
-  if (st != BURNEXT_OK) return st;
-  if (n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, norm ? p.rms : nullptr, s);
-  } else {
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
+                                  : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
+  if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
+    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
+  } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
-      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec,
-                        norm ? p.rms : nullptr, s);
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, s);
   }
   if (st != BURNEXT_OK) return st;
 
@@ -571,13 +603,15 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.wb_estride = t.blocks_per_expert;
     g.ws_estride = t.scales_per_expert;
     g.bias = gate_up ? L->b1 : L->b2;
-    g.bias_estride = gate_up ? L->w1.rows_p : L->D;
+    g.bias_estride = t.rows_p;  // multiple of 16: 16-byte aligned rows of 4 for the epilogue
     g.nrt = t.nrt;
     g.nb = t.nb;
     g.kt = t.cols;
     g.out_rows = gate_up ? L->F : L->D;
     const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
-    uint32_t mt = (uint32_t)std::min<uint64_t>(16, n);
+    // LDS rows reserved for one token pass: 8 at decode sizes (3 workgroups per CU at D = 2880;
+    // a segment above 8 tokens takes a second pass), 16 for larger batches
+    uint32_t mt = (uint32_t)std::min<uint64_t>(n <= 16 ? 8 : 16, n);
     mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
     g.mt_max = mt;
     g.seg_off = p.seg_off;
@@ -586,12 +620,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.perm = p.perm;
     g.exrec = p.exrec;
     g.topk = L->K;
-    g.x = x;
-    g.rms = p.rms;
-    g.gamma = L->gamma;
-    g.apply_norm = norm ? 1 : 0;
-    g.x_vec = (L->D % 8 == 0 && ((uintptr_t)x & 15u) == 0) ? 1 : 0;
-    g.act = p.act;
+    g.brows = gate_up ? p.xn : (const void *)p.act;
     g.out = gate_up ? p.act : p.ypart;
     g.out_stride = gate_up ? L->Fp : L->Dp;
     g.alpha = L->alpha;
@@ -603,6 +632,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     const size_t lds = gemv_total_lds_bytes(nt, mt, t.nb, g.nrec);
     const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kLdsBudget / std::max<size_t>(lds, 1)));
     const uint64_t grid = std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L->num_cus * per_cu, max_active * t.nrt));
+    if (grid > 0x7fffffffull) return fail(BURNEXT_UNSUPPORTED, "expert GEMV grid too large");
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xb, (uint32_t)grid, s), gate_up ? "gate_up launch" : "down launch");
   };
@@ -645,8 +675,13 @@ burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_d
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
   float *lg = logits ? logits : p.logits;
-  st = run_router(L, x, x_dtype == BURNEXT_BF16, n, (flags & BURNEXT_APPLY_RMSNORM) != 0, p.rms, lg, s);
-  if (st == BURNEXT_OK) st = run_topk(L, n, lg, topk_idx, topk_w, s);
+  const bool xb = x_dtype == BURNEXT_BF16, norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
+  // the forward's routing kernels for this batch size
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, lg, nullptr, s)
+                                  : run_router(L, x, xb, n, norm, p.rms, lg, nullptr, s);
+  if (st == BURNEXT_OK)
+    st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, s)
+                                   : run_topk(L, n, lg, topk_idx, topk_w, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 
@@ -662,7 +697,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, nullptr, s);
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 
