@@ -255,6 +255,30 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
       store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
     }
   }
+  if (blockIdx.y == 0 && a.xq.hi) {
+    // two-term MXFP8 rows of xn for the grouped GEMM: one 32-value block per thread-iteration,
+    // zero beyond D up to the K-group padding
+    const uint32_t nbk = a.xq.kq >> 5;
+    for (uint32_t f = threadIdx.x; f < nh * nbk; f += blockDim.x) {
+      const uint32_t tt = f / nbk, bk = f - tt * nbk;
+      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
+      float v[32], amax = 0.0f;
+#pragma unroll
+      for (uint32_t j = 0; j < 32u; ++j) {
+        const uint32_t c = bk * 32u + j;
+        float u = 0.0f;
+        if (c < D) {
+          u = xs[(size_t)tt * Dpad + tpos(c)];
+          if (a.apply_norm) u = (u * ir) * a.gamma[c];
+        }
+        v[j] = u;
+        amax = fmaxf(amax, fabsf(u));
+      }
+      const size_t row = t0 + tt;
+      mx8_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * a.xq.kq + bk * 32u,
+                     a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
+    }
+  }
   if (has0 && lane < nh) {
     // lane tt writes token tt's logits (all lanes hold the reduced values)
     float v0 = 0.0f, v1 = 0.0f;
@@ -331,9 +355,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 // atomicOr) and popcount prefixes, so the result does not depend on thread timing.
 // LDS: cnt[E], base[E], bm[E * words], wpre[E * words] (words = blockDim.x / 32).
 // ---------------------------------------------------------------------------------------------
+// Work maps of both expert GEMV launches from num_active (all threads of the block).
+__device__ void write_gemv_maps(const GemvMaps &m, uint32_t na) {
+  if (!m.map) return;
+  for (uint32_t g = threadIdx.x; g < m.g1 + m.g2; g += blockDim.x) {
+    const bool up = g < m.g1;
+    const uint32_t G = up ? m.g1 : m.g2, nrt = up ? m.nrt1 : m.nrt2, gg = up ? g : g - m.g1;
+    uint2 v = make_uint2(0xFFFFu, 0u);
+    if (na > 0u) {
+      const uint32_t wpe = max(1u, min(G / na, nrt));
+      const uint32_t ai = gg / wpe, part = gg - ai * wpe;
+      if (ai < na) v = make_uint2(ai | (part << 16), wpe | (((nrt - part + wpe - 1u) / wpe) << 16));
+    }
+    m.map[g] = v;
+  }
+}
+
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
                                int32_t *perm, int32_t *pos_of, int32_t *active, int32_t *num_active,
-                               int32_t *exrec, int32_t *lds) {
+                               int32_t *exrec, const GemvMaps &maps, int32_t *tile_off, int32_t *lds) {
   const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;
   int32_t *cnt = lds, *base = lds + E;
   uint32_t *bm = (uint32_t *)(lds + 2 * E);
@@ -349,11 +389,13 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
   __syncthreads();
   // exclusive scan and active list, each expert's thread summing the counts below it
   for (uint32_t e = tid; e < E; e += nth) {
-    int32_t off = 0, ra = 0;
+    int32_t off = 0, ra = 0, toff = 0;
     for (uint32_t e2 = 0; e2 < e; ++e2) {
       off += cnt[e2];
       ra += cnt[e2] > 0;
+      toff += (cnt[e2] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
     }
+    if (tile_off) tile_off[e] = toff;
     seg_off[e] = off;
     base[e] = off;
     segs[e] = off;
@@ -366,12 +408,15 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
     }
     if (e + 1 == E) {
       seg_off[E] = off + cnt[e];
+      if (tile_off) tile_off[E] = toff + (cnt[e] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
       const int32_t na = ra + (cnt[e] > 0);
       *num_active = na;
+      lds[4 * E + 2 * E * words] = na;
       for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) active[e3] = -1;
     }
   }
   __syncthreads();
+  write_gemv_maps(maps, (uint32_t)lds[4 * E + 2 * E * words]);
   for (uint32_t c0 = 0; c0 < n; c0 += nth) {
     for (uint32_t i = tid; i < E * words; i += nth) bm[i] = 0u;
     __syncthreads();
@@ -400,7 +445,10 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
         perm[pos] = (int32_t)(t * K + p);
         pos_of[t * K + p] = pos;
         const int32_t j = pos - segs[e];  // entry index inside the expert's segment
-        if (j < (int32_t)kRecTokens) exrec[aidx[e] * kRecWords + 4 + j] = (int32_t)(t * K + p);
+        if (j < (int32_t)kRecTokens) {
+          exrec[aidx[e] * kRecWords + 4 + j] = (int32_t)t;
+          exrec[aidx[e] * kRecWords + 4 + kRecTokens + j] = (int32_t)(t * K + p);
+        }
       }
     }
     __syncthreads();
@@ -409,12 +457,14 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
   }
 }
 
-size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) { return sizeof(int32_t) * (size_t)E * (4 + 2 * (threads / 32)); }
+size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) {
+  return sizeof(int32_t) * ((size_t)E * (4 + 2 * (threads / 32)) + 4);
+}
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec,
-                 (int32_t *)smem);
+  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec, a.maps,
+                 a.tile_off, (int32_t *)smem);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -439,11 +489,16 @@ struct RouteOut {
   int32_t *exrec;
 };
 
+template <int J>
+__device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+                                     int8_t (*rank_l)[kMaxExperts], int32_t *na_l);
+
 // Routing of T <= 16 tokens over E <= 64 * J experts from logits lg[t * E + e] (global or LDS) by
 // a workgroup of at least T waves.  Every wave of the workgroup must call it (it has a barrier).
 template <int J>
 __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                 int8_t (*rank_l)[kMaxExperts], float (*selv_l)[kMaxTopK]) {
+                                 const GemvMaps &maps, int8_t (*rank_l)[kMaxExperts], float (*selv_l)[kMaxTopK],
+                                 int32_t *na_l) {
   const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
   if (t < T) {
     float v[J];
@@ -483,7 +538,16 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
     for (uint32_t p = lane; p < K; p += 64u) o.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
   __syncthreads();
-  if (t != 0) return;
+  if (t == 0) route_small_dispatch<J>(T, E, K, o, rank_l, na_l);
+  __syncthreads();
+  write_gemv_maps(maps, (uint32_t)*na_l);
+}
+
+// Wave 0 of route_small_body: counts, scan, active list, records, segment positions.
+template <int J>
+__device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+                                     int8_t (*rank_l)[kMaxExperts], int32_t *na_l) {
+  const uint32_t lane = threadIdx.x & 63u;
   int cnt[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -530,6 +594,7 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
   if (lane == 0) {
     o.seg_off[E] = total;
     *o.num_active = nact;
+    *na_l = nact;
   }
   int seen[J];
 #pragma unroll
@@ -545,7 +610,10 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
         const int32_t slot = (int32_t)(t2 * K + (uint32_t)r);
         o.perm[pos] = slot;
         o.pos_of[slot] = pos;
-        if (seen[j] < (int)kRecTokens) o.exrec[ra[j] * kRecWords + 4 + seen[j]] = slot;
+        if (seen[j] < (int)kRecTokens) {
+          o.exrec[ra[j] * kRecWords + 4 + seen[j]] = (int32_t)t2;
+          o.exrec[ra[j] * kRecWords + 4 + kRecTokens + seen[j]] = slot;
+        }
         seen[j] += 1;
       }
     }
@@ -556,8 +624,9 @@ template <int J>
 __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
   __shared__ int8_t rank_l[kSmallRouteMaxTokens][kMaxExperts];
   __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
+  __shared__ int32_t na_l;
   const RouteOut o{a.topk_idx, a.topk_w, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec};
-  route_small_body<J>(a.logits, a.n, a.E, a.K, o, rank_l, selv_l);
+  route_small_body<J>(a.logits, a.n, a.E, a.K, o, a.maps, rank_l, selv_l, &na_l);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -669,24 +738,24 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
 // f32 activations are split into NT bf16 terms (NT MFMAs per step).
 // ---------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ float swiglu_clamp(float g, float l, float alpha, float limit) {
-  const float xg = fminf(g, limit);
-  const float xl = fmaxf(-limit, fminf(l, limit));
-  const float sig = 1.0f / (1.0f + expf(-alpha * xg));
-  return (xg * sig) * (xl + 1.0f);
+// a / b for a < 2^20 and b <= 2^12 given rb = 1.0f / b: the rounding error of (a + 0.5) * rb
+// (< 2^-22 relative) is far below the distance 0.5 / b of (a + 0.5) / b from an integer.
+__device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
+  return (uint32_t)(((float)a + 0.5f) * rb);
 }
 
+
 // Work split.  Grid of G workgroups (as many as stay resident); each active expert gets
-// wpe = G / num_active of them, each owning a contiguous range of that expert's row tiles
-// (wave w of a workgroup: tiles rt_lo + w, rt_lo + w + 4, ...), so every workgroup stages its
-// expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
+// wpe = G / num_active of them; its part-th workgroup owns row tiles part + wpe * i (wave w:
+// i = w, w + 4, ...), so an expert's workgroups sweep its weights together (few pages hot at a
+// time) and every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
 // one pass at decode sizes).  A workgroup learns num_active, its expert, segment and first tokens
 // from one round trip (num_active plus the record table).
-// Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups; the next step's
-// loads (also across tile and pass boundaries) are issued before the current step goes to the
-// matrix cores, into the other of two register buffers, so no register copy has to wait for
-// them.  Everything a step consumes besides the weights (bias, B from LDS) is requested before
-// that prefetch: loads complete in order, so waiting for those never waits for the prefetch.
+// Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups held in one
+// register buffer; each K-group slot is refilled with the next step's K-group (also across tile
+// boundaries) right after its MFMAs, so kGemvKgPerWave - 1 K-groups stay in flight.  Everything
+// a step consumes besides the weights (bias, B from LDS) is requested before that step's
+// refills: loads complete in order, so waiting for those never waits for the prefetch.
 // At start-up the B operand's staging loads are issued before the first weight loads for the same
 // reason.  No branch surrounds a weight load.
 template <int NT, bool GATE_UP, typename XT>
@@ -699,28 +768,25 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec));  // [kRecWords]
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
   const uint32_t nrt = a.nrt;
-  // one round trip: num_active and the record table (staged through the B area)
+  // one round trip: this workgroup's work map entry and the record table (the table is staged
+  // through the B area)
+  const uint2 me = a.wgmap[blockIdx.x];
   {
     const uint4 *src = (const uint4 *)a.exrec;
     uint4 *dst = (uint4 *)smem;
     const uint32_t nv = a.nrec * (kRecWords / 4u);
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
-  const uint32_t na = (uint32_t)*a.num_active;
+  const uint32_t ai = me.x & 0xFFFFu;
+  if (ai == 0xFFFFu) return;  // workgroup-uniform: no work in this launch
+  const uint32_t part = me.x >> 16, wpe = me.y & 0xFFFFu, ntw = me.y >> 16;  // tiles part + wpe * i, i < ntw
   __syncthreads();
-  if (na == 0u) return;
-  const uint32_t wpe = max(1u, min(gridDim.x / na, nrt));
-  const uint32_t ai = blockIdx.x / wpe, part = blockIdx.x % wpe;
-  if (ai >= na) return;
-  if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = ((const int32_t *)smem)[ai * kRecWords + threadIdx.x];
-  __syncthreads();
-  const int e = rec_l[0];
-  const int seg0 = rec_l[1];
-  const int M = rec_l[2];
-  const uint32_t npass = ((uint32_t)M + mtm - 1u) / mtm;
-  // even split of the expert's row tiles over its wpe workgroups (wpe <= nrt: none is empty)
-  const uint32_t rt_lo = (uint32_t)(((uint64_t)part * nrt) / wpe);
-  const uint32_t rt_hi = (uint32_t)(((uint64_t)(part + 1u) * nrt) / wpe);
+  const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
+  if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
+  const int e = rec0[0];
+  const int seg0 = rec0[1];
+  const int M = rec0[2];
+  const uint32_t npass = (uint32_t)M <= mtm ? 1u : ((uint32_t)M + mtm - 1u) / mtm;
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
@@ -754,15 +820,24 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   // true K.  Rows: gate_up the routed tokens' xn rows, down the segment's act rows (both
   // [*, Kp] in XT).  `first_loads` runs once, after the first batch's global loads are issued.
   uint32_t mt = 0, m0 = 0;
+  const float rk8n = 1.0f / (float)(Kp >> 3);
   auto stage = [&](uint32_t pass_, auto &&first_loads) {
     m0 = pass_ * mtm;
     mt = min(mtm, (uint32_t)M - m0);
     if (threadIdx.x < mt) {
-      // slot t * topk + p of segment entry jj: from the record for the first kRecTokens entries,
+      // token t (gate_up) or slot t * topk + p (down) of segment entry jj: from the record for
+      // the first kRecTokens entries (pass 0 reads the table copy in LDS, later passes rec_l),
       // else from the global segment list
       const uint32_t jj = m0 + threadIdx.x;
-      const int32_t slot = jj < kRecTokens ? rec_l[4 + jj] : a.perm[seg0 + (int)jj];
-      tok_l[threadIdx.x] = GATE_UP ? slot / (int32_t)a.topk : slot;
+      const int32_t *rec = pass_ == 0 ? rec0 : rec_l;
+      int32_t v;
+      if (jj < kRecTokens) {
+        v = rec[4 + (GATE_UP ? 0u : kRecTokens) + jj];
+      } else {
+        const int32_t slot = a.perm[seg0 + (int)jj];
+        v = GATE_UP ? slot / (int32_t)a.topk : slot;
+      }
+      tok_l[threadIdx.x] = v;
     }
     __syncthreads();
     constexpr int SB = NT == 1 ? 3 : 2;
@@ -774,7 +849,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
         const uint32_t id = min(base + (uint32_t)u * blockDim.x, nitm - 1u);
-        const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+        const uint32_t j = div_small(id, rk8n), kb = (id - j * k8n) * 8u;
         const size_t row = GATE_UP ? (size_t)tok_l[j] : (size_t)(seg0 + (int)(m0 + j));
         chunk_load(cx[u], src + row * Kp + kb);
       }
@@ -784,7 +859,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       for (int u = 0; u < SB; ++u) {
         const uint32_t id = base + (uint32_t)u * blockDim.x;
         if (id >= nitm) continue;
-        const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+        const uint32_t j = div_small(id, rk8n), kb = (id - j * k8n) * 8u;
         float v8[8];
         chunk_vals(cx[u], v8);
 #pragma unroll
@@ -807,33 +882,34 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
   };
 
-  // this wave's tiles: rt_lo + wv, rt_lo + wv + 4, ... < rt_hi (first tile clamped into the expert
-  // for the start-up loads of a wave without tiles)
-  const uint32_t my_first = rt_lo + wv;
-  const uint32_t my_tiles = my_first < rt_hi ? (rt_hi - my_first + 3u) / 4u : 0u;
+  // this wave's tiles: part + wpe * i for i = wv, wv + 4, ... < ntw (first tile clamped into the
+  // expert for the start-up loads of a wave without tiles)
+  const uint32_t my_first = part + wpe * wv, tstride = 4u * wpe;
+  const uint32_t my_tiles = wv < ntw ? (ntw - wv + 3u) / 4u : 0u;
   const uint32_t first_c = min(my_first, nrt - 1u);
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
   uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
-  uint4 abuf0[CJ], abuf1[CJ];
-  uint32_t sbuf0[CJ], sbuf1[CJ];
+  uint4 abuf[CJ];
+  uint32_t sbuf[CJ];
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  // One step: prefetch the next step into (an, sn), run the current one from (ac, scv), and at
-  // the end of a tile run the epilogue.  Returns false when the wave's steps are done.
-  auto do_step = [&](uint4(&ac)[CJ], uint32_t(&scv)[CJ], uint4(&an)[CJ], uint32_t(&sn)[CJ]) -> bool {
+  // One step: the CJ K-groups of the current step, each slot refilled with the same slot of the
+  // next step as soon as its MFMAs have consumed it (so CJ - 1 K-groups stay in flight from one
+  // register buffer); at the end of a tile, the epilogue.  Returns false when the wave's steps
+  // are done.
+  auto do_step = [&]() -> bool {
     if (g >= total) return false;
-    const uint32_t rt = my_first + 4u * ti;
-    // the bias of this lane's 4 epilogue rows, requested before the prefetch
+    const uint32_t rt = my_first + tstride * ti;
+    // the bias of this lane's 4 epilogue rows, requested before this step's refills
     const f32x4_t bias4 = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + rt * 16u + 4u * q);
-    {
-      // next step: next step of this tile, step 0 of the next tile, or (last step of the pass)
-      // the current step again -- a cache hit that keeps the load count static
-      const bool more_st = st + 1u < nst;
-      const bool more_t = ti + 1u < my_tiles;
-      const uint32_t nrt_ = more_st ? rt : (more_t ? rt + 4u : rt);
-      const uint32_t nst_ = more_st ? st + 1u : (more_t ? 0u : st);
-      load_step(nrt_, nst_, an, sn);
-    }
+    // next step: next step of this tile, step 0 of the next tile, or (last step of the pass) the
+    // current step again -- a cache hit that keeps the load count static
+    const bool more_st = st + 1u < nst;
+    const bool more_t = ti + 1u < my_tiles;
+    const uint32_t nrt_ = more_st ? rt : (more_t ? rt + tstride : rt);
+    const uint32_t nst_ = more_st ? st + 1u : (more_t ? 0u : st);
+    const uint8_t *nwt = wexp + (size_t)nrt_ * a.nb * 256u;
+    const uint8_t *nsp = sexp + (size_t)nrt_ * a.nb * 16u;
     const bool bval = i16 < mt;
     const uint16_t *brow = bs + (size_t)min(i16, mtm - 1u) * ldk;  // rows >= mt: zeroed at use
 #pragma unroll
@@ -841,9 +917,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       const uint32_t kg = kg_of(st, j);
       const bool ok = lane_ok(kg);
       const bool bok = bval && ok;
-      const float sc = ok ? e8m0_to_f32((scv[j] >> sshift) & 0xFFu) : 1.0f;
+      const float sc = ok ? e8m0_to_f32((sbuf[j] >> sshift) & 0xFFu) : 1.0f;
       const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
-      const uint32_t wd[4] = {ac[j].x, ac[j].y, ac[j].z, ac[j].w};
+      const uint32_t wd[4] = {abuf[j].x, abuf[j].y, abuf[j].z, abuf[j].w};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
@@ -855,7 +931,14 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, acc, 0, 0, 0);
         }
       }
-      // keep each K-group's LDS reads next to its MFMAs (bounds the live B registers)
+      // refill slot j with the next step's K-group j
+      {
+        const uint32_t nkg_ = kg_of(nst_, j);
+        const bool nok = lane_ok(nkg_);
+        abuf[j] = *(const uint4 *)(nwt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
+        sbuf[j] = *(const uint32_t *)(nsp + (nok ? nkg_ * 64u + (lane & ~3u) : 0u));
+      }
+      // keep each K-group's LDS reads, MFMAs and refill together (bounds the live registers)
       __builtin_amdgcn_sched_barrier(0);
     }
     ++g;
@@ -867,8 +950,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       if constexpr (GATE_UP) {
         const int pos = seg0 + (int)(m0 + i16);
         const uint32_t f0 = r0 >> 1;
-        const float o0 = swiglu_clamp(acc[0] + bias4[0], acc[1] + bias4[1], a.alpha, a.limit);
-        const float o1 = swiglu_clamp(acc[2] + bias4[2], acc[3] + bias4[3], a.alpha, a.limit);
+        const float o0 = swiglu_clamp_f(acc[0] + bias4[0], acc[1] + bias4[1], a.alpha, a.limit);
+        const float o1 = swiglu_clamp_f(acc[2] + bias4[2], acc[3] + bias4[3], a.alpha, a.limit);
         float *o = a.out + (size_t)pos * a.out_stride + f0;
         if (f0 + 1u < a.out_rows) {
           *(float2 *)o = make_float2(o0, o1);
@@ -892,11 +975,11 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   for (uint32_t pass = 0; pass < npass; ++pass) {
     // every wave (also one without tiles) reaches the staging barriers of every pass
     if (pass > 0) __syncthreads();  // all waves done with the previous pass's B
-    stage(pass, [&] { load_step(first_c, 0u, abuf0, sbuf0); });
+    stage(pass, [&] { load_step(first_c, 0u, abuf, sbuf); });
     ti = 0;
     st = 0;
     g = 0;
-    while (do_step(abuf0, sbuf0, abuf1, sbuf1) && do_step(abuf1, sbuf1, abuf0, sbuf0)) {
+    while (do_step()) {
     }
   }
 }

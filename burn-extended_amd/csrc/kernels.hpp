@@ -5,6 +5,15 @@
 
 namespace burnext {
 
+// Two-term MXFP8 rows (see mx_device.hpp): kq code bytes per row and term, K padded to whole
+// 128-wide K-groups with zero codes and zero scale bytes, natural K order; kq / 32 scale bytes
+// per row and term.
+struct QRows {
+  uint8_t *hi, *lo;    // [rows, kq]
+  uint8_t *shi, *slo;  // [rows, kq / 32]
+  uint32_t kq;
+};
+
 // Router logits for a block of tokens x a group of experts.  With apply_norm the rows are the
 // gamma-folded router weights and logit = dot(x, gw) / r + b, r = sqrt(mean(x^2) + eps); the
 // workgroups of expert group 0 also write r per token for the expert GEMV staging.
@@ -15,6 +24,7 @@ struct RouterArgs {
   float *logits;      // [n, E]
   float *rms;         // [n] (written when apply_norm), nullable
   void *xn;           // [n, Dp] normalised rows in the x dtype (expert group 0 writes), nullable
+  QRows xq;           // the same rows as two-term MXFP8 (expert group 0 writes when xq.hi)
   const float *gamma; // [D]
   uint32_t n, D, Dpad, Dp, E, tb, epw;
   float eps;
@@ -30,16 +40,28 @@ struct TopkArgs {
 };
 
 // Per-active-expert record written by the routing kernels: [0] expert, [1] segment offset,
-// [2] segment size M, [3] unused, [4 + j] slot t*K + p of the j-th segment entry, for
-// j < min(M, kRecTokens).  The expert GEMVs load the records of every possible active slot
-// together with num_active in one round trip and map themselves onto the active experts.
+// [2] segment size M, [3] unused, [4 + j] token t and [4 + kRecTokens + j] slot t*K + p of the
+// j-th segment entry, for j < min(M, kRecTokens).
 constexpr uint32_t kRecWords = 32;
-constexpr uint32_t kRecTokens = 28;
+constexpr uint32_t kRecTokens = 14;
+
+// Work map of an expert GEMV launch, written by the routing kernels once num_active is known:
+// entry g (workgroup g of a grid of G) = {slot | part << 16, wpe | ntiles << 16}: workgroup g
+// serves active slot g / wpe (wpe = max(1, min(G / num_active, nrt))) as its part-th workgroup
+// and owns that expert's row tiles part, part + wpe, ... (ntiles of them), so the workgroups of
+// an expert sweep its weights together, a window of about wpe tiles; slot 0xFFFF = no work.
+// Gate_up and down maps are stored back to back.
+struct GemvMaps {
+  uint2 *map;      // [g1 + g2]
+  uint32_t g1, nrt1, g2, nrt2;
+};
 
 struct DispatchArgs {
   const int32_t *topk_idx;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;     // [E, kRecWords]
+  GemvMaps maps;      // map == null: none written
+  int32_t *tile_off;  // [E + 1] prefix of ceil(M_e / kGemmTok), or null
   uint32_t n, K, E;
 };
 
@@ -59,6 +81,7 @@ struct GemvArgs {
   const int32_t *seg_off, *active, *num_active, *perm;
   const int32_t *exrec;   // [E, kRecWords] per-active-expert records
   uint32_t nrec;          // records loaded: min(E, n * topk), every slot that can be active
+  const uint2 *wgmap;     // [gridDim.x] work map of this launch
   uint32_t topk;
   // B operand rows: gate_up xn [n, Kp] (x dtype), down act [n*k, Kp] f32 (segment order)
   const void *brows;
@@ -75,6 +98,7 @@ struct SmallRouteArgs {
   float *topk_w;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;    // [E, kRecWords]
+  GemvMaps maps;
   uint32_t n, E, K;
 };
 
@@ -93,6 +117,30 @@ struct FrontArgs {
   int apply_norm;
 };
 constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
+
+// Grouped expert GEMM for prefill-sized batches (expert_gemm_kernel): every active expert's
+// segment is cut into tiles of kGemmTok routed tokens; a workgroup computes kGemmRows weight
+// rows x one token tile with the block-scaled MFMA (MXFP4 weights x two-term MXFP8 activations).
+constexpr uint32_t kGemmTok = 128;
+constexpr uint32_t kGemmRows = 128;
+struct GemmArgs {
+  const uint8_t *wb, *ws;  // tiled MXFP4 layout (as GemvArgs)
+  uint64_t wb_estride, ws_estride;
+  const float *bias;       // [E, rows_p]
+  uint32_t bias_estride;
+  uint32_t nrt, nb, kt, out_rows;
+  uint32_t nrb;            // kGemmRows-row blocks per expert
+  const int32_t *seg_off;  // [E + 1]
+  const int32_t *tile_off; // [E + 1] exclusive prefix of ceil(M_e / kGemmTok)
+  const int32_t *perm;     // segment entries t * topk + p
+  uint32_t E, topk;
+  QRows b;                 // B rows: gate_up xq (token rows), down act (segment rows)
+  QRows act;               // gate_up output: SwiGLU rows in segment order, quantised
+  uint32_t act_feats;      // gate_up: F (features written; [F, act.kq) zero-filled)
+  float *out;              // down: token-major slot rows [n*k, out_stride] f32
+  uint32_t out_stride;
+  float alpha, limit;
+};
 
 struct CombineArgs {
   const void *x;
@@ -125,7 +173,7 @@ __host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint
 __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
   return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
-constexpr uint32_t kGemvKgPerWave = 4;  // K-groups per wave per step (6 KiB of weights in flight)
+constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
 constexpr uint32_t kRouterThreads = 256;
 constexpr uint32_t kTopkThreads = 512;
@@ -142,6 +190,9 @@ hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s);
+hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s);
+hipError_t configure_gemm_kernels();
+size_t gemm_lds_bytes();
 hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t configure_kernels();
 

@@ -214,10 +214,46 @@ bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t
   return true;
 }
 
+// Expert GEMV launch shape for n tokens: token rows staged per pass and the persistent grid (as
+// many workgroups as stay resident: LDS-limited, at most 4 per CU, at least one per possible
+// active expert; the work map gives each active expert grid / num_active of them).
+struct GemvCfg {
+  uint32_t mt, grid, nrec;
+};
+
+GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
+  const TiledMx &t = gate_up ? L.w1 : L.w2;
+  GemvCfg c{};
+  const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
+  // LDS rows reserved for one token pass: 8 at decode sizes (3 workgroups per CU at D = 2880;
+  // a segment above 8 tokens takes a second pass), 16 for larger batches
+  uint32_t mt = (uint32_t)std::min<uint64_t>(n <= 16 ? 8 : 16, n);
+  c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
+  const uint64_t max_active = std::min<uint64_t>(L.E, n * L.K);
+  c.nrec = (uint32_t)max_active;
+  const size_t lds = gemv_total_lds_bytes(nt, c.mt, t.nb, c.nrec);
+  const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, (160 * 1024) / std::max<size_t>(lds, 1)));
+  c.grid = (uint32_t)std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L.num_cus * per_cu, max_active * t.nrt));
+  return c;
+}
+
+// Upper bound of gemv_cfg().grid over n (work map entries per launch).
+uint64_t gemv_max_grid(const burnext_moe_layer &L) { return std::max<uint64_t>(L.E, 4ull * L.num_cus); }
+
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, xn, act, ypart, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, wgmap, perm, pos_of, xn, act, ypart, total;
+  uint64_t tile_off, xq[4], aq[4];  // grouped-GEMM path: tile prefix, xq / act rows (hi lo shi slo)
+  bool gemm;                        // the grouped-GEMM regions are present
 };
+
+// bf16 batches of at least this many tokens run the grouped GEMM (expert segments of ~n*k/E
+// tokens fill its 128-token tiles); smaller ones, and every f32 batch (the GEMM's two MXFP8
+// terms carry bf16-level precision), run the expert GEMVs.
+constexpr uint64_t kGemmMinTokens = 256;
+
+// Row bytes of two-term MXFP8 rows over K = cols of a tiled projection (whole 128-wide K-groups).
+inline uint32_t qrow_bytes(const TiledMx &t) { return ((t.nb + 3u) / 4u) * 128u; }
 
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   WsLayout w{};
@@ -234,10 +270,24 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   w.topk_w = take(nk * 4);
   w.meta = take((2ull * L.E + 2) * 4);
   w.exrec = take((uint64_t)L.E * kRecWords * 4);
+  w.wgmap = take(2ull * gemv_max_grid(L) * 8);
   w.perm = take(nk * 4);
   w.pos_of = take(nk * 4);
+  w.gemm = n >= kGemmMinTokens;
   w.xn = take(n * L.Dp * 4);  // normalised rows, x dtype (f32 size covers both)
   w.act = take(nk * L.Fp * 4);
+  if (w.gemm) {
+    w.tile_off = take((L.E + 1ull) * 4);
+    const uint64_t kx = qrow_bytes(L.w1), ka = qrow_bytes(L.w2);
+    w.xq[0] = take(n * kx);
+    w.xq[1] = take(n * kx);
+    w.xq[2] = take(n * kx / 32);
+    w.xq[3] = take(n * kx / 32);
+    w.aq[0] = take(nk * ka);
+    w.aq[1] = take(nk * ka);
+    w.aq[2] = take(nk * ka / 32);
+    w.aq[3] = take(nk * ka / 32);
+  }
   w.ypart = take(nk * L.Dp * 4);
   w.total = off;
   return w;
@@ -250,8 +300,11 @@ struct WsPtrs {
   float *topk_w;
   int32_t *seg_off, *active, *num_active, *perm, *pos_of;
   int32_t *exrec;
+  uint2 *wgmap;
   void *xn;
   float *act, *ypart;
+  int32_t *tile_off;
+  QRows xq, aq;
 };
 
 WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
@@ -266,6 +319,12 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.num_active = p.active + L.E;
   p.exrec = (int32_t *)(b + w.exrec);
   p.xn = b + w.xn;
+  p.wgmap = (uint2 *)(b + w.wgmap);
+  if (w.gemm) {
+    p.tile_off = (int32_t *)(b + w.tile_off);
+    p.xq = QRows{b + w.xq[0], b + w.xq[1], b + w.xq[2], b + w.xq[3], qrow_bytes(L.w1)};
+    p.aq = QRows{b + w.aq[0], b + w.aq[1], b + w.aq[2], b + w.aq[3], qrow_bytes(L.w2)};
+  }
   p.perm = (int32_t *)(b + w.perm);
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
@@ -314,9 +373,10 @@ burnext_status check_launch(hipError_t e, const char *what) {
 
 // Router logits (and r per token when normalising) into the workspace.
 burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
-                          float *logits, void *xn, hipStream_t s) {
+                          float *logits, void *xn, hipStream_t s, const QRows *xq = nullptr) {
   RouterArgs ra{};
   ra.xn = xn;
+  if (xq) ra.xq = *xq;
   ra.gamma = L->gamma;
   ra.Dp = L->Dp;
   ra.x = x;
@@ -339,8 +399,9 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
 }
 
 burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *logits,
-                               int32_t *topk_idx, float *topk_w, hipStream_t s) {
+                               int32_t *topk_idx, float *topk_w, const GemvMaps &maps, hipStream_t s) {
   SmallRouteArgs a{};
+  a.maps = maps;
   a.logits = logits;
   a.exrec = p.exrec;
   a.topk_idx = topk_idx;
@@ -370,8 +431,11 @@ burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, i
 }
 
 burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
-                            int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec, hipStream_t s) {
+                            int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec,
+                            const GemvMaps &maps, hipStream_t s, int32_t *tile_off = nullptr) {
   DispatchArgs da{};
+  da.maps = maps;
+  da.tile_off = tile_off;
   da.exrec = exrec;
   da.topk_idx = idx;
   da.seg_off = seg_off;
@@ -415,6 +479,74 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
   return check_launch(launch_router_small(a, x_bf16, w_bf16, s), "router kernel launch");
 }
 
+// The weighted combine + residual of every path (token-major slot rows in p.ypart).
+burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
+                       const WsPtrs &p, hipStream_t s) {
+  CombineArgs c{};
+  c.x = x;
+  c.y = y;
+  c.ypart = p.ypart;
+  c.topk_w = p.topk_w;
+  c.n = (uint32_t)n;
+  c.D = L->D;
+  c.Dp = L->Dp;
+  c.K = L->K;
+  c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
+  burnext_status st;
+  {
+    ProfScope ps(L, s, kKCombine);
+    st = check_launch(launch_combine(c, xb, s), "combine launch");
+  }
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+// Grouped-GEMM path (n >= kGemmMinTokens): router (+ two-term MXFP8 rows of xn), top-k,
+// dispatch (+ token-tile prefix), gate_up GEMM (SwiGLU, quantised act rows), down GEMM (slot rows).
+burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64_t n, bool norm, const WsPtrs &p,
+                            hipStream_t s) {
+  burnext_status st = run_router(L, x, xb, n, norm, p.rms, p.logits, nullptr, s, &p.xq);
+  if (st == BURNEXT_OK) st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
+  if (st == BURNEXT_OK)
+    st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, s,
+                      p.tile_off);
+  if (st != BURNEXT_OK) return st;
+  const uint64_t nk = n * L->K;
+  const uint64_t max_tiles = (nk + kGemmTok - 1) / kGemmTok + std::min<uint64_t>(L->E, nk);
+  for (int up = 1; up >= 0; --up) {
+    const TiledMx &t = up ? L->w1 : L->w2;
+    GemmArgs g{};
+    g.wb = t.blocks;
+    g.ws = t.scales;
+    g.wb_estride = t.blocks_per_expert;
+    g.ws_estride = t.scales_per_expert;
+    g.bias = up ? L->b1 : L->b2;
+    g.bias_estride = t.rows_p;
+    g.nrt = t.nrt;
+    g.nb = t.nb;
+    g.kt = t.cols;
+    g.out_rows = up ? 2 * L->F : L->D;
+    g.nrb = (t.rows_p + kGemmRows - 1) / kGemmRows;
+    g.seg_off = p.seg_off;
+    g.tile_off = p.tile_off;
+    g.perm = p.perm;
+    g.E = L->E;
+    g.topk = L->K;
+    g.b = up ? p.xq : p.aq;
+    g.act = p.aq;
+    g.act_feats = L->F;
+    g.out = p.ypart;
+    g.out_stride = L->Dp;
+    g.alpha = L->alpha;
+    g.limit = L->limit;
+    const uint64_t grid = align_up((uint64_t)g.nrb * max_tiles, 8);
+    if (grid > 0x7fffffffull) return fail(BURNEXT_UNSUPPORTED, "expert GEMM grid too large");
+    ProfScope ps(L, s, up ? kKGateUp : kKDown);
+    st = check_launch(launch_gemm(g, up != 0, (uint32_t)grid, s), up ? "gate_up GEMM launch" : "down GEMM launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  return BURNEXT_OK;
+}
+
 burnext_status check_ws(burnext_moe_layer *L, uint64_t n, void *ws, uint64_t ws_bytes, WsLayout &w) {
   w = ws_layout(*L, n);
   if (!ws) return fail(BURNEXT_INVALID_ARG, "workspace is null");
@@ -451,6 +583,7 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   const uint32_t D = cfg->d_model, F = cfg->ffn_hidden, E = cfg->num_experts;
   if (D == 0 || F == 0 || E == 0) return fail(BURNEXT_INVALID_ARG, "d_model, ffn_hidden and num_experts must be > 0");
   if (E > kMaxExperts) return fail(BURNEXT_UNSUPPORTED, "num_experts above 256 is not supported");
+  if (D > 32768 || F > 32768) return fail(BURNEXT_UNSUPPORTED, "d_model and ffn_hidden above 32768 are not supported");
   const uint32_t K = std::min(std::max(cfg->experts_per_token, 1u), E);
   if (K > kMaxTopK) return fail(BURNEXT_UNSUPPORTED, "experts_per_token above 32 is not supported");
   if ((bias_dtype != BURNEXT_F32 && bias_dtype != BURNEXT_BF16) ||
@@ -471,7 +604,10 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   {
     static std::once_flag once;
     static hipError_t cfg_err = hipSuccess;
-    std::call_once(once, [] { cfg_err = configure_kernels(); });
+    std::call_once(once, [] {
+      cfg_err = configure_kernels();
+      if (cfg_err == hipSuccess) cfg_err = configure_gemm_kernels();
+    });
     if (cfg_err != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string("kernel configuration failed: ") + hipGetErrorString(cfg_err));
   }
 
@@ -582,20 +718,27 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
   const bool norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
+  if (w.gemm && xb) {
+    st = forward_gemm(L, x, xb, n, norm, p, s);
+    if (st != BURNEXT_OK) return st;
+    return combine(L, x, y, xb, n, flags, p, s);
+  }
+  const int nt = xb ? 1 : 3;
+  const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
+  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt};
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
+    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, maps, s);
   } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
-      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, s);
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, maps, s);
   }
   if (st != BURNEXT_OK) return st;
 
-  const int nt = xb ? 1 : 3;
-  const uint64_t max_active = std::min<uint64_t>(L->E, n * L->K);
   auto gemv = [&](bool gate_up) -> burnext_status {
+    const GemvCfg &cf = gate_up ? cfg_up : cfg_dn;
     const TiledMx &t = gate_up ? L->w1 : L->w2;
     GemvArgs g{};
     g.wb = t.blocks;
@@ -608,12 +751,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.nb = t.nb;
     g.kt = t.cols;
     g.out_rows = gate_up ? L->F : L->D;
-    const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
-    // LDS rows reserved for one token pass: 8 at decode sizes (3 workgroups per CU at D = 2880;
-    // a segment above 8 tokens takes a second pass), 16 for larger batches
-    uint32_t mt = (uint32_t)std::min<uint64_t>(n <= 16 ? 8 : 16, n);
-    mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
-    g.mt_max = mt;
+    g.mt_max = cf.mt;
     g.seg_off = p.seg_off;
     g.active = p.active;
     g.num_active = p.num_active;
@@ -625,37 +763,17 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.out_stride = gate_up ? L->Fp : L->Dp;
     g.alpha = L->alpha;
     g.limit = L->limit;
-    // persistent grid: as many workgroups as stay resident at once (LDS-limited, at most 4 per
-    // CU), at least one per possible active expert (the kernel gives each active expert
-    // grid / num_active workgroups)
-    g.nrec = (uint32_t)max_active;
-    const size_t lds = gemv_total_lds_bytes(nt, mt, t.nb, g.nrec);
-    const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kLdsBudget / std::max<size_t>(lds, 1)));
-    const uint64_t grid = std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L->num_cus * per_cu, max_active * t.nrt));
-    if (grid > 0x7fffffffull) return fail(BURNEXT_UNSUPPORTED, "expert GEMV grid too large");
+    g.nrec = cf.nrec;
+    g.wgmap = p.wgmap + (gate_up ? 0 : cfg_up.grid);
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
-    return check_launch(launch_gemv(g, nt, gate_up, xb, (uint32_t)grid, s), gate_up ? "gate_up launch" : "down launch");
+    return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
   st = gemv(false);
   if (st != BURNEXT_OK) return st;
 
-  CombineArgs c{};
-  c.x = x;
-  c.y = y;
-  c.ypart = p.ypart;
-  c.topk_w = p.topk_w;
-  c.n = (uint32_t)n;
-  c.D = L->D;
-  c.Dp = L->Dp;
-  c.K = L->K;
-  c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
-  {
-    ProfScope ps(L, s, kKCombine);
-    st = check_launch(launch_combine(c, xb, s), "combine launch");
-  }
-  return st == BURNEXT_OK ? ok() : st;
+  return combine(L, x, y, xb, n, flags, p, s);
 }
 
 burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, uint64_t n,
@@ -680,7 +798,7 @@ burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_d
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, lg, nullptr, s)
                                   : run_router(L, x, xb, n, norm, p.rms, lg, nullptr, s);
   if (st == BURNEXT_OK)
-    st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, s)
+    st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, GemvMaps{}, s)
                                    : run_topk(L, n, lg, topk_idx, topk_w, s);
   return st == BURNEXT_OK ? ok() : st;
 }
@@ -697,7 +815,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, s);
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 

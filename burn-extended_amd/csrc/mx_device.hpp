@@ -97,4 +97,75 @@ __device__ __forceinline__ bf16x8_t fp4x8_to_bf16x8(uint32_t w, float scale) {
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
+// ---------------------------------------------------------------------------------------------
+// MXFP8 (OCP e4m3fn with one e8m0 scale per 32 values), as the block-scaled MFMA reads it.
+// A value v of a block with scale byte sb is stored as e4m3(v * 2^(127 - sb)).  The scale of a
+// block is the smallest power of two that brings the block's largest magnitude to <= 448 (the
+// largest finite e4m3fn value), so every code is finite; an all-zero block gets scale byte 0.
+// Activations are carried as two such terms, hi + lo (lo = the block-scaled residual of hi),
+// which keeps about 2^-8 relative accuracy: bf16-like, where one term alone (2^-4) is not.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
+  const uint32_t u = __float_as_uint(amax);
+  const uint32_t be = (u >> 23) & 0xFFu;  // biased exponent: amax = m * 2^(be - 127), m in [1, 2)
+  if (amax <= 0.0f || be == 0u) return 0u;
+  const uint32_t adj = (u & 0x7FFFFFu) > 0x600000u ? 1u : 0u;  // m > 1.75: m * 256 > 448
+  const int sb = (int)be - 8 + (int)adj;
+  return (uint32_t)min(max(sb, 1), 253);
+}
+
+// 2^(127 - sb) for sb in [1, 253] (exact), the multiplier that applies the inverse scale.
+__device__ __forceinline__ float mx8_inv_scale(uint32_t sb) { return __uint_as_float((254u - sb) << 23); }
+
+// Two floats -> two e4m3fn codes (round to nearest even) in the low 16 bits.
+__device__ __forceinline__ uint32_t f32x2_to_fp8x2(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// e4m3fn code (byte SEL of w) -> float.
+template <int SEL>
+__device__ __forceinline__ float fp8_to_f32(uint32_t w) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)w, SEL);
+}
+
+// Clamped SwiGLU of one (gate, linear) pair (reference src/activation/mod.rs:5-45,
+// src/quant/gpu.rs:140-145): g = min(g, limit), l = clamp(l, +-limit), g * sigmoid(alpha g) * (l + 1).
+__device__ __forceinline__ float swiglu_clamp_f(float g, float l, float alpha, float limit) {
+  const float xg = fminf(g, limit);
+  const float xl = fmaxf(-limit, fminf(l, limit));
+  const float sig = 1.0f / (1.0f + expf(-alpha * xg));
+  return (xg * sig) * (xl + 1.0f);
+}
+
+// One block of 32 values (largest magnitude amax) -> two-term MXFP8: 32 hi codes, 32 lo codes
+// (16-byte aligned destinations) and the two scale bytes.
+__device__ __forceinline__ void mx8_quantize32(const float (&v)[32], float amax, uint8_t *hi, uint8_t *lo,
+                                               uint8_t *shi, uint8_t *slo) {
+  const uint32_t sbh = mx8_scale_byte(amax);
+  const float ih = sbh ? mx8_inv_scale(sbh) : 0.0f, sh = e8m0_to_f32(sbh);
+  uint32_t wh[8], wl[8];
+  float r[32], rmax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t c = f32x2_to_fp8x2(v[2 * k] * ih, v[2 * k + 1] * ih);
+    r[2 * k] = v[2 * k] - fp8_to_f32<0>(c) * sh;
+    r[2 * k + 1] = v[2 * k + 1] - fp8_to_f32<1>(c) * sh;
+    rmax = fmaxf(rmax, fmaxf(fabsf(r[2 * k]), fabsf(r[2 * k + 1])));
+    if (k & 1) wh[k >> 1] |= c << 16; else wh[k >> 1] = c;
+  }
+  const uint32_t sbl = mx8_scale_byte(rmax);
+  const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t c = f32x2_to_fp8x2(r[2 * k] * il, r[2 * k + 1] * il);
+    if (k & 1) wl[k >> 1] |= c << 16; else wl[k >> 1] = c;
+  }
+  *(uint4 *)hi = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+  *(uint4 *)(hi + 16) = make_uint4(wh[4], wh[5], wh[6], wh[7]);
+  *(uint4 *)lo = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+  *(uint4 *)(lo + 16) = make_uint4(wl[4], wl[5], wl[6], wl[7]);
+  *shi = (uint8_t)sbh;
+  *slo = (uint8_t)sbl;
+}
+
 }  // namespace burnext

@@ -229,6 +229,46 @@ def test_forward_prefill_sampled_rows(M, oracle):
     layer.close()
 
 
+# ---------------------------------------------------------------------------------------------
+# grouped-GEMM path (bf16 batches of >= 256 tokens): every output row against the oracle
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("D,F,E,K,n,layout,ue8,zipf", [
+    (256, 256, 4, 2, 300, "interleaved", 0, False),   # partial token tiles, 2 experts per token
+    (200, 96, 6, 3, 257, "halves", 14, False),        # K not a multiple of 128 or 32, tail K-groups
+    (512, 384, 8, 2, 1024, "interleaved", 0, True),   # skewed segments (multi-tile experts)
+    (2880, 2880, 32, 4, 512, "interleaved", 0, False),
+])
+def test_forward_gemm_path_all_rows(M, oracle, D, F, E, K, n, layout, ue8, zipf):
+    from burnext_amd import synth
+    bias = synth.zipf_router_bias(E, 1.1, gamma=1.0, seed=0) if zipf else None
+    L = _make(synth, D, F, E, K, seed=3, dtype="bf16", router_bias=bias, gate_up_layout=layout,
+              ue8_offset=ue8, with_gamma=True)
+    x = synth.make_tokens(n, D, seed=4, dtype="bf16")
+    print(f"gemm case D={D} F={F} E={E} K={K} n={n} {layout} ue8={ue8} zipf={zipf}", flush=True)
+    layer = M.MoeLayer(L)
+    y = _np(layer.forward(M.to_device_x(x, "bf16")))
+    torch.cuda.synchronize()
+    y_ref, _, _ = oracle.moe_forward(L, x)
+    err = oracle.max_abs_rel(y, y_ref)
+    moe_err = oracle.max_abs_rel(y - x, y_ref - x)
+    print(f"  max-abs-rel {err:.3e} (moe part {moe_err:.3e})")
+    assert np.isfinite(y).all()
+    assert err <= TOL_BF16 and moe_err <= TOL_BF16
+    layer.close()
+
+
+def test_gemm_path_deterministic(M):
+    from burnext_amd import synth
+    L = _make(synth, 512, 384, 8, 2, seed=5, dtype="bf16")
+    layer = M.MoeLayer(L)
+    x = M.to_device_x(synth.make_tokens(640, 512, seed=6, dtype="bf16"), "bf16")
+    y1 = layer.forward(x).clone()
+    y2 = layer.forward(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    layer.close()
+
+
 def test_moe_basic_zero_weights_residual(M):
     """tests/moe_basic_tests.rs:6-34: d=16, F=32, E=k=4, zero weights and biases => y == x."""
     from burnext_amd import synth
