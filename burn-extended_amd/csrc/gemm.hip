@@ -21,29 +21,40 @@ namespace burnext {
 typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
 
 namespace {
-// One K-group of the B tile in LDS, chunk-major: [term 2][16-byte chunk 8][token 128], so the 16
-// lanes reading one chunk of 16 consecutive tokens read 256 contiguous bytes; then the scale
-// dwords [term 2][token 128] (byte g = scale of K [32 g, 32 g + 32)).
-constexpr uint32_t kBufBytes = 2u * 8u * kGemmTok * 16u;
-constexpr uint32_t kScBytes = 2u * kGemmTok * 4u;
+// One pipeline stage (one 128-wide K-group) in LDS:
+//   B codes [term 2][token 128][slot 8] x 16 bytes, chunk c of token t in slot c ^ ((t >> 1) & 7):
+//     a fill instruction reads 8 whole 128-byte rows (coalesced) and the 16 lanes reading one
+//     chunk of 16 consecutive tokens hit 16 distinct 16-byte bank groups;
+//   B scale dwords [term 2][token 128] (byte g = scale of K [32 g, 32 g + 32));
+//   A codes [row tile 8][lane 64] x 16 bytes (the tiled weight layout's K-group, unchanged);
+//   A scales [row tile 8][lane 64] bytes.
+constexpr uint32_t kBData = 2u * 8u * kGemmTok * 16u;
+constexpr uint32_t kBScale = 2u * kGemmTok * 4u;
+constexpr uint32_t kAData = 8u * 64u * 16u;
+constexpr uint32_t kAScale = 8u * 64u;
+constexpr uint32_t kStage = kBData + kBScale + kAData + kAScale;
+constexpr uint32_t kStages = 3;
+constexpr uint32_t kWaves = 8;
 typedef __attribute__((address_space(3))) void lds_void;
+// s_waitcnt with vmcnt(n) only (expcnt and lgkmcnt left at their maxima), n < 16
+constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8); }
 }  // namespace
 
-size_t gemm_lds_bytes() { return 2 * ((size_t)kBufBytes + kScBytes) + 2 * kGemmTok * 4 + 64; }
+size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64; }
 
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
 // take a contiguous run of items, then item = token tile gt * nrb + row block rb (rb fastest):
-// the workgroups sharing a token tile's B run together on one XCD.  Each workgroup computes
-// kGemmRows weight rows (8 row tiles) x kGemmTok tokens with 4 waves of 64 x 64 (wave wr, wc:
-// rows 64 wr.., tokens 64 wc..; 4 x 4 MFMA tiles).  Per K-group the B tile (two terms) is staged
-// into LDS by direct-to-LDS loads (double buffered, one barrier per K-group) while each wave
-// loads its own A K-group (4 row tiles, 16 bytes per lane each) one K-group ahead.
+// the workgroups sharing a token tile's B run together on one XCD.  A workgroup (8 waves, one
+// per CU) computes kGemmRows weight rows (8 row tiles) x kGemmTok tokens; wave w computes rows
+// 64 (w / 4) .. and tokens 32 (w % 4) .. (4 x 2 MFMA tiles, two terms each).  K-groups stream
+// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (46 wave
+// instructions per stage, 5 or 6 per wave), one barrier per K-group.
 template <bool GATE_UP>
-__global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  int32_t *rows_l = (int32_t *)(smem + 2 * (kBufBytes + kScBytes));  // [kGemmTok] B row, -1 = none
-  int32_t *slot_l = rows_l + kGemmTok;                                // [kGemmTok] down: slot
-  int32_t *info_l = slot_l + kGemmTok;                                // [0] expert [1] tile of it
+  int32_t *rows_l = (int32_t *)(smem + kStages * kStage);  // [kGemmTok] B row, -1 = none
+  int32_t *slot_l = rows_l + kGemmTok;                     // [kGemmTok] down: slot
+  int32_t *info_l = slot_l + kGemmTok;                     // [0] expert [1] tile of it
 
   const uint32_t G = gridDim.x, b = blockIdx.x;
   const uint32_t it = (b & 7u) * (G >> 3) + (b >> 3);  // G is a multiple of 8
@@ -77,90 +88,89 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-  const uint32_t wr = wv >> 1, wc = wv & 1u;
+  const uint32_t wr = wv >> 2, wc = wv & 3u;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2, tail = a.nb - 4u * (nkg - 1u);
   const uint32_t kq = a.b.kq, sq = kq >> 5;  // code bytes and scale bytes per B row
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
+  auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
 
-  // ---- B staging by direct-to-LDS loads (no registers): per K-group 32 wave instructions of
-  // 64 x 16 bytes (wave w: instructions w, w + 4, ..: chunk plane (term, chunk) = i / 2, tokens
-  // 64 (i % 2) + lane) and 4 of 64 x 4 scale bytes (wave w: term w / 2, tokens 64 (w % 2) + lane).
-  // Token columns beyond the tile read the tile's first row; their results are never stored.
-  // row offsets of tokens lane and 64 + lane; wave w's scale instruction: term w / 2, half w % 2
+  // ---- stage fill by direct-to-LDS loads.  Token columns beyond the tile read the tile's first
+  // row and row tiles beyond the expert its last one; their results are never stored.  Lanes
+  // outside a K-group's blocks read the row tile's first 16 bytes; they are neutralised at use.
+  // B codes: instruction k = wv + 8 m (m < 4) of 32 fills term k / 16, tokens 8 (k % 16) + lane / 8;
+  // this lane's two tokens (m even / odd) and its swizzled chunk
+  const uint32_t tk0 = 8u * wv + (lane >> 3), tk1 = tk0 + 64u;
+  const int32_t rk0 = rows_l[tk0], rk1 = rows_l[tk1];
+  const size_t browk0 = (size_t)(rk0 >= 0 ? rk0 : rows_l[0]) * kq, browk1 = (size_t)(rk1 >= 0 ? rk1 : rows_l[0]) * kq;
+  const uint32_t bchunk = ((lane & 7u) ^ ((tk0 >> 1) & 7u)) * 16u;  // tk1 has the same swizzle
+  // B scales (waves 0-3): term wv / 2, tokens 64 (wv % 2) + lane
   const int32_t r0l = rows_l[lane], r1l = rows_l[64u + lane];
   const size_t row0 = (size_t)(r0l >= 0 ? r0l : rows_l[0]), row1 = (size_t)(r1l >= 0 ? r1l : rows_l[0]);
-  const uint8_t *ssrc = ((wv >> 1) ? a.b.slo : a.b.shi) + ((wv & 1u) ? row1 : row0) * sq;
+  const uint32_t a_rt = min(rb * 8u + wv, a.nrt - 1u);                    // A codes: row tile wv
+  const uint32_t as_rt = min(rb * 8u + (wv & 1u) * 4u + (lane >> 4), a.nrt - 1u);  // A scales (waves 4, 5)
   auto stage = [&](uint32_t kg, uint32_t p) {
-    uint8_t *bd = smem + p * kBufBytes;
+    uint8_t *st = smem + p * kStage;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t i = wv + 4u * (uint32_t)k;
-      const uint32_t plane = i >> 1, half = i & 1u, term = plane >> 3, chunk = plane & 7u;
-      const uint8_t *src = (term ? a.b.lo : a.b.hi) + (half ? row1 : row0) * kq;
-      __builtin_amdgcn_global_load_lds((const void *)(src + kg * 128u + chunk * 16u),
-                                       (lds_void *)(bd + (plane * kGemmTok + half * 64u) * 16u), 16, 0, 0);
+    for (int m = 0; m < 4; ++m) {  // B codes: term m / 2, token group wv + 8 (m % 2)
+      const uint32_t term = (uint32_t)m >> 1, tg = wv + 8u * ((uint32_t)m & 1u);
+      const uint8_t *src = (term ? a.b.lo : a.b.hi) + ((m & 1) ? browk1 : browk0) + kg * 128u + bchunk;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + (term * kGemmTok * 8u + tg * 64u) * 16u), 16, 0, 0);
     }
-    __builtin_amdgcn_global_load_lds((const void *)(ssrc + kg * 4u),
-                                     (lds_void *)(smem + 2 * kBufBytes + p * kScBytes +
-                                                  ((wv >> 1) * kGemmTok + (wv & 1u) * 64u) * 4u),
-                                     4, 0, 0);
-  };
-
-  // ---- A: this wave's 4 row tiles of K-group kg (lanes outside the tile's blocks read the
-  // tile's first 16 bytes and are neutralised: zero codes, scale 1)
-  uint32_t rtile[4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) rtile[rt] = min(rb * 8u + wr * 4u + (uint32_t)rt, a.nrt - 1u);
-  auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
-  uint4 aw[4];
-  uint32_t as[4];
-  auto load_a = [&](uint32_t kg, uint4(&w)[4], uint32_t(&s)[4]) {
-    const bool ok = lane_ok(kg);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      w[rt] = *(const uint4 *)(wexp + (size_t)rtile[rt] * a.nb * 256u + (ok ? kg * 1024u + lane * 16u : 0u));
-      s[rt] = *(const uint32_t *)(sexp + (size_t)rtile[rt] * a.nb * 16u + (ok ? kg * 64u + (lane & ~3u) : 0u));
+    {  // A codes of row tile wv
+      const bool ok = lane_ok(kg);
+      const uint8_t *src = wexp + (size_t)a_rt * a.nb * 256u + (ok ? kg * 1024u + lane * 16u : 0u);
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBData + kBScale + wv * 1024u), 16, 0, 0);
+    }
+    if (wv < 4u) {  // B scales: term wv / 2, tokens 64 (wv % 2) + lane
+      const uint8_t *src = ((wv >> 1) ? a.b.slo : a.b.shi) + ((wv & 1u) ? row1 : row0) * sq + kg * 4u;
+      __builtin_amdgcn_global_load_lds((const void *)src,
+                                       (lds_void *)(st + kBData + ((wv >> 1) * kGemmTok + (wv & 1u) * 64u) * 4u), 4, 0, 0);
+    } else if (wv < 6u) {  // A scales of row tiles 4 (wv - 4) .. +4: 4 bytes per lane
+      const uint32_t g = lane & 15u;  // 4-byte group of the row tile's 64 scale bytes
+      const uint8_t *src = sexp + (size_t)as_rt * a.nb * 16u + min(kg * 64u + 4u * g, a.nb * 16u - 4u);
+      __builtin_amdgcn_global_load_lds((const void *)src,
+                                       (lds_void *)(st + kBData + kBScale + kAData + (wv - 4u) * 256u), 4, 0, 0);
     }
   };
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][2];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < 2; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   stage(0, 0);
-  load_a(0, aw, as);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's direct-to-LDS loads have landed
+  stage(min(1u, nkg - 1u), 1);
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(5));  // stage 0 landed (this wave issued 5 or 6 after it)
   __syncthreads();
-  const uint32_t ash = 8u * (lane & 3u);
   for (uint32_t kg = 0; kg < nkg; ++kg) {
-    const uint32_t p = kg & 1u;
-    const uint32_t kn = min(kg + 1u, nkg - 1u);  // last iteration: reloads (unused), no branch
-    stage(kn, p ^ 1u);  // the other buffer: every wave left it at the previous barrier
-    uint4 awn[4];
-    uint32_t asn[4];
-    load_a(kn, awn, asn);
+    const uint32_t p = kg % kStages;
+    stage(min(kg + 2u, nkg - 1u), (kg + 2u) % kStages);  // the stage every wave left at the last barrier
+    const uint8_t *st = smem + p * kStage;
     const bool ok = lane_ok(kg);
     i32x8_t A[4];
     int32_t sa[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      const uint4 w4 = ok ? aw[rt] : make_uint4(0u, 0u, 0u, 0u);
-      A[rt] = i32x8_t{(int32_t)w4.x, (int32_t)w4.y, (int32_t)w4.z, (int32_t)w4.w, 0, 0, 0, 0};
-      sa[rt] = ok ? (int32_t)((as[rt] >> ash) & 0xFFu) : 127;
+      const uint32_t rtl = wr * 4u + (uint32_t)rt;
+      const uint4 w4 = *(const uint4 *)(st + kBData + kBScale + (rtl * 64u + lane) * 16u);
+      const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+      const uint4 v = ok ? w4 : z;
+      A[rt] = i32x8_t{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w, 0, 0, 0, 0};
+      sa[rt] = ok ? (int32_t)st[kBData + kBScale + kAData + rtl * 64u + lane] : 127;
     }
-    const uint8_t *bd = smem + p * kBufBytes;
-    const uint8_t *bsc = smem + 2 * kBufBytes + p * kScBytes;
+    const uint8_t *bsc = st + kBData;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 2; ++tt) {
+      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
       // lane group q: chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)) of both terms
-      const uint8_t *r = bd + (q * kGemmTok + tok) * 16u;
-      const uint4 h0 = *(const uint4 *)r, h1 = *(const uint4 *)(r + 4u * kGemmTok * 16u);
-      const uint4 l0 = *(const uint4 *)(r + 8u * kGemmTok * 16u), l1 = *(const uint4 *)(r + 12u * kGemmTok * 16u);
+      const uint32_t sw = (tok >> 1) & 7u;
+      const uint8_t *r = st + tok * 128u;
+      const uint32_t s1 = (q ^ sw) * 16u, s2 = ((4u + q) ^ sw) * 16u;
+      const uint4 h0 = *(const uint4 *)(r + s1), h1 = *(const uint4 *)(r + s2);
+      const uint4 l0 = *(const uint4 *)(r + kGemmTok * 128u + s1), l1 = *(const uint4 *)(r + kGemmTok * 128u + s2);
       const i32x8_t Bh = {(int32_t)h0.x, (int32_t)h0.y, (int32_t)h0.z, (int32_t)h0.w,
                           (int32_t)h1.x, (int32_t)h1.y, (int32_t)h1.z, (int32_t)h1.w};
       const i32x8_t Bl = {(int32_t)l0.x, (int32_t)l0.y, (int32_t)l0.z, (int32_t)l0.w,
@@ -171,15 +181,10 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
         acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bh, acc[rt][tt], 4, 0, 0, sa[rt], 0, sbh);
         acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, acc[rt][tt], 4, 0, 0, sa[rt], 0, sbl);
       }
-      // one token tile's B fragments live at a time
-      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      aw[rt] = awn[rt];
-      as[rt] = asn[rt];
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // K-group kn's direct-to-LDS loads have landed
+    // this wave issued 5 or 6 instructions for stage kg + 2 after stage kg + 1's: wait until at
+    // most 5 are outstanding (stage kg + 1 landed; an over-wait of one for waves that issued 6)
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(5));
     __syncthreads();
   }
 
@@ -189,8 +194,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     // features 8 rt + 2 q + {0, 1} (interleaved gate/linear row pairs) of its token columns.
     const uint32_t fb = rb * 64u + wr * 32u;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 2; ++tt) {
+      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
       float o[8];
       float amax = 0.0f;
 #pragma unroll
@@ -256,8 +261,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   } else {
     // token-major slot rows t * topk + p, expert bias b2 added once
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 2; ++tt) {
+      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
       if (tok >= ntok) continue;
       float *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
 #pragma unroll
@@ -287,9 +292,9 @@ hipError_t configure_gemm_kernels() {
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s) {
   if (grid == 0 || (grid & 7u) != 0 || a.nrb == 0 || a.b.kq % 128u != 0) return hipErrorInvalidValue;
   if (gate_up)
-    expert_gemm_kernel<true><<<dim3(grid), dim3(256), gemm_lds_bytes(), s>>>(a);
+    expert_gemm_kernel<true><<<dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s>>>(a);
   else
-    expert_gemm_kernel<false><<<dim3(grid), dim3(256), gemm_lds_bytes(), s>>>(a);
+    expert_gemm_kernel<false><<<dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s>>>(a);
   return hipGetLastError();
 }
 
