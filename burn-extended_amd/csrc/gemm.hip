@@ -26,12 +26,13 @@ namespace {
 //     a fill instruction reads 8 whole 128-byte rows (coalesced) and the 16 lanes reading one
 //     chunk of 16 consecutive tokens hit 16 distinct 16-byte bank groups;
 //   B scale dwords [term 2][token 128] (byte g = scale of K [32 g, 32 g + 32));
-//   A codes [row tile 8][lane 64] x 16 bytes (the tiled weight layout's K-group, unchanged);
-//   A scales [row tile 8][lane 64] bytes.
+//   A codes [row tile 16][lane 64] x 16 bytes (the tiled weight layout's K-group, unchanged);
+//   A scales [row tile 16][lane 64] bytes.
+constexpr uint32_t kRowTiles = kGemmRows / 16u;
 constexpr uint32_t kBData = 2u * 8u * kGemmTok * 16u;
 constexpr uint32_t kBScale = 2u * kGemmTok * 4u;
-constexpr uint32_t kAData = 8u * 64u * 16u;
-constexpr uint32_t kAScale = 8u * 64u;
+constexpr uint32_t kAData = kRowTiles * 64u * 16u;
+constexpr uint32_t kAScale = kRowTiles * 64u;
 constexpr uint32_t kStage = kBData + kBScale + kAData + kAScale;
 constexpr uint32_t kStages = 3;
 constexpr uint32_t kWaves = 8;
@@ -45,10 +46,10 @@ size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 6
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
 // take a contiguous run of items, then item = token tile gt * nrb + row block rb (rb fastest):
 // the workgroups sharing a token tile's B run together on one XCD.  A workgroup (8 waves, one
-// per CU) computes kGemmRows weight rows (8 row tiles) x kGemmTok tokens; wave w computes rows
-// 64 (w / 4) .. and tokens 32 (w % 4) .. (4 x 2 MFMA tiles, two terms each).  K-groups stream
-// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (46 wave
-// instructions per stage, 5 or 6 per wave), one barrier per K-group.
+// per CU) computes kGemmRows weight rows (16 row tiles) x kGemmTok tokens; wave w computes rows
+// 64 (w / 2) .. and tokens 64 (w % 2) .. (4 x 4 MFMA tiles, two terms each).  K-groups stream
+// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (56 wave
+// instructions per stage, 7 per wave), one barrier per K-group.
 template <bool GATE_UP>
 __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-  const uint32_t wr = wv >> 2, wc = wv & 3u;
+  const uint32_t wr = wv >> 1, wc = wv & 1u;
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2, tail = a.nb - 4u * (nkg - 1u);
   const uint32_t kq = a.b.kq, sq = kq >> 5;  // code bytes and scale bytes per B row
@@ -105,11 +106,12 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   const int32_t rk0 = rows_l[tk0], rk1 = rows_l[tk1];
   const size_t browk0 = (size_t)(rk0 >= 0 ? rk0 : rows_l[0]) * kq, browk1 = (size_t)(rk1 >= 0 ? rk1 : rows_l[0]) * kq;
   const uint32_t bchunk = ((lane & 7u) ^ ((tk0 >> 1) & 7u)) * 16u;  // tk1 has the same swizzle
-  // B scales (waves 0-3): term wv / 2, tokens 64 (wv % 2) + lane
+  // B scales (waves 4-7): term (wv - 4) / 2, tokens 64 (wv % 2) + lane
   const int32_t r0l = rows_l[lane], r1l = rows_l[64u + lane];
   const size_t row0 = (size_t)(r0l >= 0 ? r0l : rows_l[0]), row1 = (size_t)(r1l >= 0 ? r1l : rows_l[0]);
-  const uint32_t a_rt = min(rb * 8u + wv, a.nrt - 1u);                    // A codes: row tile wv
-  const uint32_t as_rt = min(rb * 8u + (wv & 1u) * 4u + (lane >> 4), a.nrt - 1u);  // A scales (waves 4, 5)
+  const uint32_t a_rt0 = min(rb * kRowTiles + wv, a.nrt - 1u);       // A codes: row tiles wv, wv + 8
+  const uint32_t a_rt1 = min(rb * kRowTiles + wv + 8u, a.nrt - 1u);
+  const uint32_t as_rt = min(rb * kRowTiles + (wv & 3u) * 4u + (lane >> 4), a.nrt - 1u);  // A scales (waves 0-3)
   auto stage = [&](uint32_t kg, uint32_t p) {
     uint8_t *st = smem + p * kStage;
 #pragma unroll
@@ -118,32 +120,35 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       const uint8_t *src = (term ? a.b.lo : a.b.hi) + ((m & 1) ? browk1 : browk0) + kg * 128u + bchunk;
       __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + (term * kGemmTok * 8u + tg * 64u) * 16u), 16, 0, 0);
     }
-    {  // A codes of row tile wv
-      const bool ok = lane_ok(kg);
-      const uint8_t *src = wexp + (size_t)a_rt * a.nb * 256u + (ok ? kg * 1024u + lane * 16u : 0u);
-      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBData + kBScale + wv * 1024u), 16, 0, 0);
+    {  // A codes of row tiles wv and wv + 8
+      const uint32_t off = lane_ok(kg) ? kg * 1024u + lane * 16u : 0u;
+      __builtin_amdgcn_global_load_lds((const void *)(wexp + (size_t)a_rt0 * a.nb * 256u + off),
+                                       (lds_void *)(st + kBData + kBScale + wv * 1024u), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(wexp + (size_t)a_rt1 * a.nb * 256u + off),
+                                       (lds_void *)(st + kBData + kBScale + (wv + 8u) * 1024u), 16, 0, 0);
     }
-    if (wv < 4u) {  // B scales: term wv / 2, tokens 64 (wv % 2) + lane
-      const uint8_t *src = ((wv >> 1) ? a.b.slo : a.b.shi) + ((wv & 1u) ? row1 : row0) * sq + kg * 4u;
+    if (wv >= 4u) {  // B scales: term (wv - 4) / 2, tokens 64 (wv % 2) + lane
+      const uint32_t term = (wv - 4u) >> 1;
+      const uint8_t *src = (term ? a.b.slo : a.b.shi) + ((wv & 1u) ? row1 : row0) * sq + kg * 4u;
       __builtin_amdgcn_global_load_lds((const void *)src,
-                                       (lds_void *)(st + kBData + ((wv >> 1) * kGemmTok + (wv & 1u) * 64u) * 4u), 4, 0, 0);
-    } else if (wv < 6u) {  // A scales of row tiles 4 (wv - 4) .. +4: 4 bytes per lane
+                                       (lds_void *)(st + kBData + (term * kGemmTok + (wv & 1u) * 64u) * 4u), 4, 0, 0);
+    } else {  // A scales of row tiles 4 wv .. +4: 4 bytes per lane
       const uint32_t g = lane & 15u;  // 4-byte group of the row tile's 64 scale bytes
       const uint8_t *src = sexp + (size_t)as_rt * a.nb * 16u + min(kg * 64u + 4u * g, a.nb * 16u - 4u);
       __builtin_amdgcn_global_load_lds((const void *)src,
-                                       (lds_void *)(st + kBData + kBScale + kAData + (wv - 4u) * 256u), 4, 0, 0);
+                                       (lds_void *)(st + kBData + kBScale + kAData + wv * 256u), 4, 0, 0);
     }
   };
 
-  f32x4_t acc[4][2];
+  f32x4_t acc[4][4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   stage(0, 0);
   stage(min(1u, nkg - 1u), 1);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(5));  // stage 0 landed (this wave issued 5 or 6 after it)
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(7));  // stage 0 landed (this wave issued 7 after it)
   __syncthreads();
   for (uint32_t kg = 0; kg < nkg; ++kg) {
     const uint32_t p = kg % kStages;
@@ -163,8 +168,8 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     }
     const uint8_t *bsc = st + kBData;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
       // lane group q: chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)) of both terms
       const uint32_t sw = (tok >> 1) & 7u;
       const uint8_t *r = st + tok * 128u;
@@ -182,26 +187,26 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, acc[rt][tt], 4, 0, 0, sa[rt], 0, sbl);
       }
     }
-    // this wave issued 5 or 6 instructions for stage kg + 2 after stage kg + 1's: wait until at
-    // most 5 are outstanding (stage kg + 1 landed; an over-wait of one for waves that issued 6)
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(5));
+    // this wave issued 7 instructions for stage kg + 2 after stage kg + 1's: stage kg + 1 landed
+    // once at most 7 are outstanding
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(7));
     __syncthreads();
   }
 
   // ---- epilogue
   if constexpr (GATE_UP) {
-    // wave wr owns features rb*64 + wr*32 .. +32: one MX block per token.  Lane (q, j) holds
+    // wave wr owns features rb*128 + wr*32 .. +32: one MX block per token.  Lane (q, j) holds
     // features 8 rt + 2 q + {0, 1} (interleaved gate/linear row pairs) of its token columns.
-    const uint32_t fb = rb * 64u + wr * 32u;
+    const uint32_t fb = rb * (kGemmRows / 2u) + wr * 32u;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
       float o[8];
       float amax = 0.0f;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        const uint32_t r0 = rb * 128u + wr * 64u + (uint32_t)rt * 16u + 4u * q;  // W1 row
-        const bool rv = rb * 8u + wr * 4u + (uint32_t)rt < a.nrt;
+        const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;  // W1 row
+        const bool rv = rb * kRowTiles + wr * 4u + (uint32_t)rt < a.nrt;
         const f32x4_t bb = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
         const uint32_t f0 = fb + (uint32_t)rt * 8u + 2u * q;
         float v0 = swiglu_clamp_f(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1], a.alpha, a.limit);
@@ -246,7 +251,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     }
     // zero the K padding of the act rows beyond the last row block's features
     if (rb + 1u == a.nrb) {
-      const uint32_t f_end = a.nrb * 64u, padb = a.act.kq - f_end;  // multiple of 32
+      const uint32_t f_end = a.nrb * (kGemmRows / 2u), padb = a.act.kq - f_end;  // multiple of 32
       for (uint32_t i = threadIdx.x; i < ntok * padb; i += blockDim.x) {
         const uint32_t tk = i / padb, c = i - tk * padb;
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tk));
@@ -261,14 +266,14 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   } else {
     // token-major slot rows t * topk + p, expert bias b2 added once
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const uint32_t tok = wc * 32u + (uint32_t)tt * 16u + i16;
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
       if (tok >= ntok) continue;
       float *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        if (rb * 8u + wr * 4u + (uint32_t)rt >= a.nrt) continue;
-        const uint32_t r0 = rb * 128u + wr * 64u + (uint32_t)rt * 16u + 4u * q;
+        if (rb * kRowTiles + wr * 4u + (uint32_t)rt >= a.nrt) continue;
+        const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
         const f32x4_t bb = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + r0);
         if (r0 + 3u < a.out_rows) {
           *(float4 *)(orow + r0) = make_float4(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1],

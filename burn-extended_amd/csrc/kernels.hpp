@@ -122,7 +122,7 @@ constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 // segment is cut into tiles of kGemmTok routed tokens; a workgroup computes kGemmRows weight
 // rows x one token tile with the block-scaled MFMA (MXFP4 weights x two-term MXFP8 activations).
 constexpr uint32_t kGemmTok = 128;
-constexpr uint32_t kGemmRows = 128;
+constexpr uint32_t kGemmRows = 256;
 struct GemmArgs {
   const uint8_t *wb, *ws;  // tiled MXFP4 layout (as GemvArgs)
   uint64_t wb_estride, ws_estride;
