@@ -2,6 +2,8 @@
 //
 // router_kernel     RmsNorm + router logits, parallel over token blocks x expert groups
 //                   replaces src/moe/mod.rs:109-110 (Burn RmsNorm / Linear)
+// router_rows       the same for prefill batches: one wave per few tokens, rows in registers,
+//                   also writes the two-term MXFP8 rows of the grouped GEMM
 // topk_kernel       top-k + softmax over the selected logits, one wave per token
 //                   replaces src/moe/mod.rs:271-276 (topk_with_indices, max/exp/sum/div)
 // dispatch_kernel   histogram / exclusive scan / stable scatter into expert segments
@@ -99,6 +101,35 @@ __device__ __forceinline__ void wave_sum_butterfly_n(float (&v)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = v[i] + __shfl_xor(v[i], off, 64);
   }
+}
+
+// The same sums as wave_sum_butterfly_n, valid in lane 0 only: the xor-32 and xor-16 levels by
+// permlane swaps, xor 8 by a row rotation (exact), and the xor-4/2/1 levels by a row rotation and
+// quad permutations that pair lane l < 4 with l ^ 4, l ^ 2, l ^ 1 -- every addition lane 0's
+// chain depends on adds the same two values as the butterfly's.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_to_lane0_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+    v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+    v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x128>(v[i]);  // row_ror:8
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x124>(v[i]);  // row_ror:4
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x4E>(v[i]);   // quad_perm [2,3,0,1]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0xB1>(v[i]);   // quad_perm [1,0,3,2]
 }
 
 template <typename XT, typename WT, bool VEC>
@@ -292,6 +323,223 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     const float r = a.apply_norm ? rr[lane] : 1.0f;
     a.logits[(size_t)t * E + e0] = (a.apply_norm ? v0 / r : v0) + a.rb[e0];
     if (has1) a.logits[(size_t)t * E + e1] = (a.apply_norm ? v1 / r : v1) + a.rb[e1];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Prefill router (D % 8 == 0, D, Dp and the MXFP8 row length <= 512 * kFrontChunks, 16-byte
+// aligned rows).  Workgroup of kRowsThreads: wave w holds tokens 2 (8 b + w) .. +2 in registers
+// (f32); the router rows pass through LDS as f32 in stages of kRowsExperts experts (double
+// buffered, filled by all threads, one barrier per stage), so each row is converted once per
+// workgroup and read by every wave from LDS.  LDS row layout: element 512 i + 8 l + j at
+// 512 i + 256 (j / 4) + 4 l + j % 4, so lane l's two float4 of its chunk are conflict-free.
+// Same fixed reduction order and formulas as router_kernel (lane l owns chunks c = 512 i + 8 l + j,
+// fmaf over i then j, xor butterfly; logit = dot / r + b): the logits, r and the written rows
+// equal router_kernel's bit for bit.  The two-term MXFP8 rows come from the registers: a 32-value
+// block is the 8-value chunks of lanes 4 b .. 4 b + 3, its maxima taken over those four lanes.
+// ---------------------------------------------------------------------------------------------
+constexpr int kRowsTokens = 2;     // tokens per wave
+constexpr int kRowsExperts = 4;    // experts per LDS stage
+constexpr uint32_t kRowsSpan = 512u * kFrontChunks;  // f32 LDS row stride
+size_t router_rows_lds_bytes() { return sizeof(float) * (2u * kRowsExperts * kRowsSpan + kMaxExperts); }
+
+template <typename XT, typename WT>
+__global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a) {
+  constexpr int T = kRowsTokens, G = kRowsExperts, RC = kFrontChunks;
+  constexpr uint32_t FC = (G * kRowsSpan / 8u + kRowsThreads - 1u) / kRowsThreads;  // fill chunks per thread
+  extern __shared__ __align__(16) float wls[];  // [2][G][kRowsSpan], then rb [E]
+  float *rbl = wls + 2u * G * kRowsSpan;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t t0 = (blockIdx.x * (kRowsThreads / 64u) + (threadIdx.x >> 6)) * (uint32_t)T;
+  const bool active = t0 < a.n;  // wave-uniform; inactive waves still fill and meet the barriers
+  const uint32_t D = a.D, E = a.E, cpr = D / 8u;  // chunks per router row
+  const XT *x = (const XT *)a.x;
+  const WT *rw = (const WT *)a.rw;
+  const uint32_t nt = active ? min((uint32_t)T, a.n - t0) : 0u;
+  const uint32_t nstage = (E + G - 1u) / G;
+
+  // stage fill: chunk f = threadIdx.x + kRowsThreads m of a stage is chunk ch = f % cpr (= 64 i + l)
+  // of the stage's expert row k = f / cpr
+  uint32_t fk[FC], fsrc[FC], fdst[FC];
+#pragma unroll
+  for (uint32_t m = 0; m < FC; ++m) {
+    const uint32_t f = threadIdx.x + kRowsThreads * m, k = f / cpr, ch = f - k * cpr;
+    fk[m] = k;
+    fsrc[m] = k * D + ch * 8u;
+    fdst[m] = k * kRowsSpan + (ch >> 6) * 512u + (ch & 63u) * 4u;
+  }
+  Chunk8<WT> fr[FC];
+  auto fill_load = [&](uint32_t st) {
+#pragma unroll
+    for (uint32_t m = 0; m < FC; ++m)
+      if (fk[m] < (uint32_t)G && st * G + fk[m] < E) chunk_load(fr[m], rw + (size_t)st * G * D + fsrc[m]);
+  };
+  auto fill_store = [&](uint32_t st, uint32_t buf) {
+#pragma unroll
+    for (uint32_t m = 0; m < FC; ++m) {
+      if (fk[m] < (uint32_t)G && st * G + fk[m] < E) {
+        float v[8];
+        chunk_vals(fr[m], v);
+        float *d = wls + buf * G * kRowsSpan + fdst[m];
+        *(float4 *)d = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4 *)(d + 256) = make_float4(v[4], v[5], v[6], v[7]);
+      }
+    }
+  };
+  fill_load(0);
+  for (uint32_t e = threadIdx.x; e < E; e += kRowsThreads) rbl[e] = a.rb[e];
+  // zeros at the chunk positions beyond D of every row (never filled): the dot loop runs over
+  // all RC chunks, and fmaf(0, 0, acc) == acc for the +0-started sums
+  for (uint32_t f = threadIdx.x; f < 2u * G * (RC * 64u - cpr); f += kRowsThreads) {
+    const uint32_t row = f / (RC * 64u - cpr), ch = cpr + (f - row * (RC * 64u - cpr));
+    float *d = wls + row * kRowsSpan + (ch >> 6) * 512u + (ch & 63u) * 4u;
+    *(float4 *)d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    *(float4 *)(d + 256) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+
+  // this wave's token rows as f32 (zeros beyond D)
+  float xv[T][RC][8];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const uint32_t c0 = 512u * i + 8u * lane;
+      Chunk8<XT> c;
+      if (active && c0 < D) {
+        chunk_load(c, x + (size_t)(t0 + min((uint32_t)t, nt - 1u)) * D + c0);
+        chunk_vals(c, xv[t][i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[t][i][j] = 0.0f;
+      }
+    }
+
+  // r per token
+  float r[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) r[t] = 1.0f;
+  if (a.apply_norm) {
+    float ss[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      ss[t] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < RC; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss[t] = fmaf(xv[t][i][j], xv[t][i][j], ss[t]);
+    }
+    wave_sum_to_lane0_n<T>(ss);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      r[t] = sqrtf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss[t]), 0)) / (float)D + a.eps);
+      if (a.rms && lane == 0 && (uint32_t)t < nt) a.rms[t0 + t] = r[t];
+    }
+  }
+
+  // normalised rows xn = x * (1/r) * gamma (x without RmsNorm), zero padded to Dp, and their
+  // two-term MXFP8 form zero padded to the K-group length; written before the dot products so
+  // the stores drain meanwhile
+  if (active && (a.xn || a.xq.hi)) {
+    const uint32_t nbk = a.xq.kq >> 5;
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const uint32_t c0 = 512u * i + 8u * lane;
+      if (512u * i >= max(a.xn ? a.Dp : 0u, a.xq.hi ? a.xq.kq : 0u)) break;  // wave-uniform
+      float g[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[j] = 1.0f;
+      if (a.apply_norm && c0 < D) {
+        const float4 g0 = *(const float4 *)(a.gamma + c0), g1 = *(const float4 *)(a.gamma + c0 + 4);
+        g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w; g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float ir = a.apply_norm ? 1.0f / r[t] : 1.0f;
+        float u[8];  // zeros beyond D: xv is zero there and gamma one
+#pragma unroll
+        for (int j = 0; j < 8; ++j) u[j] = a.apply_norm ? (xv[t][i][j] * ir) * g[j] : xv[t][i][j];
+        const size_t row = t0 + (uint32_t)t;
+        const bool tv = (uint32_t)t < nt;
+        if (a.xn && tv && c0 < a.Dp) store8((XT *)a.xn + row * a.Dp + c0, u);
+        if (a.xq.hi && 512u * i < a.xq.kq) {  // wave-uniform
+          float amax = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(u[j]));
+          amax = fmaxf(amax, dpp_mov<0xB1>(amax));  // lanes 4 b .. 4 b + 3 hold block b
+          amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+          const uint32_t sbh = mx8_scale_byte(amax);
+          const float ih = sbh ? mx8_inv_scale(sbh) : 0.0f, sh = e8m0_to_f32(sbh);
+          uint32_t ch[4];
+          float res[8], rmax = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            ch[k] = f32x2_to_fp8x2(u[2 * k] * ih, u[2 * k + 1] * ih);
+            res[2 * k] = u[2 * k] - fp8_to_f32<0>(ch[k]) * sh;
+            res[2 * k + 1] = u[2 * k + 1] - fp8_to_f32<1>(ch[k]) * sh;
+            rmax = fmaxf(rmax, fmaxf(fabsf(res[2 * k]), fabsf(res[2 * k + 1])));
+          }
+          rmax = fmaxf(rmax, dpp_mov<0xB1>(rmax));
+          rmax = fmaxf(rmax, dpp_mov<0x4E>(rmax));
+          const uint32_t sbl = mx8_scale_byte(rmax);
+          const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
+          if (tv && c0 < a.xq.kq) {
+            uint32_t cl[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cl[k] = f32x2_to_fp8x2(res[2 * k] * il, res[2 * k + 1] * il);
+            *(uint2 *)(a.xq.hi + row * a.xq.kq + c0) = make_uint2(ch[0] | (ch[1] << 16), ch[2] | (ch[3] << 16));
+            *(uint2 *)(a.xq.lo + row * a.xq.kq + c0) = make_uint2(cl[0] | (cl[1] << 16), cl[2] | (cl[3] << 16));
+            if ((lane & 3u) == 0u) {
+              a.xq.shi[row * nbk + (c0 >> 5)] = (uint8_t)sbh;
+              a.xq.slo[row * nbk + (c0 >> 5)] = (uint8_t)sbl;
+            }
+          }
+        }
+      }
+    }
+  }
+
+  fill_store(0, 0);
+  __syncthreads();
+
+  // dot products, G experts per stage; lane q < G * T finishes (expert st * G + q / T, token q % T)
+  for (uint32_t st = 0; st < nstage; ++st) {
+    const uint32_t buf = st & 1u;
+    if (st + 1u < nstage) fill_load(st + 1u);
+    if (active) {
+      float acc[G * T];
+#pragma unroll
+      for (int q = 0; q < G * T; ++q) acc[q] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const float *wrow = wls + (buf * G + k) * kRowsSpan + lane * 4u;
+#pragma unroll
+        for (int i = 0; i < RC; ++i) {
+          const float4 w0 = *(const float4 *)(wrow + 512u * i), w1 = *(const float4 *)(wrow + 512u * i + 256u);
+          const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[k * T + t] = fmaf(xv[t][i][j], w[j], acc[k * T + t]);
+        }
+      }
+      wave_sum_to_lane0_n<G * T>(acc);
+      float v = 0.0f, rq = r[0];
+#pragma unroll
+      for (int q = 0; q < G * T; ++q) {
+        const float aq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc[q]), 0));
+        if (lane == (uint32_t)q) {
+          v = aq;
+          rq = r[q % T];
+        }
+      }
+      const uint32_t e = st * G + lane / T, t = lane % T;
+      if (lane < (uint32_t)(G * T) && e < E && t < nt)
+        a.logits[(size_t)(t0 + t) * E + e] = (a.apply_norm ? v / rq : v) + rbl[e];
+    }
+    if (st + 1u < nstage) {
+      fill_store(st + 1u, buf ^ 1u);
+      __syncthreads();
+    }
   }
 }
 
@@ -1068,6 +1316,10 @@ hipError_t configure_kernels() {
   BX_ATTR((router_kernel<float, uint16_t, false>));
   BX_ATTR((router_kernel<uint16_t, float, false>));
   BX_ATTR((router_kernel<uint16_t, uint16_t, false>));
+  BX_ATTR((router_rows_kernel<float, float>));
+  BX_ATTR((router_rows_kernel<float, uint16_t>));
+  BX_ATTR((router_rows_kernel<uint16_t, float>));
+  BX_ATTR((router_rows_kernel<uint16_t, uint16_t>));
   BX_ATTR(topk_kernel);
   BX_ATTR(dispatch_kernel);
   BX_ATTR((expert_gemv_kernel<1, true, uint16_t>));
@@ -1086,6 +1338,23 @@ static void router_launch(const RouterArgs &a, bool vec, dim3 grid, size_t lds, 
     router_kernel<XT, WT, true><<<grid, dim3(kRouterThreads), lds, s>>>(a);
   else
     router_kernel<XT, WT, false><<<grid, dim3(kRouterThreads), lds, s>>>(a);
+}
+
+hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, hipStream_t s) {
+  if (a.D % 8u != 0 || a.D > kRowsSpan || (a.xn && a.Dp > kRowsSpan) || (a.xq.hi && a.xq.kq > kRowsSpan))
+    return hipErrorInvalidValue;
+  const uint32_t tpb = kRowsTokens * (kRowsThreads / 64u);
+  const dim3 grid((a.n + tpb - 1) / tpb), block(kRowsThreads);
+  const size_t lds = router_rows_lds_bytes();
+  if (x_bf16 && w_bf16)
+    router_rows_kernel<uint16_t, uint16_t><<<grid, block, lds, s>>>(a);
+  else if (x_bf16)
+    router_rows_kernel<uint16_t, float><<<grid, block, lds, s>>>(a);
+  else if (w_bf16)
+    router_rows_kernel<float, uint16_t><<<grid, block, lds, s>>>(a);
+  else
+    router_rows_kernel<float, float><<<grid, block, lds, s>>>(a);
+  return hipGetLastError();
 }
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s) {

@@ -176,6 +176,8 @@ __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, 
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
 constexpr uint32_t kRouterThreads = 256;
+constexpr uint32_t kRouterRowsMinTokens = 512;  // router_rows_kernel from this batch size on
+constexpr uint32_t kRowsThreads = 512;
 constexpr uint32_t kTopkThreads = 512;
 constexpr uint32_t kDispatchThreads = 1024;
 constexpr uint32_t kGemvThreads = 256;
@@ -184,6 +186,9 @@ constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
+// router_rows_kernel: D % 8 == 0 and D, Dp (with xn) and xq.kq (with xq) <= 512 * kFrontChunks,
+// 16-byte aligned x and router rows
+hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);
 hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
 hipError_t launch_topk(const TopkArgs &a, hipStream_t s);

@@ -371,7 +371,8 @@ burnext_status check_launch(hipError_t e, const char *what) {
   return BURNEXT_OK;
 }
 
-// Router logits (and r per token when normalising) into the workspace.
+// Router logits (and r per token when normalising) into the workspace: router_rows_kernel for
+// batches of kRouterRowsMinTokens tokens or more whose rows fit its registers, router_kernel else.
 burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
                           float *logits, void *xn, hipStream_t s, const QRows *xq = nullptr) {
   RouterArgs ra{};
@@ -394,8 +395,12 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
   ra.eps = L->eps;
   ra.apply_norm = norm ? 1 : 0;
   const bool vec = L->D % 8 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)ra.rw & 15u) == 0;
+  const uint32_t lim = 512u * kFrontChunks;
+  const bool rows = vec && n >= kRouterRowsMinTokens && L->D <= lim && (!xn || L->Dp <= lim) &&
+                    (!xq || !xq->hi || xq->kq <= lim);
   ProfScope ps(L, s, kKRouter);
-  return check_launch(launch_router(ra, x_bf16, w_bf16, vec, s), "router kernel launch");
+  return check_launch(rows ? launch_router_rows(ra, x_bf16, w_bf16, s) : launch_router(ra, x_bf16, w_bf16, vec, s),
+                      "router kernel launch");
 }
 
 burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *logits,

@@ -93,6 +93,12 @@ ROUTE_CASES = [
     (2880, 128, 4, 64, "bf16", True, False),
     (2880, 128, 4, 1, "f32", True, True),
     (200, 7, 3, 37, "f32", True, False),
+    # prefill-sized batches (token rows held in registers)
+    (2880, 32, 4, 1027, "bf16", True, False),
+    (2880, 32, 4, 1024, "bf16", True, True),
+    (2880, 128, 4, 512, "bf16", False, False),
+    (1000, 7, 3, 600, "f32", True, True),
+    (200, 9, 2, 513, "f32", False, False),
 ]
 
 
