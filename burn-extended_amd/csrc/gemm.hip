@@ -19,6 +19,7 @@
 namespace burnext {
 
 typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 // One pipeline stage (one 128-wide K-group) in LDS:
@@ -39,6 +40,21 @@ constexpr uint32_t kWaves = 8;
 typedef __attribute__((address_space(3))) void lds_void;
 // s_waitcnt with vmcnt(n) only (expcnt and lgkmcnt left at their maxima), n < 16
 constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8); }
+// s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima)
+constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
+
+// Barrier of the stage ring.  Each wave has already waited (vmcnt) for its own direct-to-LDS
+// loads of the stage the others read next; its LDS reads are complete (lgkmcnt(0)) before it
+// arrives, so a slot refilled after the barrier has no pending readers.  Loads of later stages
+// stay in flight: __syncthreads() would wait for every outstanding load (its fence covers the
+// direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
+// accesses across.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 }  // namespace
 
 size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64; }
@@ -146,52 +162,77 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  stage(0, 0);
-  stage(min(1u, nkg - 1u), 1);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(7));  // stage 0 landed (this wave issued 7 after it)
-  __syncthreads();
-  for (uint32_t kg = 0; kg < nkg; ++kg) {
-    const uint32_t p = kg % kStages;
-    stage(min(kg + 2u, nkg - 1u), (kg + 2u) % kStages);  // the stage every wave left at the last barrier
-    const uint8_t *st = smem + p * kStage;
-    const bool ok = lane_ok(kg);
-    i32x8_t A[4];
+  // MFMA operands: the A operands (row tiles) of a K-group, and the B operands of one token tile
+  struct AFrag {
+    i32x4_t A[4];
     int32_t sa[4];
+  };
+  struct BFrag {
+    i32x8_t Bh, Bl;
+    int32_t sbh, sbl;
+  };
+  const i32x4_t z4 = {0, 0, 0, 0};
+  auto read_a = [&](uint32_t kg, const uint8_t *st, AFrag &f) {
+    const bool ok = lane_ok(kg);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const uint32_t rtl = wr * 4u + (uint32_t)rt;
-      const uint4 w4 = *(const uint4 *)(st + kBData + kBScale + (rtl * 64u + lane) * 16u);
-      const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-      const uint4 v = ok ? w4 : z;
-      A[rt] = i32x8_t{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w, 0, 0, 0, 0};
-      sa[rt] = ok ? (int32_t)st[kBData + kBScale + kAData + rtl * 64u + lane] : 127;
+      const i32x4_t w4 = *(const i32x4_t *)(st + kBData + kBScale + (rtl * 64u + lane) * 16u);
+      f.A[rt] = ok ? w4 : z4;
+      f.sa[rt] = ok ? (int32_t)st[kBData + kBScale + kAData + rtl * 64u + lane] : 127;
     }
-    const uint8_t *bsc = st + kBData;
+  };
+  auto read_b = [&](const uint8_t *st, int tt, BFrag &f) {
+    const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+    // lane group q: chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)) of both terms
+    const uint32_t sw = (tok >> 1) & 7u;
+    const uint8_t *r = st + tok * 128u;
+    const uint32_t s1 = (q ^ sw) * 16u, s2 = ((4u + q) ^ sw) * 16u;
+    const i32x4_t h0 = *(const i32x4_t *)(r + s1), h1 = *(const i32x4_t *)(r + s2);
+    const i32x4_t l0 = *(const i32x4_t *)(r + kGemmTok * 128u + s1), l1 = *(const i32x4_t *)(r + kGemmTok * 128u + s2);
+    f.Bh = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    f.Bl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+    f.sbh = st[kBData + tok * 4u + q];
+    f.sbl = st[kBData + (kGemmTok + tok) * 4u + q];
+  };
+  auto mma = [&](const AFrag &fa, const BFrag &fb, int tt) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
-      // lane group q: chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)) of both terms
-      const uint32_t sw = (tok >> 1) & 7u;
-      const uint8_t *r = st + tok * 128u;
-      const uint32_t s1 = (q ^ sw) * 16u, s2 = ((4u + q) ^ sw) * 16u;
-      const uint4 h0 = *(const uint4 *)(r + s1), h1 = *(const uint4 *)(r + s2);
-      const uint4 l0 = *(const uint4 *)(r + kGemmTok * 128u + s1), l1 = *(const uint4 *)(r + kGemmTok * 128u + s2);
-      const i32x8_t Bh = {(int32_t)h0.x, (int32_t)h0.y, (int32_t)h0.z, (int32_t)h0.w,
-                          (int32_t)h1.x, (int32_t)h1.y, (int32_t)h1.z, (int32_t)h1.w};
-      const i32x8_t Bl = {(int32_t)l0.x, (int32_t)l0.y, (int32_t)l0.z, (int32_t)l0.w,
-                          (int32_t)l1.x, (int32_t)l1.y, (int32_t)l1.z, (int32_t)l1.w};
-      const int32_t sbh = bsc[tok * 4u + q], sbl = bsc[(kGemmTok + tok) * 4u + q];
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bh, acc[rt][tt], 4, 0, 0, sa[rt], 0, sbh);
-        acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, acc[rt][tt], 4, 0, 0, sa[rt], 0, sbl);
-      }
+    for (int rt = 0; rt < 4; ++rt) {
+      const i32x8_t A8 = __builtin_shufflevector(fa.A[rt], z4, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bh, acc[rt][tt], 4, 0, 0, fa.sa[rt], 0, fb.sbh);
     }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const i32x8_t A8 = __builtin_shufflevector(fa.A[rt], z4, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bl, acc[rt][tt], 4, 0, 0, fa.sa[rt], 0, fb.sbl);
+    }
+  };
+
+  stage(0, 0);
+  stage(min(1u, nkg - 1u), 1);
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(7));  // stage 0 landed (this wave issued 7 after it)
+  ring_barrier();
+  for (uint32_t kg = 0; kg < nkg; ++kg) {
+    stage(min(kg + 2u, nkg - 1u), (kg + 2u) % kStages);  // the stage every wave left at the last barrier
+    const uint8_t *st = smem + (kg % kStages) * kStage;
+    // token tile tt + 1's operands are read while tile tt's MFMAs run
+    AFrag fa;
+    BFrag b0, b1;
+    read_a(kg, st, fa);
+    read_b(st, 0, b0);
+    read_b(st, 1, b1);
+    mma(fa, b0, 0);
+    read_b(st, 2, b0);
+    mma(fa, b1, 1);
+    read_b(st, 3, b1);
+    mma(fa, b0, 2);
+    mma(fa, b1, 3);
     // this wave issued 7 instructions for stage kg + 2 after stage kg + 1's: stage kg + 1 landed
     // once at most 7 are outstanding
     __builtin_amdgcn_s_waitcnt(vmcnt_only(7));
-    __syncthreads();
+    ring_barrier();
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the trailing reloads have landed
 
   // ---- epilogue
   if constexpr (GATE_UP) {
