@@ -709,6 +709,107 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) {
   return sizeof(int32_t) * ((size_t)E * (4 + 2 * (threads / 32)) + 4);
 }
 
+// Dispatch of a large batch in two launches over chunks of kDispatchChunk tokens (workgroup c owns
+// tokens [c * kDispatchChunk, +kDispatchChunk), thread = token).  dispatch_count_kernel: the
+// per-expert entry counts of each chunk (LDS atomics: order-independent).  dispatch_wide_kernel:
+// totals and earlier-chunk counts from those; an entry's segment position is seg_off[e] + (entries
+// of e in earlier chunks) + (rank among this chunk's tokens choosing e, from a per-expert token
+// bitmap).  Its workgroup 0 writes the segment offsets, token-tile prefix, active list, records
+// and GEMV maps.  Results equal block_dispatch's.
+__global__ __launch_bounds__(kDispatchChunk) void dispatch_count_kernel(DispatchArgs a) {
+  __shared__ int32_t cnt[kMaxExperts];
+  const uint32_t tid = threadIdx.x, E = a.E, K = a.K;
+  for (uint32_t e = tid; e < E; e += kDispatchChunk) cnt[e] = 0;
+  __syncthreads();
+  const uint32_t t = blockIdx.x * kDispatchChunk + tid;
+  if (t < a.n) {
+    for (uint32_t p = 0; p < K; ++p) {
+      const int32_t e = a.topk_idx[(size_t)t * K + p];
+      if (e >= 0 && (uint32_t)e < E) atomicAdd(&cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < E; e += kDispatchChunk) a.chunk_cnt[(size_t)blockIdx.x * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchArgs a) {
+  constexpr uint32_t W = kDispatchChunk / 32u;  // bitmap words per expert
+  __shared__ int32_t call[kMaxExperts], cbef[kMaxExperts], segs[kMaxExperts], aidx[kMaxExperts], base[kMaxExperts];
+  __shared__ uint32_t bm[kMaxExperts * W];
+  __shared__ int32_t na_l;
+  const uint32_t tid = threadIdx.x, c = blockIdx.x, E = a.E, K = a.K, n = a.n;
+  const uint32_t t = c * kDispatchChunk + tid;
+  const uint32_t nchunk = gridDim.x;
+  for (uint32_t e = tid; e < E; e += kDispatchChunk) {
+    int32_t all = 0, bef = 0;
+    for (uint32_t c2 = 0; c2 < nchunk; ++c2) {
+      const int32_t v = a.chunk_cnt[(size_t)c2 * E + e];
+      all += v;
+      bef += c2 < c ? v : 0;
+    }
+    call[e] = all;
+    cbef[e] = bef;
+  }
+  for (uint32_t i = tid; i < E * W; i += kDispatchChunk) bm[i] = 0u;
+  __syncthreads();
+  if (t < n) {
+    for (uint32_t p = 0; p < K; ++p) {
+      const int32_t e = a.topk_idx[(size_t)t * K + p];
+      if (e >= 0 && (uint32_t)e < E) atomicOr(&bm[e * W + (tid >> 5)], 1u << (tid & 31u));
+    }
+  }
+  __syncthreads();
+  // exclusive scan over experts (each expert's thread sums the counts below it)
+  for (uint32_t e = tid; e < E; e += kDispatchChunk) {
+    int32_t off = 0, ra = 0, toff = 0;
+    for (uint32_t e2 = 0; e2 < e; ++e2) {
+      off += call[e2];
+      ra += call[e2] > 0;
+      toff += (call[e2] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
+    }
+    segs[e] = off;
+    aidx[e] = ra;
+    base[e] = off + cbef[e];
+    if (c == 0) {
+      if (a.tile_off) a.tile_off[e] = toff;
+      a.seg_off[e] = off;
+      if (call[e] > 0) {
+        a.active[ra] = (int32_t)e;
+        a.exrec[ra * kRecWords + 0] = (int32_t)e;
+        a.exrec[ra * kRecWords + 1] = off;
+        a.exrec[ra * kRecWords + 2] = call[e];
+      }
+      if (e + 1 == E) {
+        a.seg_off[E] = off + call[e];
+        if (a.tile_off) a.tile_off[E] = toff + (call[e] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
+        const int32_t na = ra + (call[e] > 0);
+        *a.num_active = na;
+        na_l = na;
+        for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) a.active[e3] = -1;
+      }
+    }
+  }
+  __syncthreads();
+  if (c == 0) write_gemv_maps(a.maps, (uint32_t)na_l);
+  if (t >= n) return;
+  const uint32_t wi = tid >> 5, bit = tid & 31u;
+  for (uint32_t p = 0; p < K; ++p) {
+    const int32_t e = a.topk_idx[(size_t)t * K + p];
+    if (e < 0 || (uint32_t)e >= E) continue;
+    int32_t r = __popc(bm[e * W + wi] & ((1u << bit) - 1u));
+    for (uint32_t w2 = 0; w2 < wi; ++w2) r += __popc(bm[e * W + w2]);
+    const int32_t pos = base[e] + r;
+    const int32_t slot = (int32_t)(t * K + p);
+    a.perm[pos] = slot;
+    a.pos_of[slot] = pos;
+    const int32_t j = pos - segs[e];
+    if (j < (int32_t)kRecTokens) {
+      a.exrec[aidx[e] * kRecWords + 4 + j] = (int32_t)t;
+      a.exrec[aidx[e] * kRecWords + 4 + kRecTokens + j] = slot;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec, a.maps,
@@ -1408,7 +1509,14 @@ hipError_t launch_topk(const TopkArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
-  dispatch_kernel<<<dim3(1), dim3(kDispatchThreads), dispatch_lds_bytes(a.E, kDispatchThreads), s>>>(a);
+  if (a.n >= kDispatchWideMinTokens) {
+    if (!a.chunk_cnt) return hipErrorInvalidValue;
+    const dim3 grid((a.n + kDispatchChunk - 1) / kDispatchChunk), block(kDispatchChunk);
+    dispatch_count_kernel<<<grid, block, 0, s>>>(a);
+    dispatch_wide_kernel<<<grid, block, 0, s>>>(a);
+  } else {
+    dispatch_kernel<<<dim3(1), dim3(kDispatchThreads), dispatch_lds_bytes(a.E, kDispatchThreads), s>>>(a);
+  }
   return hipGetLastError();
 }
 

@@ -62,6 +62,7 @@ struct DispatchArgs {
   int32_t *exrec;     // [E, kRecWords]
   GemvMaps maps;      // map == null: none written
   int32_t *tile_off;  // [E + 1] prefix of ceil(M_e / kGemmTok), or null
+  int32_t *chunk_cnt; // [ceil(n / kDispatchChunk), E] scratch of the multi-workgroup dispatch
   uint32_t n, K, E;
 };
 
@@ -180,6 +181,8 @@ constexpr uint32_t kRouterRowsMinTokens = 512;  // router_rows_kernel from this 
 constexpr uint32_t kRowsThreads = 512;
 constexpr uint32_t kTopkThreads = 512;
 constexpr uint32_t kDispatchThreads = 1024;
+constexpr uint32_t kDispatchChunk = 256;           // dispatch_wide_kernel: tokens per workgroup
+constexpr uint32_t kDispatchWideMinTokens = 1024;  // dispatch_wide_kernel from this batch size on
 constexpr uint32_t kGemvThreads = 256;
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;

@@ -242,7 +242,7 @@ uint64_t gemv_max_grid(const burnext_moe_layer &L) { return std::max<uint64_t>(L
 
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, wgmap, perm, pos_of, xn, act, ypart, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, wgmap, perm, pos_of, xn, act, ypart, dcnt, total;
   uint64_t tile_off, xq[4], aq[4];  // grouped-GEMM path: tile prefix, xq / act rows (hi lo shi slo)
   bool gemm;                        // the grouped-GEMM regions are present
 };
@@ -289,6 +289,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[3] = take(nk * ka / 32);
   }
   w.ypart = take(nk * L.Dp * 4);
+  w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   w.total = off;
   return w;
 }
@@ -304,6 +305,7 @@ struct WsPtrs {
   void *xn;
   float *act, *ypart;
   int32_t *tile_off;
+  int32_t *dcnt;  // per-chunk expert counts of the multi-workgroup dispatch
   QRows xq, aq;
 };
 
@@ -329,6 +331,7 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
   p.ypart = (float *)(b + w.ypart);
+  p.dcnt = (int32_t *)(b + w.dcnt);
   return p;
 }
 
@@ -437,8 +440,9 @@ burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, i
 
 burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
                             int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec,
-                            const GemvMaps &maps, hipStream_t s, int32_t *tile_off = nullptr) {
+                            const GemvMaps &maps, int32_t *chunk_cnt, hipStream_t s, int32_t *tile_off = nullptr) {
   DispatchArgs da{};
+  da.chunk_cnt = chunk_cnt;
   da.maps = maps;
   da.tile_off = tile_off;
   da.exrec = exrec;
@@ -512,7 +516,7 @@ burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64
   burnext_status st = run_router(L, x, xb, n, norm, p.rms, p.logits, nullptr, s, &p.xq);
   if (st == BURNEXT_OK) st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
   if (st == BURNEXT_OK)
-    st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, s,
+    st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, p.dcnt, s,
                       p.tile_off);
   if (st != BURNEXT_OK) return st;
   const uint64_t nk = n * L->K;
@@ -738,7 +742,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
-      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, maps, s);
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, maps, p.dcnt, s);
   }
   if (st != BURNEXT_OK) return st;
 
@@ -820,7 +824,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, s);
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, p.dcnt, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 

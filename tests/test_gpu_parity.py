@@ -138,7 +138,8 @@ def test_route_ties_lower_index(M):
 # ---------------------------------------------------------------------------------------------
 # dispatch
 # ---------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("n,E,K", [(8, 32, 4), (1, 4, 4), (4096, 32, 4), (3000, 128, 4), (1500, 7, 2)])
+@pytest.mark.parametrize("n,E,K", [(8, 32, 4), (1, 4, 4), (4096, 32, 4), (3000, 128, 4), (1500, 7, 2),
+                                   (1023, 32, 4), (1024, 256, 8), (5000, 3, 3)])
 def test_dispatch_matches_oracle(M, oracle, n, E, K):
     from burnext_amd import synth
     rng = np.random.default_rng(n * 7 + E)
@@ -201,6 +202,18 @@ def test_forward_20b_decode_bf16(M, oracle):
     print(f"20b decode bf16: max-abs-rel {err:.3e} (MoE part alone {moe_err:.3e})")
     assert err <= TOL_BF16
     assert moe_err <= TOL_BF16
+
+
+def test_forward_f32_large_batch_gemv_records(M, oracle):
+    """f32 batch above the multi-workgroup dispatch threshold: the expert GEMVs run on the records
+    and segment lists that dispatch wrote (some experts hold more tokens than a record lists)."""
+    from burnext_amd import synth
+    L = _make(synth, 64, 96, 8, 2, seed=6, dtype="f32")
+    x = synth.make_tokens(1100, 64, seed=6, dtype="f32")
+    y, y_ref = _forward_case(M, oracle, L, x, "f32", flags=3)
+    err = oracle.max_abs_rel(y, y_ref)
+    print(f"f32 n=1100: max-abs-rel {err:.3e}")
+    assert err <= TOL_F32
 
 
 def test_forward_20b_f32_activations(M, oracle):
