@@ -84,7 +84,10 @@ def main():
     torch.cuda.set_device(dev)
     bias = synth.zipf_router_bias(E, 1.1, gamma=1.0, seed=0) if wl["zipf"] else None
     data = synth.make_layer(D, F, E, K, seed=0, dtype="bf16", router_bias=bias)
-    layers = [moe.MoeLayer(data, device=dev) for _ in range(max(1, args.copies))]
+    layers = []
+    for i in range(max(1, args.copies)):
+        layers.append(moe.MoeLayer(data, device=dev))
+        print(f"[bench] layer copy {i + 1}/{max(1, args.copies)} resident", file=sys.stderr, flush=True)
     x_np = synth.make_tokens(T, D, seed=0, dtype="bf16")
     x = moe.to_device_x(x_np, "bf16", dev)
     y = torch.empty_like(x)
@@ -183,6 +186,7 @@ def main():
         fl = 6 * T * K * F * D
         out["layer_fp4_mfma_util"] = round(fl / (ms_step * 1e-3) / 1e12 / FP4_PEAK_TFLOPS, 4)
 
+    print(f"[bench] timed {args.steps} steps: {ms_step * 1e3:.1f} us/step", file=sys.stderr, flush=True)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(data, x_np, args.cpu_seconds)
     for L in layers:

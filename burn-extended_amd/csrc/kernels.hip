@@ -549,15 +549,15 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
 // selection, in order.  Softmax over the selected logits: w_p = exp(v_p - v_0) / sum_q
 // exp(v_q - v_0), the sum taken q = 0..K-1 ascending from 0.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void rank_select(const float *lr, uint32_t E, uint32_t K, uint32_t e, int32_t *sel,
-                                            float *selv) {
-  const float v = lr[e];
-  const uint64_t ke = topk_key(v, e);
+// kr: the packed keys topk_key(lr[e], e) of the token's experts
+__device__ __forceinline__ void rank_select(const float *lr, const uint64_t *kr, uint32_t E, uint32_t K, uint32_t e,
+                                            int32_t *sel, float *selv) {
+  const uint64_t ke = kr[e];
   uint32_t rank = 0;
-  for (uint32_t e2 = 0; e2 < E; ++e2) rank += topk_key(lr[e2], e2) > ke ? 1u : 0u;
+  for (uint32_t e2 = 0; e2 < E; ++e2) rank += kr[e2] > ke ? 1u : 0u;
   if (rank < K) {
     sel[rank] = (int32_t)e;
-    selv[rank] = v;
+    selv[rank] = lr[e];
   }
 }
 
@@ -568,9 +568,11 @@ __device__ __forceinline__ float softmax_weight(const float *selv, uint32_t K, u
   return expf(selv[p] - m) / s;
 }
 
-size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads) {
-  return (size_t)(threads / 64) * (sizeof(float) * E + 2 * sizeof(int32_t) * K);
+// per-wave LDS of topk_kernel: keys [E] u64, logits [E], sel [K], selv [K], 8-byte aligned stride
+__host__ __device__ inline size_t topk_wave_bytes(uint32_t E, uint32_t K) {
+  return ((size_t)12 * E + 8 * (size_t)K + 7) / 8 * 8;
 }
+size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads) { return (size_t)(threads / 64) * topk_wave_bytes(E, K); }
 
 // One wave per token; the workgroup's waves work on separate LDS rows, so only wave-level
 // ordering is needed between the phases (block barriers keep it simple and uniform).
@@ -578,15 +580,21 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t t = blockIdx.x * (blockDim.x >> 6) + w;
-  float *lr = (float *)smem + (size_t)w * (a.E + 2 * a.K);
+  // per wave: keys [E] (8-byte aligned first), logits [E], sel [K], selv [K]
+  uint64_t *kr = (uint64_t *)(smem + (size_t)w * topk_wave_bytes(a.E, a.K));
+  float *lr = (float *)(kr + a.E);
   int32_t *sel = (int32_t *)(lr + a.E);
   float *selv = (float *)(sel + a.K);
   const bool live = t < a.n;
   if (live)
-    for (uint32_t e = lane; e < a.E; e += 64) lr[e] = a.logits[(size_t)t * a.E + e];
+    for (uint32_t e = lane; e < a.E; e += 64) {
+      const float v = a.logits[(size_t)t * a.E + e];
+      lr[e] = v;
+      kr[e] = topk_key(v, e);
+    }
   __syncthreads();
   if (live)
-    for (uint32_t e = lane; e < a.E; e += 64) rank_select(lr, a.E, a.K, e, sel, selv);
+    for (uint32_t e = lane; e < a.E; e += 64) rank_select(lr, kr, a.E, a.K, e, sel, selv);
   __syncthreads();
   if (live) {
     for (uint32_t p = lane; p < a.K; p += 64) {
@@ -1477,7 +1485,8 @@ hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec
 
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
   if (a.n == 0 || a.n > kSmallRouteMaxTokens || a.E > kMaxExperts || a.K > kMaxTopK) return hipErrorInvalidValue;
-  const dim3 block(64 * a.n);
+  // at least 8 waves: the work-map writes spread over the whole workgroup
+  const dim3 block(64 * max(a.n, 8u));
   if (a.E <= 64)
     small_route_kernel<1><<<dim3(1), block, 0, s>>>(a);
   else if (a.E <= 128)
