@@ -204,6 +204,17 @@ def test_forward_20b_decode_bf16(M, oracle):
     assert moe_err <= TOL_BF16
 
 
+def test_forward_120b_shape_decode(M, oracle):
+    """120B-shaped layer (E = 128, D = F = 2880, k = 4): 8 tokens on the GEMV path against the oracle."""
+    from burnext_amd import synth
+    L = _make(synth, 2880, 2880, 128, 4, seed=7, dtype="bf16", with_gamma=True)
+    x = synth.make_tokens(8, 2880, seed=7, dtype="bf16")
+    y, y_ref = _forward_case(M, oracle, L, x, "bf16", flags=3)
+    err = oracle.max_abs_rel(y, y_ref)
+    print(f"120b decode: max-abs-rel {err:.3e}")
+    assert err <= TOL_BF16
+
+
 def test_forward_f32_large_batch_gemv_records(M, oracle):
     """f32 batch above the multi-workgroup dispatch threshold: the expert GEMVs run on the records
     and segment lists that dispatch wrote (some experts hold more tokens than a record lists)."""
