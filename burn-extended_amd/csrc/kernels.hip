@@ -848,13 +848,13 @@ struct RouteOut {
 
 template <int J>
 __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                     int8_t (*rank_l)[kMaxExperts], int32_t *na_l);
+                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l);
 
 // Routing of T <= 16 tokens over E <= 64 * J experts from logits lg[t * E + e] (global or LDS) by
 // a workgroup of at least T waves.  Every wave of the workgroup must call it (it has a barrier).
 template <int J>
 __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                 const GemvMaps &maps, int8_t (*rank_l)[kMaxExperts], float (*selv_l)[kMaxTopK],
+                                 const GemvMaps &maps, int8_t (*rank_l)[kSmallRouteMaxTokens], float (*selv_l)[kMaxTopK],
                                  int32_t *na_l) {
   const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
   if (t < T) {
@@ -884,13 +884,14 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
       const uint32_t e = lane + 64u * j;
       if (e >= E) continue;
       const bool sel = rank[j] < K;
-      rank_l[t][e] = sel ? (int8_t)rank[j] : (int8_t)-1;
+      rank_l[e][t] = sel ? (int8_t)rank[j] : (int8_t)-1;
       if (sel) {
         selv_l[t][rank[j]] = v[j];
         o.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // this wave's selv_l writes complete (lgkmcnt(0) only: the global stores stay in flight)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
     for (uint32_t p = lane; p < K; p += 64u) o.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
@@ -900,17 +901,31 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
   write_gemv_maps(maps, (uint32_t)*na_l);
 }
 
-// Wave 0 of route_small_body: counts, scan, active list, records, segment positions.
+// Rank of token t in the 16 rank bytes rk (4 dwords) of one expert: -1 = not chosen.
+__device__ __forceinline__ int rank_byte(const uint32_t (&rk)[4], uint32_t t) {
+  return (int)(int8_t)(uint8_t)(rk[t >> 2] >> (8u * (t & 3u)));
+}
+
+// Wave 0 of route_small_body: counts, scan, active list, records, segment positions.  Lane e
+// reads the ranks of expert e in all tokens with one 16-byte LDS read (rank_l[e][t]).
 template <int J>
 __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                     int8_t (*rank_l)[kMaxExperts], int32_t *na_l) {
+                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l) {
+  static_assert(kSmallRouteMaxTokens == 16, "one 16-byte read per expert");
   const uint32_t lane = threadIdx.x & 63u;
   int cnt[J];
+  uint32_t rk[J][4];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const uint32_t e = lane + 64u * j;
+    const uint4 v = e < E ? *(const uint4 *)rank_l[e] : make_uint4(~0u, ~0u, ~0u, ~0u);
+    rk[j][0] = v.x;
+    rk[j][1] = v.y;
+    rk[j][2] = v.z;
+    rk[j][3] = v.w;
     int c = 0;
-    for (uint32_t t2 = 0; t2 < T; ++t2) c += (e < E && rank_l[t2][e] >= 0) ? 1 : 0;
+#pragma unroll
+    for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) c += (t2 < T && rank_byte(rk[j], t2) >= 0) ? 1 : 0;
     cnt[j] = c;
   }
   int off[J], ra[J];
@@ -956,12 +971,14 @@ __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const R
   int seen[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) seen[j] = 0;
-  for (uint32_t t2 = 0; t2 < T; ++t2) {
+#pragma unroll
+  for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) {
+    if (t2 >= T) break;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const uint32_t e = lane + 64u * j;
       if (e >= E) continue;
-      const int r = rank_l[t2][e];
+      const int r = rank_byte(rk[j], t2);
       if (r >= 0) {
         const int pos = off[j] + seen[j];
         const int32_t slot = (int32_t)(t2 * K + (uint32_t)r);
@@ -979,7 +996,7 @@ __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const R
 
 template <int J>
 __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
-  __shared__ int8_t rank_l[kSmallRouteMaxTokens][kMaxExperts];
+  __shared__ __align__(16) int8_t rank_l[kMaxExperts][kSmallRouteMaxTokens];
   __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
   __shared__ int32_t na_l;
   const RouteOut o{a.topk_idx, a.topk_w, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec};
@@ -989,12 +1006,14 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
 // ---------------------------------------------------------------------------------------------
 // Decode router (n <= 16 tokens, D % 8 == 0, D <= 512 * kFrontChunks, 16-byte aligned rows):
 // workgroup e = expert e, wave w = tokens 2w and 2w + 1.  Every lane issues all of its loads
-// at once (router row chunks and both tokens' chunks; workgroup 0 also gamma), then computes the
-// two dot products and sums of squares in the fixed lane order (lane l owns chunks
+// at once (router row chunks and both tokens' chunks, and the gamma chunks it normalises), then
+// computes the two dot products and sums of squares in the fixed lane order (lane l owns chunks
 // c = 512 i + 8 l + j, fmaf over i then j, xor butterfly) -- no LDS, no barrier.
 // logit = dot / r + b with r = sqrt(sum(x^2) / D + eps) (r = 1 without RmsNorm).  Workgroup 0
-// writes r and the normalised rows xn_t = x_t * (1/r_t) * gamma (x_t without RmsNorm) in the x
-// dtype, zero padded to Dp, for the expert GEMV.  Results equal router_kernel bit for bit.
+// writes r; the normalised rows xn_t = x_t * (1/r_t) * gamma (x_t without RmsNorm) in the x
+// dtype, zero padded to Dp, for the expert GEMV are written chunk by chunk, chunk i (columns
+// 512 i ..) by workgroup i mod E, so no workgroup carries all of them.  Results equal
+// router_kernel bit for bit.
 // ---------------------------------------------------------------------------------------------
 template <typename XT, typename WT>
 __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
@@ -1007,6 +1026,8 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
   const XT *x = (const XT *)a.x;
   const WT *rw = (const WT *)a.rw + (size_t)e * D;
   const bool xn_wg = blockIdx.x == 0 && a.xn;
+  // xn chunk i is written by workgroup i mod E
+  auto own = [&](int i) { return a.xn != nullptr && (uint32_t)i % E == e; };
 
   Chunk8<WT> wc[RC];
   Chunk8<XT> xc0[RC], xc1[RC];
@@ -1017,7 +1038,7 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
     chunk_load(wc[i], rw + c0);
     chunk_load(xc0[i], x + (size_t)t0 * D + c0);
     chunk_load(xc1[i], x + (size_t)t1 * D + c0);
-    if (xn_wg && a.apply_norm) chunk_load(gc[i], a.gamma + c0);
+    if (own(i) && a.apply_norm) chunk_load(gc[i], a.gamma + c0);
   }
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // dot t0, dot t1, sumsq t0, sumsq t1
 #pragma unroll
@@ -1046,14 +1067,14 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
       if (has1) a.rms[t1] = r1;
     }
   }
-  if (!xn_wg) return;
+  if (!a.xn) return;
   const float ir0 = 1.0f / r0, ir1 = 1.0f / r1;
   XT *xn0 = (XT *)a.xn + (size_t)t0 * a.Dp;
   XT *xn1 = (XT *)a.xn + (size_t)t1 * a.Dp;
 #pragma unroll
   for (int i = 0; i < RC; ++i) {
     const uint32_t c0 = 512u * i + 8u * lane;
-    if (c0 >= a.Dp) continue;  // Dp is a multiple of 32, D of 8: a chunk is all data or all padding
+    if (!own(i) || c0 >= a.Dp) continue;  // Dp is a multiple of 32, D of 8: a chunk is all data or all padding
     float x0[8], x1[8], g[8];
     if (c0 < D) {
       chunk_vals(xc0[i], x0);
@@ -1074,7 +1095,7 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
     if (has1) store8(xn1 + c0, x1);
   }
   // rows beyond RC chunks of padding (Dp > 512 * RC cannot happen: Dp <= D + 31 <= 512 * RC + 31)
-  for (uint32_t c0 = 512u * RC + 8u * lane; c0 < a.Dp; c0 += 512u) {
+  for (uint32_t c0 = 512u * RC + 8u * lane; xn_wg && c0 < a.Dp; c0 += 512u) {
     const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     store8(xn0 + c0, z);
     if (has1) store8(xn1 + c0, z);
