@@ -826,16 +826,58 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 
 // ---------------------------------------------------------------------------------------------
 // Routing of a decode-sized batch (T <= 16, E <= 256) by one workgroup of T waves.
-//  phase 1 (wave t = token t): lane l holds experts l + 64 j (j < J); the rank of each is the
-//    number of experts whose packed key (topk_key, the `beats` order) is larger, counted over
-//    readlane broadcasts; ranks < K are the selection; softmax over the selected logits
-//    (q ascending) by lanes p < K.
-//  phase 2 (wave 0): per-expert counts, exclusive scan and active list by a readlane loop, and
-//    segment positions in token order from per-lane running counters.
+//  phase 1 (wave t = token t): lane l holds experts l + 64 j (j < J); K rounds of a wave-wide
+//    maximum of the packed keys (topk_key, the `beats` order) not yet taken select the experts
+//    of ranks 0 .. K-1; softmax over the selected logits (q ascending) by lanes p < K.
+//  phase 2 (every wave): per-expert counts and exclusive scans (DPP prefix sums); wave 0 writes
+//    the active list and records, wave t token t's segment positions (earlier tokens first).
 // Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
+}
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+// (h, l) = the larger of the 64-bit keys (h, l) and (h2, l2), high word first
+__device__ __forceinline__ void key_max(uint32_t &h, uint32_t &l, uint32_t h2, uint32_t l2) {
+  const bool g = h2 > h || (h2 == h && l2 > l);
+  h = g ? h2 : h;
+  l = g ? l2 : l;
+}
+// Maximum of the 64-bit keys (h, l) over the wave, in every lane: quad permutations (lanes
+// l ^ 1, l ^ 2), row rotations by 4 and 8 (the row's four quads), then the permlane swaps
+// between rows 16 and 32 apart.
+__device__ __forceinline__ void wave_max_key(uint32_t &h, uint32_t &l) {
+  key_max(h, l, dpp_u<0xB1>(h), dpp_u<0xB1>(l));    // quad_perm [1,0,3,2]
+  key_max(h, l, dpp_u<0x4E>(h), dpp_u<0x4E>(l));    // quad_perm [2,3,0,1]
+  key_max(h, l, dpp_u<0x124>(h), dpp_u<0x124>(l));  // row_ror:4
+  key_max(h, l, dpp_u<0x128>(h), dpp_u<0x128>(l));  // row_ror:8
+  {
+    const auto ph = __builtin_amdgcn_permlane16_swap(h, h, false, false);
+    const auto pl = __builtin_amdgcn_permlane16_swap(l, l, false, false);
+    h = ph[0];
+    l = pl[0];
+    key_max(h, l, ph[1], pl[1]);
+  }
+  {
+    const auto ph = __builtin_amdgcn_permlane32_swap(h, h, false, false);
+    const auto pl = __builtin_amdgcn_permlane32_swap(l, l, false, false);
+    h = ph[0];
+    l = pl[0];
+    key_max(h, l, ph[1], pl[1]);
+  }
+}
+// Inclusive prefix sum over the wave's lanes: row_shr 1, 2, 4, 8 inside each row of 16 (lanes
+// without a source add 0), then the totals of the rows below (lanes 15, 31, 47).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_u<0x111>(v);  // row_shr:1
+  v += dpp_u<0x112>(v);  // row_shr:2
+  v += dpp_u<0x114>(v);  // row_shr:4
+  v += dpp_u<0x118>(v);  // row_shr:8
+  const uint32_t r0 = readlane_u(v, 15), r1 = readlane_u(v, 31), r2 = readlane_u(v, 47);
+  const uint32_t row = (threadIdx.x & 63u) >> 4;
+  return v + (row == 0u ? 0u : row == 1u ? r0 : row == 2u ? r0 + r1 : r0 + r1 + r2);
 }
 
 // Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
@@ -866,18 +908,29 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
       v[j] = e < E ? lg[(size_t)t * E + e] : 0.0f;
       key[j] = topk_key(v[j], e);
     }
-    uint32_t rank[J];
+    // K rounds of a wave-wide maximum over the keys not yet taken: round r finds the expert of
+    // rank r (keys are unique, so exactly one lane holds it); the rest keep rank ~0u
+    uint32_t rank[J], kh[J], kl[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) rank[j] = 0u;
+    for (int j = 0; j < J; ++j) {
+      rank[j] = ~0u;
+      kh[j] = (uint32_t)(key[j] >> 32);
+      kl[j] = (uint32_t)key[j];
+    }
+    for (uint32_t r = 0; r < K; ++r) {
+      uint32_t bh = 0u, bl = 0u;  // below every real key (the low word ~index is never 0)
 #pragma unroll
-    for (int jj = 0; jj < J; ++jj) {
-      const uint32_t kn = min(64u, E - 64u * jj);
-      const uint32_t khi = (uint32_t)(key[jj] >> 32), klo = (uint32_t)key[jj];
-      for (uint32_t kk = 0; kk < kn; ++kk) {
-        const uint64_t kb = ((uint64_t)readlane_u(khi, kk) << 32) | readlane_u(klo, kk);
-#pragma unroll
-        for (int j = 0; j < J; ++j) rank[j] += kb > key[j] ? 1u : 0u;
+      for (int j = 0; j < J; ++j) {
+        const bool cand = lane + 64u * j < E && rank[j] == ~0u;
+        if (cand && (kh[j] > bh || (kh[j] == bh && kl[j] > bl))) {
+          bh = kh[j];
+          bl = kl[j];
+        }
       }
+      wave_max_key(bh, bl);
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (lane + 64u * j < E && kh[j] == bh && kl[j] == bl) rank[j] = r;
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -896,7 +949,7 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
     for (uint32_t p = lane; p < K; p += 64u) o.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
   __syncthreads();
-  if (t == 0) route_small_dispatch<J>(T, E, K, o, rank_l, na_l);
+  route_small_dispatch<J>(T, E, K, o, rank_l, na_l);
   __syncthreads();
   write_gemv_maps(maps, (uint32_t)*na_l);
 }
@@ -906,13 +959,16 @@ __device__ __forceinline__ int rank_byte(const uint32_t (&rk)[4], uint32_t t) {
   return (int)(int8_t)(uint8_t)(rk[t >> 2] >> (8u * (t & 3u)));
 }
 
-// Wave 0 of route_small_body: counts, scan, active list, records, segment positions.  Lane e
-// reads the ranks of expert e in all tokens with one 16-byte LDS read (rank_l[e][t]).
+// Dispatch part of route_small_body, run by every wave: each computes the per-expert counts and
+// scans (lane e reads the ranks of expert e in all tokens with one 16-byte LDS read,
+// rank_l[e][t]); wave 0 writes the per-expert outputs (segment offsets, active list, record
+// headers), wave t < T the segment entries of token t (its position inside expert e's segment is
+// the number of earlier tokens that chose e).
 template <int J>
 __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
                                      int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l) {
   static_assert(kSmallRouteMaxTokens == 16, "one 16-byte read per expert");
-  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
   int cnt[J];
   uint32_t rk[J][4];
 #pragma unroll
@@ -928,31 +984,23 @@ __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const R
     for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) c += (t2 < T && rank_byte(rk[j], t2) >= 0) ? 1 : 0;
     cnt[j] = c;
   }
+  // exclusive scans over the experts (token counts and experts with tokens), chunk by chunk
   int off[J], ra[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) off[j] = ra[j] = 0;
   int total = 0, nact = 0;
 #pragma unroll
-  for (int jj = 0; jj < J; ++jj) {
-    const uint32_t kn = min(64u, E - 64u * jj);
-    for (uint32_t kk = 0; kk < kn; ++kk) {
-      const int c = (int)readlane_u((uint32_t)cnt[jj], kk);
-      const uint32_t ek = 64u * jj + kk;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const bool before = ek < lane + 64u * j;
-        off[j] += before ? c : 0;
-        ra[j] += (before && c > 0) ? 1 : 0;
-      }
-      total += c;
-      nact += c > 0 ? 1 : 0;
-    }
+  for (int j = 0; j < J; ++j) {
+    const uint32_t c = (uint32_t)cnt[j], nz = c > 0u ? 1u : 0u;
+    const uint32_t ic = wave_incl_scan(c), inz = wave_incl_scan(nz);
+    off[j] = total + (int)(ic - c);
+    ra[j] = nact + (int)(inz - nz);
+    total += (int)readlane_u(ic, 63);
+    nact += (int)readlane_u(inz, 63);
   }
   // seg_off, active[0..nact) from the experts with tokens, active[nact..E) = -1 (disjoint writes)
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const uint32_t e = lane + 64u * j;
-    if (e >= E) continue;
+    if (t != 0 || e >= E) continue;
     o.seg_off[e] = off[j];
     if (cnt[j] > 0) {
       o.active[ra[j]] = (int32_t)e;
@@ -963,33 +1011,28 @@ __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const R
     }
     if ((int)e >= nact) o.active[e] = -1;
   }
-  if (lane == 0) {
+  if (t == 0 && lane == 0) {
     o.seg_off[E] = total;
     *o.num_active = nact;
     *na_l = nact;
   }
-  int seen[J];
+  if (t >= T) return;
 #pragma unroll
-  for (int j = 0; j < J; ++j) seen[j] = 0;
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    if (e >= E) continue;
+    const int r = rank_byte(rk[j], t);
+    if (r < 0) continue;
+    int seen = 0;  // earlier tokens that chose e
 #pragma unroll
-  for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) {
-    if (t2 >= T) break;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t e = lane + 64u * j;
-      if (e >= E) continue;
-      const int r = rank_byte(rk[j], t2);
-      if (r >= 0) {
-        const int pos = off[j] + seen[j];
-        const int32_t slot = (int32_t)(t2 * K + (uint32_t)r);
-        o.perm[pos] = slot;
-        o.pos_of[slot] = pos;
-        if (seen[j] < (int)kRecTokens) {
-          o.exrec[ra[j] * kRecWords + 4 + seen[j]] = (int32_t)t2;
-          o.exrec[ra[j] * kRecWords + 4 + kRecTokens + seen[j]] = slot;
-        }
-        seen[j] += 1;
-      }
+    for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) seen += (t2 < t && rank_byte(rk[j], t2) >= 0) ? 1 : 0;
+    const int pos = off[j] + seen;
+    const int32_t slot = (int32_t)(t * K + (uint32_t)r);
+    o.perm[pos] = slot;
+    o.pos_of[slot] = pos;
+    if (seen < (int)kRecTokens) {
+      o.exrec[ra[j] * kRecWords + 4 + seen] = (int32_t)t;
+      o.exrec[ra[j] * kRecWords + 4 + kRecTokens + seen] = slot;
     }
   }
 }
