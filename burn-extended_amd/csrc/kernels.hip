@@ -1167,9 +1167,10 @@ __device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
 
 
 // Work split.  Grid of G workgroups (as many as stay resident); each active expert gets
-// wpe = G / num_active of them; its part-th workgroup owns row tiles part + wpe * i (wave w:
-// i = w, w + 4, ...), so an expert's workgroups sweep its weights together (few pages hot at a
-// time) and every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
+// wpe = G / num_active of them; its part-th workgroup owns work units part + wpe * i (wave w:
+// i = w, w + 4, ...), a unit being a row tile or (down with ksplit) one of the two fixed K-halves
+// of a row tile (units u < nrt the first halves, u - nrt the second), so an expert's workgroups
+// sweep its weights together (few pages hot at a time) and every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
 // one pass at decode sizes).  A workgroup learns num_active, its expert, segment and first tokens
 // from one round trip (num_active plus the record table).
 // Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups held in one
@@ -1213,22 +1214,31 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2;
   const uint32_t tail = a.nb - 4u * (nkg - 1u);
-  const uint32_t nst = (nkg + CJ - 1u) / CJ;  // steps per tile
+  // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of half u / nrt
+  const uint32_t nsplit = (!GATE_UP && a.ksplit) ? 2u : 1u;
+  const uint32_t H = (nkg + nsplit - 1u) / nsplit;  // K-groups per unit
+  const uint32_t nst = (H + CJ - 1u) / CJ;           // steps per unit
+  const uint32_t nunits = nrt * nsplit;
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
+  auto unit_rt = [&](uint32_t u) { return u < nrt ? u : u - nrt; };
+  auto unit_h = [&](uint32_t u) { return u < nrt ? 0u : 1u; };
 
   // K-group of slot j of step st; lanes outside the tile load the tile's first 16 bytes instead
   // (valid memory) and are neutralised at use (scale 1.0, zero B): no branch surrounds a load, so
   // partial vmcnt waits keep later loads in flight.
-  auto kg_of = [&](uint32_t st, uint32_t j) { return CJ * st + j; };
-  auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
-  auto load_step = [&](uint32_t rt, uint32_t st, uint4(&av)[CJ], uint32_t(&sv)[CJ]) {
+  auto kg_of = [&](uint32_t h, uint32_t st, uint32_t j) { return h * H + CJ * st + j; };
+  auto lane_ok = [&](uint32_t h, uint32_t kg) {
+    return kg < min(h * H + H, nkg) && q < (kg + 1u == nkg ? tail : 4u);
+  };
+  auto load_step = [&](uint32_t u, uint32_t st, uint4(&av)[CJ], uint32_t(&sv)[CJ]) {
+    const uint32_t rt = unit_rt(u), h = unit_h(u);
     const uint8_t *wt = wexp + (size_t)rt * a.nb * 256u;
     const uint8_t *stp = sexp + (size_t)rt * a.nb * 16u;
 #pragma unroll
     for (uint32_t j = 0; j < CJ; ++j) {
-      const uint32_t kg = kg_of(st, j);
-      const bool ok = lane_ok(kg);
+      const uint32_t kg = kg_of(h, st, j);
+      const bool ok = lane_ok(h, kg);
       av[j] = *(const uint4 *)(wt + (ok ? kg * 1024u + lane * 16u : 0u));
       // the dword holding this lane's scale byte (byte lane & 3), kept raw until use: a byte load
       // would be re-extended at the loop back-edge, which waits for the prefetch to land
@@ -1303,11 +1313,11 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
   };
 
-  // this wave's tiles: part + wpe * i for i = wv, wv + 4, ... < ntw (first tile clamped into the
-  // expert for the start-up loads of a wave without tiles)
+  // this wave's units: part + wpe * i for i = wv, wv + 4, ... < ntw (first unit clamped into the
+  // expert for the start-up loads of a wave without units)
   const uint32_t my_first = part + wpe * wv, tstride = 4u * wpe;
   const uint32_t my_tiles = wv < ntw ? (ntw - wv + 3u) / 4u : 0u;
-  const uint32_t first_c = min(my_first, nrt - 1u);
+  const uint32_t first_c = min(my_first, nunits - 1u);
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
   uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
   uint4 abuf[CJ];
@@ -1320,14 +1330,15 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   // are done.
   auto do_step = [&]() -> bool {
     if (g >= total) return false;
-    const uint32_t rt = my_first + tstride * ti;
+    const uint32_t u = my_first + tstride * ti, rt = unit_rt(u), h = unit_h(u);
     // the bias of this lane's 4 epilogue rows, requested before this step's refills
     const f32x4_t bias4 = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + rt * 16u + 4u * q);
     // next step: next step of this tile, step 0 of the next tile, or (last step of the pass) the
     // current step again -- a cache hit that keeps the load count static
     const bool more_st = st + 1u < nst;
     const bool more_t = ti + 1u < my_tiles;
-    const uint32_t nrt_ = more_st ? rt : (more_t ? rt + tstride : rt);
+    const uint32_t nu = more_st ? u : (more_t ? u + tstride : u);
+    const uint32_t nrt_ = unit_rt(nu), nh = unit_h(nu);
     const uint32_t nst_ = more_st ? st + 1u : (more_t ? 0u : st);
     const uint8_t *nwt = wexp + (size_t)nrt_ * a.nb * 256u;
     const uint8_t *nsp = sexp + (size_t)nrt_ * a.nb * 16u;
@@ -1335,8 +1346,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const uint16_t *brow = bs + (size_t)min(i16, mtm - 1u) * ldk;  // rows >= mt: zeroed at use
 #pragma unroll
     for (uint32_t j = 0; j < CJ; ++j) {
-      const uint32_t kg = kg_of(st, j);
-      const bool ok = lane_ok(kg);
+      const uint32_t kg = kg_of(h, st, j);
+      const bool ok = lane_ok(h, kg);
       const bool bok = bval && ok;
       const float sc = ok ? e8m0_to_f32((sbuf[j] >> sshift) & 0xFFu) : 1.0f;
       const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
@@ -1354,8 +1365,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       }
       // refill slot j with the next step's K-group j
       {
-        const uint32_t nkg_ = kg_of(nst_, j);
-        const bool nok = lane_ok(nkg_);
+        const uint32_t nkg_ = kg_of(nh, nst_, j);
+        const bool nok = lane_ok(nh, nkg_);
         abuf[j] = *(const uint4 *)(nwt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
         sbuf[j] = *(const uint32_t *)(nsp + (nok ? nkg_ * 64u + (lane & ~3u) : 0u));
       }
@@ -1380,13 +1391,14 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
           o[0] = o0;
         }
       } else {
-        // token-major slot row t * topk + p, expert bias b2 added once
-        float *o = a.out + (size_t)tok_l[i16] * a.out_stride + r0;
+        // token-major slot row t * topk + p, expert bias b2 added once (first K-half)
+        float *o = a.out + (h ? a.out_half : 0u) + (size_t)tok_l[i16] * a.out_stride + r0;
+        const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : bias4;
         if (r0 + 3u < a.out_rows) {
-          *(float4 *)o = make_float4(acc[0] + bias4[0], acc[1] + bias4[1], acc[2] + bias4[2], acc[3] + bias4[3]);
+          *(float4 *)o = make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
         } else {
           for (uint32_t r = 0; r < 4u; ++r)
-            if (r0 + r < a.out_rows) o[r] = acc[r] + bias4[r];
+            if (r0 + r < a.out_rows) o[r] = acc[r] + b4[r];
         }
       }
     }
@@ -1429,6 +1441,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
       const uint32_t p = min(p0 + u, a.K - 1u);
       wv[u] = a.topk_w[(size_t)t * a.K + p];
       yv[u] = *(const float4 *)(a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 4 == 0, d0 < Dp
+      if (a.ypart2) {
+        const float4 y2 = *(const float4 *)(a.ypart2 + ((size_t)t * a.K + p) * a.Dp + d0);
+        yv[u] = make_float4(yv[u].x + y2.x, yv[u].y + y2.y, yv[u].z + y2.z, yv[u].w + y2.w);
+      }
     }
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {

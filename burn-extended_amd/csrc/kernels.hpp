@@ -89,6 +89,10 @@ struct GemvArgs {
   float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
+  // down only: 1 = every row tile's K range is split into two fixed halves, separate work units;
+  // the second half's partial sums (without b2) go to out + out_half, combine adds the two
+  uint32_t ksplit;
+  uint64_t out_half;
 };
 
 // Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,
@@ -147,6 +151,7 @@ struct CombineArgs {
   const void *x;
   void *y;
   const float *ypart;  // token-major slot rows [n*K, Dp], expert bias included
+  const float *ypart2; // null, or the second K-half's partial sums of the same rows (added first)
   const float *topk_w;
   uint32_t n, D, Dp, K;
   int add_residual;

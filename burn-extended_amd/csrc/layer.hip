@@ -288,7 +288,9 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[2] = take(nk * ka / 32);
     w.aq[3] = take(nk * ka / 32);
   }
-  w.ypart = take(nk * L.Dp * 4);
+  // expert GEMV batches (n < kGemmMinTokens) split the down projection's K range in two halves:
+  // a second partial-sum buffer
+  w.ypart = take(nk * L.Dp * 4 * (n < kGemmMinTokens ? 2 : 1));
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   w.total = off;
   return w;
@@ -490,11 +492,12 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
 
 // The weighted combine + residual of every path (token-major slot rows in p.ypart).
 burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
-                       const WsPtrs &p, hipStream_t s) {
+                       const WsPtrs &p, hipStream_t s, bool ksplit = false) {
   CombineArgs c{};
   c.x = x;
   c.y = y;
   c.ypart = p.ypart;
+  c.ypart2 = ksplit ? p.ypart + n * L->K * L->Dp : nullptr;
   c.topk_w = p.topk_w;
   c.n = (uint32_t)n;
   c.D = L->D;
@@ -734,7 +737,10 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   }
   const int nt = xb ? 1 : 3;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
-  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt};
+  // down projection: every row tile's K range in two fixed halves (separate work units, so the
+  // units of a batch are about half a tile each and spread evenly over the waves)
+  const bool ksplit = n < kGemmMinTokens && L->w2.nb > 4u;
+  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt * (ksplit ? 2u : 1u)};
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
@@ -774,6 +780,10 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.limit = L->limit;
     g.nrec = cf.nrec;
     g.wgmap = p.wgmap + (gate_up ? 0 : cfg_up.grid);
+    if (!gate_up && ksplit) {
+      g.ksplit = 1;
+      g.out_half = n * L->K * L->Dp;
+    }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
@@ -782,7 +792,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   st = gemv(false);
   if (st != BURNEXT_OK) return st;
 
-  return combine(L, x, y, xb, n, flags, p, s);
+  return combine(L, x, y, xb, n, flags, p, s, ksplit);
 }
 
 burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, uint64_t n,
