@@ -1168,8 +1168,8 @@ __device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
 
 // Work split.  Grid of G workgroups (as many as stay resident); each active expert gets
 // wpe = G / num_active of them; its part-th workgroup owns work units part + wpe * i (wave w:
-// i = w, w + 4, ...), a unit being a row tile or (down with ksplit) one of the two fixed K-halves
-// of a row tile (units u < nrt the first halves, u - nrt the second), so an expert's workgroups
+// i = w, w + 4, ...), a unit being a row tile or (down with ksplit) one of ksplit fixed K-parts
+// of a row tile (unit u: part u / nrt of row tile u mod nrt), so an expert's workgroups
 // sweep its weights together (few pages hot at a time) and every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
 // one pass at decode sizes).  A workgroup learns num_active, its expert, segment and first tokens
 // from one round trip (num_active plus the record table).
@@ -1214,15 +1214,15 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2;
   const uint32_t tail = a.nb - 4u * (nkg - 1u);
-  // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of half u / nrt
-  const uint32_t nsplit = (!GATE_UP && a.ksplit) ? 2u : 1u;
+  // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
+  const uint32_t nsplit = (!GATE_UP && a.ksplit > 1u) ? a.ksplit : 1u;
   const uint32_t H = (nkg + nsplit - 1u) / nsplit;  // K-groups per unit
   const uint32_t nst = (H + CJ - 1u) / CJ;           // steps per unit
   const uint32_t nunits = nrt * nsplit;
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
-  auto unit_rt = [&](uint32_t u) { return u < nrt ? u : u - nrt; };
-  auto unit_h = [&](uint32_t u) { return u < nrt ? 0u : 1u; };
+  auto unit_h = [&](uint32_t u) { return nsplit == 1u ? 0u : u / nrt; };
+  auto unit_rt = [&](uint32_t u) { return u - unit_h(u) * nrt; };
 
   // K-group of slot j of step st; lanes outside the tile load the tile's first 16 bytes instead
   // (valid memory) and are neutralised at use (scale 1.0, zero B): no branch surrounds a load, so
@@ -1391,8 +1391,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
           o[0] = o0;
         }
       } else {
-        // token-major slot row t * topk + p, expert bias b2 added once (first K-half)
-        float *o = a.out + (h ? a.out_half : 0u) + (size_t)tok_l[i16] * a.out_stride + r0;
+        // token-major slot row t * topk + p, expert bias b2 added once (K-part 0)
+        float *o = a.out + h * a.out_half + (size_t)tok_l[i16] * a.out_stride + r0;
         const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : bias4;
         if (r0 + 3u < a.out_rows) {
           *(float4 *)o = make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
@@ -1441,8 +1441,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
       const uint32_t p = min(p0 + u, a.K - 1u);
       wv[u] = a.topk_w[(size_t)t * a.K + p];
       yv[u] = *(const float4 *)(a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 4 == 0, d0 < Dp
-      if (a.ypart2) {
-        const float4 y2 = *(const float4 *)(a.ypart2 + ((size_t)t * a.K + p) * a.Dp + d0);
+      for (uint32_t h = 1; h < a.nparts; ++h) {
+        const float4 y2 = *(const float4 *)(a.ypart + h * a.part_stride + ((size_t)t * a.K + p) * a.Dp + d0);
         yv[u] = make_float4(yv[u].x + y2.x, yv[u].y + y2.y, yv[u].z + y2.z, yv[u].w + y2.w);
       }
     }

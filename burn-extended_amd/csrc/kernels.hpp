@@ -89,8 +89,8 @@ struct GemvArgs {
   float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
-  // down only: 1 = every row tile's K range is split into two fixed halves, separate work units;
-  // the second half's partial sums (without b2) go to out + out_half, combine adds the two
+  // down only: every row tile's K range split into ksplit (0 or 1: none) fixed parts, separate
+  // work units; part h's partial sums go to out + h * out_half (b2 in part 0), combine adds them
   uint32_t ksplit;
   uint64_t out_half;
 };
@@ -151,7 +151,8 @@ struct CombineArgs {
   const void *x;
   void *y;
   const float *ypart;  // token-major slot rows [n*K, Dp], expert bias included
-  const float *ypart2; // null, or the second K-half's partial sums of the same rows (added first)
+  uint32_t nparts;     // K-parts of ypart (1 = complete rows), parts part_stride floats apart,
+  uint64_t part_stride;  // summed in order before the weighting
   const float *topk_w;
   uint32_t n, D, Dp, K;
   int add_residual;
@@ -189,6 +190,7 @@ constexpr uint32_t kDispatchThreads = 1024;
 constexpr uint32_t kDispatchChunk = 256;           // dispatch_wide_kernel: tokens per workgroup
 constexpr uint32_t kDispatchWideMinTokens = 1024;  // dispatch_wide_kernel from this batch size on
 constexpr uint32_t kGemvThreads = 256;
+constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert GEMV (decode-sized batches; 3, 4 and 6 measured slower)
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel

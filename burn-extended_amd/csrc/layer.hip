@@ -288,9 +288,9 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[2] = take(nk * ka / 32);
     w.aq[3] = take(nk * ka / 32);
   }
-  // expert GEMV batches (n < kGemmMinTokens) split the down projection's K range in two halves:
-  // a second partial-sum buffer
-  w.ypart = take(nk * L.Dp * 4 * (n < kGemmMinTokens ? 2 : 1));
+  // expert GEMV batches (n < kGemmMinTokens) split the down projection's K range in up to
+  // kDownSplit parts: a partial-sum buffer each
+  w.ypart = take(nk * L.Dp * 4 * (n < kGemmMinTokens ? kDownSplit : 1));
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   w.total = off;
   return w;
@@ -492,12 +492,13 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
 
 // The weighted combine + residual of every path (token-major slot rows in p.ypart).
 burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
-                       const WsPtrs &p, hipStream_t s, bool ksplit = false) {
+                       const WsPtrs &p, hipStream_t s, uint32_t nparts = 1) {
   CombineArgs c{};
   c.x = x;
   c.y = y;
   c.ypart = p.ypart;
-  c.ypart2 = ksplit ? p.ypart + n * L->K * L->Dp : nullptr;
+  c.nparts = nparts;
+  c.part_stride = n * L->K * L->Dp;
   c.topk_w = p.topk_w;
   c.n = (uint32_t)n;
   c.D = L->D;
@@ -737,10 +738,11 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   }
   const int nt = xb ? 1 : 3;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
-  // down projection: every row tile's K range in two fixed halves (separate work units, so the
-  // units of a batch are about half a tile each and spread evenly over the waves)
-  const bool ksplit = n < kGemmMinTokens && L->w2.nb > 4u;
-  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt * (ksplit ? 2u : 1u)};
+  // down projection: every row tile's K range in ksplit fixed parts of whole K-groups (separate
+  // work units, so the units of a batch are a fraction of a tile each and spread evenly over the
+  // waves)
+  const uint32_t ksplit = n < kGemmMinTokens ? std::min<uint32_t>(kDownSplit, (L->w2.nb + 3u) / 4u) : 1u;
+  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt * ksplit};
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
@@ -780,8 +782,8 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.limit = L->limit;
     g.nrec = cf.nrec;
     g.wgmap = p.wgmap + (gate_up ? 0 : cfg_up.grid);
-    if (!gate_up && ksplit) {
-      g.ksplit = 1;
+    if (!gate_up && ksplit > 1u) {
+      g.ksplit = ksplit;
       g.out_half = n * L->K * L->Dp;
     }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
