@@ -135,6 +135,35 @@ def test_route_ties_lower_index(M):
     layer.close()
 
 
+@pytest.mark.parametrize("E,K,n", [(130, 6, 5), (256, 8, 16), (64, 4, 1), (65, 5, 9)])
+def test_route_small_ties_nan_signed_zero(M, oracle, E, K, n):
+    """Decode-sized routing (wave-wide key maxima) on logits made of ties, a NaN, -0 and +0, with
+    equal values on both sides of the 64-expert lane chunks: indices and weights as the oracle's
+    order (NaN lowest, -0 == +0, equal values by lower index)."""
+    from burnext_amd import synth
+    print(f"small route ties E={E} K={K} n={n}", flush=True)
+    L = _make(synth, 64, 32, E, K, dtype="f32")
+    L.router_w_f32[:] = 0.0
+    b = np.full(E, 0.5, np.float32)
+    for e_, v in ((E - 1, 2.0), (0, 1.0), (min(63, E - 1), 1.0), (min(64, E - 1), 1.0), (E // 2, 0.75),
+                  (E // 3, 0.75), (7 % E, -0.0), (8 % E, 0.0), ((E * 3) // 4, np.nan)):
+        b[e_] = v
+    L.router_b_f32[:] = b
+    layer = M.MoeLayer(L)
+    x = synth.make_tokens(n, 64, dtype="f32")
+    idx, w, lg = layer.route(M.to_device_x(x, "f32"))
+    torch.cuda.synchronize()
+    lg_ref = oracle.route_logits(x, L.router_w_f32, L.router_b_f32, L.gamma_f32, L.rms_eps, True)
+    idx_ref, w_ref = oracle.topk_softmax(lg_ref, K)
+    assert np.array_equal(idx.cpu().numpy(), idx_ref)
+    np.testing.assert_allclose(_np(w), w_ref, rtol=4e-7 * 8, atol=0)
+    seg, perm = layer.dispatch(idx)
+    seg_ref, perm_ref, _ = oracle.dispatch(idx_ref, E)
+    assert np.array_equal(seg.cpu().numpy(), seg_ref)
+    assert np.array_equal(perm.cpu().numpy(), perm_ref)
+    layer.close()
+
+
 # ---------------------------------------------------------------------------------------------
 # dispatch
 # ---------------------------------------------------------------------------------------------
