@@ -611,25 +611,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 // atomicOr) and popcount prefixes, so the result does not depend on thread timing.
 // LDS: cnt[E], base[E], bm[E * words], wpre[E * words] (words = blockDim.x / 32).
 // ---------------------------------------------------------------------------------------------
-// Work maps of both expert GEMV launches from num_active (all threads of the block).
-__device__ void write_gemv_maps(const GemvMaps &m, uint32_t na) {
-  if (!m.map) return;
-  for (uint32_t g = threadIdx.x; g < m.g1 + m.g2; g += blockDim.x) {
-    const bool up = g < m.g1;
-    const uint32_t G = up ? m.g1 : m.g2, nrt = up ? m.nrt1 : m.nrt2, gg = up ? g : g - m.g1;
-    uint2 v = make_uint2(0xFFFFu, 0u);
-    if (na > 0u) {
-      const uint32_t wpe = max(1u, min(G / na, nrt));
-      const uint32_t ai = gg / wpe, part = gg - ai * wpe;
-      if (ai < na) v = make_uint2(ai | (part << 16), wpe | (((nrt - part + wpe - 1u) / wpe) << 16));
-    }
-    m.map[g] = v;
-  }
-}
-
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
                                int32_t *perm, int32_t *pos_of, int32_t *active, int32_t *num_active,
-                               int32_t *exrec, const GemvMaps &maps, int32_t *tile_off, int32_t *lds) {
+                               int32_t *exrec, int32_t *tile_off, int32_t *lds) {
   const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;
   int32_t *cnt = lds, *base = lds + E;
   uint32_t *bm = (uint32_t *)(lds + 2 * E);
@@ -672,7 +656,6 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
     }
   }
   __syncthreads();
-  write_gemv_maps(maps, (uint32_t)lds[4 * E + 2 * E * words]);
   for (uint32_t c0 = 0; c0 < n; c0 += nth) {
     for (uint32_t i = tid; i < E * words; i += nth) bm[i] = 0u;
     __syncthreads();
@@ -722,8 +705,8 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) {
 // per-expert entry counts of each chunk (LDS atomics: order-independent).  dispatch_wide_kernel:
 // totals and earlier-chunk counts from those; an entry's segment position is seg_off[e] + (entries
 // of e in earlier chunks) + (rank among this chunk's tokens choosing e, from a per-expert token
-// bitmap).  Its workgroup 0 writes the segment offsets, token-tile prefix, active list, records
-// and GEMV maps.  Results equal block_dispatch's.
+// bitmap).  Its workgroup 0 writes the segment offsets, token-tile prefix, active list and
+// records.  Results equal block_dispatch's.
 __global__ __launch_bounds__(kDispatchChunk) void dispatch_count_kernel(DispatchArgs a) {
   __shared__ int32_t cnt[kMaxExperts];
   const uint32_t tid = threadIdx.x, E = a.E, K = a.K;
@@ -798,7 +781,6 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
     }
   }
   __syncthreads();
-  if (c == 0) write_gemv_maps(a.maps, (uint32_t)na_l);
   if (t >= n) return;
   const uint32_t wi = tid >> 5, bit = tid & 31u;
   for (uint32_t p = 0; p < K; ++p) {
@@ -820,7 +802,7 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec, a.maps,
+  block_dispatch(a.topk_idx, a.n, a.K, a.E, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec,
                  a.tile_off, (int32_t *)smem);
 }
 
@@ -896,7 +878,7 @@ __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const R
 // a workgroup of at least T waves.  Every wave of the workgroup must call it (it has a barrier).
 template <int J>
 __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                 const GemvMaps &maps, int8_t (*rank_l)[kSmallRouteMaxTokens], float (*selv_l)[kMaxTopK],
+                                 int8_t (*rank_l)[kSmallRouteMaxTokens], float (*selv_l)[kMaxTopK],
                                  int32_t *na_l) {
   const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
   if (t < T) {
@@ -950,8 +932,6 @@ __device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32
   }
   __syncthreads();
   route_small_dispatch<J>(T, E, K, o, rank_l, na_l);
-  __syncthreads();
-  write_gemv_maps(maps, (uint32_t)*na_l);
 }
 
 // Rank of token t in the 16 rank bytes rk (4 dwords) of one expert: -1 = not chosen.
@@ -1043,7 +1023,7 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
   __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
   __shared__ int32_t na_l;
   const RouteOut o{a.topk_idx, a.topk_w, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec};
-  route_small_body<J>(a.logits, a.n, a.E, a.K, o, a.maps, rank_l, selv_l, &na_l);
+  route_small_body<J>(a.logits, a.n, a.E, a.K, o, rank_l, selv_l, &na_l);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1166,13 +1146,43 @@ __device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
 }
 
 
-// Work split.  Grid of G workgroups (as many as stay resident); each active expert gets
-// wpe = G / num_active of them; its part-th workgroup owns work units part + wpe * i (wave w:
-// i = w, w + 4, ...), a unit being a row tile or (down with ksplit) one of ksplit fixed K-parts
-// of a row tile (unit u: part u / nrt of row tile u mod nrt), so an expert's workgroups
-// sweep its weights together (few pages hot at a time) and every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the expert's routed tokens;
-// one pass at decode sizes).  A workgroup learns num_active, its expert, segment and first tokens
-// from one round trip (num_active plus the record table).
+// Share of workgroup g of a grid of G among na active experts of nunits work units each: active
+// slot ai = g mod na, as its p-th workgroup (p = g / na), owns the contiguous units
+// [lo, lo + cnt).  The shares of a slot's workgroups are weighted by dispatch round r =
+// min(g / num_cus, 3) (kRoundWeight): workgroups are placed on the CUs round by round, and the
+// later ones share their CU with older ones that the memory system serves first.  32-bit
+// arithmetic: nunits * kRoundWeight[0] * G < 2^32 (checked at launch).  Returns false when the
+// workgroup has no units.
+__device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, uint32_t nunits, uint32_t num_cus,
+                                           uint32_t &ai, uint32_t &lo, uint32_t &cnt) {
+  if (na == 0u || na > G) return false;
+  ai = g % na;
+  const uint32_t p = g / na, nw = (G - 1u - ai) / na + 1u;  // part index, workgroups of slot ai
+  uint32_t b[4];  // parts p' >= b[k] are in round >= k (p' * na + ai >= k * num_cus)
+#pragma unroll
+  for (uint32_t k = 1; k < 4; ++k) {
+    const uint32_t kc = k * num_cus;
+    b[k] = kc <= ai ? 0u : (kc - ai + na - 1u) / na;
+  }
+  auto wsum = [&](uint32_t x) {  // weights of parts 0 .. x-1
+    int32_t w = (int32_t)(kRoundWeight[0] * x);
+#pragma unroll
+    for (uint32_t k = 1; k < 4; ++k)
+      if (x > b[k]) w += ((int32_t)kRoundWeight[k] - (int32_t)kRoundWeight[k - 1]) * (int32_t)(x - b[k]);
+    return (uint32_t)w;
+  };
+  const uint32_t wt = wsum(nw);
+  lo = nunits * wsum(p) / wt;
+  cnt = nunits * wsum(p + 1u) / wt - lo;
+  return cnt > 0u;
+}
+
+// Work split.  Grid of G workgroups (as many as stay resident); workgroup g owns the units
+// gemv_share gives it, wave w units lo + w, lo + w + 4, ...  A unit is a row tile or (down with
+// ksplit) one of ksplit fixed K-parts of a row tile (unit u: part u / nrt of row tile u mod nrt).
+// Every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the
+// expert's routed tokens; one pass at decode sizes).  A workgroup learns num_active, its expert,
+// segment and first tokens from one round trip (num_active plus the record table).
 // Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups held in one
 // register buffer; each K-group slot is refilled with the next step's K-group (also across tile
 // boundaries) right after its MFMAs, so kGemvKgPerWave - 1 K-groups stay in flight.  Everything
@@ -1190,18 +1200,19 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec));  // [kRecWords]
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
   const uint32_t nrt = a.nrt;
-  // one round trip: this workgroup's work map entry and the record table (the table is staged
-  // through the B area)
-  const uint2 me = a.wgmap[blockIdx.x];
+  // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
+  const uint32_t nsplit = (!GATE_UP && a.ksplit > 1u) ? a.ksplit : 1u;
+  const uint32_t nunits = nrt * nsplit;
+  // one round trip: num_active and the record table (the table is staged through the B area)
+  const uint32_t na = (uint32_t)*a.num_active;
   {
     const uint4 *src = (const uint4 *)a.exrec;
     uint4 *dst = (uint4 *)smem;
     const uint32_t nv = a.nrec * (kRecWords / 4u);
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
-  const uint32_t ai = me.x & 0xFFFFu;
-  if (ai == 0xFFFFu) return;  // workgroup-uniform: no work in this launch
-  const uint32_t part = me.x >> 16, wpe = me.y & 0xFFFFu, ntw = me.y >> 16;  // tiles part + wpe * i, i < ntw
+  uint32_t ai = 0, lo = 0, ntw = 0;  // active slot, units lo .. lo + ntw - 1
+  if (!gemv_share(blockIdx.x, gridDim.x, na, nunits, a.num_cus, ai, lo, ntw)) return;  // workgroup-uniform
   __syncthreads();
   const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
@@ -1214,11 +1225,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2;
   const uint32_t tail = a.nb - 4u * (nkg - 1u);
-  // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
-  const uint32_t nsplit = (!GATE_UP && a.ksplit > 1u) ? a.ksplit : 1u;
   const uint32_t H = (nkg + nsplit - 1u) / nsplit;  // K-groups per unit
   const uint32_t nst = (H + CJ - 1u) / CJ;           // steps per unit
-  const uint32_t nunits = nrt * nsplit;
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
   auto unit_h = [&](uint32_t u) { return nsplit == 1u ? 0u : u / nrt; };
@@ -1313,9 +1321,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
   };
 
-  // this wave's units: part + wpe * i for i = wv, wv + 4, ... < ntw (first unit clamped into the
+  // this wave's units: lo + i for i = wv, wv + 4, ... < ntw (first unit clamped into the
   // expert for the start-up loads of a wave without units)
-  const uint32_t my_first = part + wpe * wv, tstride = 4u * wpe;
+  const uint32_t my_first = lo + wv, tstride = 4u;
   const uint32_t my_tiles = wv < ntw ? (ntw - wv + 3u) / 4u : 0u;
   const uint32_t first_c = min(my_first, nunits - 1u);
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
@@ -1610,6 +1618,8 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
+  const uint64_t nunits = (uint64_t)a.nrt * (!gate_up && a.ksplit > 1u ? a.ksplit : 1u);
+  if (grid == 0 || nunits * kRoundWeight[0] * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
   const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
   if (nt == 1) {

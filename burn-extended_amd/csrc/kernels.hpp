@@ -45,22 +45,10 @@ struct TopkArgs {
 constexpr uint32_t kRecWords = 32;
 constexpr uint32_t kRecTokens = 14;
 
-// Work map of an expert GEMV launch, written by the routing kernels once num_active is known:
-// entry g (workgroup g of a grid of G) = {slot | part << 16, wpe | ntiles << 16}: workgroup g
-// serves active slot g / wpe (wpe = max(1, min(G / num_active, nrt))) as its part-th workgroup
-// and owns that expert's row tiles part, part + wpe, ... (ntiles of them), so the workgroups of
-// an expert sweep its weights together, a window of about wpe tiles; slot 0xFFFF = no work.
-// Gate_up and down maps are stored back to back.
-struct GemvMaps {
-  uint2 *map;      // [g1 + g2]
-  uint32_t g1, nrt1, g2, nrt2;
-};
-
 struct DispatchArgs {
   const int32_t *topk_idx;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;     // [E, kRecWords]
-  GemvMaps maps;      // map == null: none written
   int32_t *tile_off;  // [E + 1] prefix of ceil(M_e / kGemmTok), or null
   int32_t *chunk_cnt; // [ceil(n / kDispatchChunk), E] scratch of the multi-workgroup dispatch
   uint32_t n, K, E;
@@ -82,7 +70,7 @@ struct GemvArgs {
   const int32_t *seg_off, *active, *num_active, *perm;
   const int32_t *exrec;   // [E, kRecWords] per-active-expert records
   uint32_t nrec;          // records loaded: min(E, n * topk), every slot that can be active
-  const uint2 *wgmap;     // [gridDim.x] work map of this launch
+  uint32_t num_cus;       // CUs of the device (dispatch rounds of the grid, see gemv_share)
   uint32_t topk;
   // B operand rows: gate_up xn [n, Kp] (x dtype), down act [n*k, Kp] f32 (segment order)
   const void *brows;
@@ -103,7 +91,6 @@ struct SmallRouteArgs {
   float *topk_w;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
   int32_t *exrec;    // [E, kRecWords]
-  GemvMaps maps;
   uint32_t n, E, K;
 };
 
@@ -190,6 +177,8 @@ constexpr uint32_t kDispatchThreads = 1024;
 constexpr uint32_t kDispatchChunk = 256;           // dispatch_wide_kernel: tokens per workgroup
 constexpr uint32_t kDispatchWideMinTokens = 1024;  // dispatch_wide_kernel from this batch size on
 constexpr uint32_t kGemvThreads = 256;
+// relative shares of the expert GEMV workgroups of dispatch rounds 0..3 (see gemv_share)
+constexpr uint32_t kRoundWeight[4] = {20, 16, 11, 8};
 constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert GEMV (decode-sized batches; 3, 4 and 6 measured slower)
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;

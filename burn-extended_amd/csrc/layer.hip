@@ -216,7 +216,7 @@ bool check_desc(const burnext_mxfp4_desc *d, uint64_t E, uint64_t rows, uint64_t
 
 // Expert GEMV launch shape for n tokens: token rows staged per pass and the persistent grid (as
 // many workgroups as stay resident: LDS-limited, at most 4 per CU, at least one per possible
-// active expert; the work map gives each active expert grid / num_active of them).
+// active expert; the kernel splits it among the active experts, gemv_share).
 struct GemvCfg {
   uint32_t mt, grid, nrec;
 };
@@ -237,12 +237,9 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   return c;
 }
 
-// Upper bound of gemv_cfg().grid over n (work map entries per launch).
-uint64_t gemv_max_grid(const burnext_moe_layer &L) { return std::max<uint64_t>(L.E, 4ull * L.num_cus); }
-
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
-  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, wgmap, perm, pos_of, xn, act, ypart, dcnt, total;
+  uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, xn, act, ypart, dcnt, total;
   uint64_t tile_off, xq[4], aq[4];  // grouped-GEMM path: tile prefix, xq / act rows (hi lo shi slo)
   bool gemm;                        // the grouped-GEMM regions are present
 };
@@ -270,7 +267,6 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   w.topk_w = take(nk * 4);
   w.meta = take((2ull * L.E + 2) * 4);
   w.exrec = take((uint64_t)L.E * kRecWords * 4);
-  w.wgmap = take(2ull * gemv_max_grid(L) * 8);
   w.perm = take(nk * 4);
   w.pos_of = take(nk * 4);
   w.gemm = n >= kGemmMinTokens;
@@ -303,7 +299,6 @@ struct WsPtrs {
   float *topk_w;
   int32_t *seg_off, *active, *num_active, *perm, *pos_of;
   int32_t *exrec;
-  uint2 *wgmap;
   void *xn;
   float *act, *ypart;
   int32_t *tile_off;
@@ -323,7 +318,6 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.num_active = p.active + L.E;
   p.exrec = (int32_t *)(b + w.exrec);
   p.xn = b + w.xn;
-  p.wgmap = (uint2 *)(b + w.wgmap);
   if (w.gemm) {
     p.tile_off = (int32_t *)(b + w.tile_off);
     p.xq = QRows{b + w.xq[0], b + w.xq[1], b + w.xq[2], b + w.xq[3], qrow_bytes(L.w1)};
@@ -409,9 +403,8 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
 }
 
 burnext_status run_small_route(burnext_moe_layer *L, uint64_t n, const WsPtrs &p, const float *logits,
-                               int32_t *topk_idx, float *topk_w, const GemvMaps &maps, hipStream_t s) {
+                               int32_t *topk_idx, float *topk_w, hipStream_t s) {
   SmallRouteArgs a{};
-  a.maps = maps;
   a.logits = logits;
   a.exrec = p.exrec;
   a.topk_idx = topk_idx;
@@ -442,10 +435,9 @@ burnext_status run_topk(burnext_moe_layer *L, uint64_t n, const float *logits, i
 
 burnext_status run_dispatch(burnext_moe_layer *L, uint64_t n, const int32_t *idx, int32_t *seg_off, int32_t *perm,
                             int32_t *pos_of, int32_t *active, int32_t *num_active, int32_t *exrec,
-                            const GemvMaps &maps, int32_t *chunk_cnt, hipStream_t s, int32_t *tile_off = nullptr) {
+                            int32_t *chunk_cnt, hipStream_t s, int32_t *tile_off = nullptr) {
   DispatchArgs da{};
   da.chunk_cnt = chunk_cnt;
-  da.maps = maps;
   da.tile_off = tile_off;
   da.exrec = exrec;
   da.topk_idx = idx;
@@ -520,7 +512,7 @@ burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64
   burnext_status st = run_router(L, x, xb, n, norm, p.rms, p.logits, nullptr, s, &p.xq);
   if (st == BURNEXT_OK) st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
   if (st == BURNEXT_OK)
-    st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, p.dcnt, s,
+    st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s,
                       p.tile_off);
   if (st != BURNEXT_OK) return st;
   const uint64_t nk = n * L->K;
@@ -742,15 +734,14 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   // work units, so the units of a batch are a fraction of a tile each and spread evenly over the
   // waves)
   const uint32_t ksplit = n < kGemmMinTokens ? std::min<uint32_t>(kDownSplit, (L->w2.nb + 3u) / 4u) : 1u;
-  const GemvMaps maps{p.wgmap, cfg_up.grid, L->w1.nrt, cfg_dn.grid, L->w2.nrt * ksplit};
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, maps, s);
+    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
   } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
-      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, maps, p.dcnt, s);
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
   }
   if (st != BURNEXT_OK) return st;
 
@@ -781,7 +772,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.alpha = L->alpha;
     g.limit = L->limit;
     g.nrec = cf.nrec;
-    g.wgmap = p.wgmap + (gate_up ? 0 : cfg_up.grid);
+    g.num_cus = (uint32_t)L->num_cus;
     if (!gate_up && ksplit > 1u) {
       g.ksplit = ksplit;
       g.out_half = n * L->K * L->Dp;
@@ -819,7 +810,7 @@ burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_d
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, lg, nullptr, s)
                                   : run_router(L, x, xb, n, norm, p.rms, lg, nullptr, s);
   if (st == BURNEXT_OK)
-    st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, GemvMaps{}, s)
+    st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, s)
                                    : run_topk(L, n, lg, topk_idx, topk_w, s);
   return st == BURNEXT_OK ? ok() : st;
 }
@@ -836,7 +827,7 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
-  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, GemvMaps{}, p.dcnt, s);
+  st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
   return st == BURNEXT_OK ? ok() : st;
 }
 
