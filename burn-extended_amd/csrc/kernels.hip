@@ -1149,12 +1149,14 @@ __device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
 // Share of workgroup g of a grid of G among na active experts of nunits work units each: active
 // slot ai = g mod na, as its p-th workgroup (p = g / na), owns the contiguous units
 // [lo, lo + cnt).  The shares of a slot's workgroups are weighted by dispatch round r =
-// min(g / num_cus, 3) (kRoundWeight): workgroups are placed on the CUs round by round, and the
+// min(g / num_cus, 3) (kRoundWeight, per projection): workgroups are placed on the CUs round by round, and the
 // later ones share their CU with older ones that the memory system serves first.  32-bit
-// arithmetic: nunits * kRoundWeight[0] * G < 2^32 (checked at launch).  Returns false when the
+// arithmetic: nunits * (round-0 weight) * G < 2^32 (checked at launch).  Returns false when the
 // workgroup has no units.
+template <bool GATE_UP>
 __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, uint32_t nunits, uint32_t num_cus,
                                            uint32_t &ai, uint32_t &lo, uint32_t &cnt) {
+  constexpr const uint32_t *wr = kRoundWeight[GATE_UP ? 0 : 1];
   if (na == 0u || na > G) return false;
   ai = g % na;
   const uint32_t p = g / na, nw = (G - 1u - ai) / na + 1u;  // part index, workgroups of slot ai
@@ -1165,10 +1167,10 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
     b[k] = kc <= ai ? 0u : (kc - ai + na - 1u) / na;
   }
   auto wsum = [&](uint32_t x) {  // weights of parts 0 .. x-1
-    int32_t w = (int32_t)(kRoundWeight[0] * x);
+    int32_t w = (int32_t)(wr[0] * x);
 #pragma unroll
     for (uint32_t k = 1; k < 4; ++k)
-      if (x > b[k]) w += ((int32_t)kRoundWeight[k] - (int32_t)kRoundWeight[k - 1]) * (int32_t)(x - b[k]);
+      if (x > b[k]) w += ((int32_t)wr[k] - (int32_t)wr[k - 1]) * (int32_t)(x - b[k]);
     return (uint32_t)w;
   };
   const uint32_t wt = wsum(nw);
@@ -1212,7 +1214,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
   uint32_t ai = 0, lo = 0, ntw = 0;  // active slot, units lo .. lo + ntw - 1
-  if (!gemv_share(blockIdx.x, gridDim.x, na, nunits, a.num_cus, ai, lo, ntw)) return;  // workgroup-uniform
+  if (!gemv_share<GATE_UP>(blockIdx.x, gridDim.x, na, nunits, a.num_cus, ai, lo, ntw)) return;  // workgroup-uniform
   __syncthreads();
   const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
@@ -1619,7 +1621,7 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
 
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
   const uint64_t nunits = (uint64_t)a.nrt * (!gate_up && a.ksplit > 1u ? a.ksplit : 1u);
-  if (grid == 0 || nunits * kRoundWeight[0] * grid >= (1ull << 32)) return hipErrorInvalidValue;
+  if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
   const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
   if (nt == 1) {

@@ -177,8 +177,9 @@ constexpr uint32_t kDispatchThreads = 1024;
 constexpr uint32_t kDispatchChunk = 256;           // dispatch_wide_kernel: tokens per workgroup
 constexpr uint32_t kDispatchWideMinTokens = 1024;  // dispatch_wide_kernel from this batch size on
 constexpr uint32_t kGemvThreads = 256;
-// relative shares of the expert GEMV workgroups of dispatch rounds 0..3 (see gemv_share)
-constexpr uint32_t kRoundWeight[4] = {20, 16, 11, 8};
+// relative shares of the expert GEMV workgroups of dispatch rounds 0..3 (see gemv_share), gate_up
+// and down (measured: flatter weights for down, where the K-halves already even out the waves)
+constexpr uint32_t kRoundWeight[2][4] = {{20, 10, 4, 2}, {20, 16, 11, 8}};
 constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert GEMV (decode-sized batches; 3, 4 and 6 measured slower)
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
