@@ -1180,7 +1180,8 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 }
 
 // Work split.  Grid of G workgroups (as many as stay resident); workgroup g owns the units
-// gemv_share gives it, wave w units lo + w, lo + w + 4, ...  A unit is a row tile or (down with
+// gemv_share gives it (decode-sized batches) or a strided share (units part + wpe * i of slot
+// g / wpe, larger batches), wave w every 4th of them from its w-th.  A unit is a row tile or (down with
 // ksplit) one of ksplit fixed K-parts of a row tile (unit u: part u / nrt of row tile u mod nrt).
 // Every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the
 // expert's routed tokens; one pass at decode sizes).  A workgroup learns num_active, its expert,
@@ -1192,8 +1193,9 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // refills: loads complete in order, so waiting for those never waits for the prefetch.
 // At start-up the B operand's staging loads are issued before the first weight loads for the same
 // reason.  No branch surrounds a weight load.
-template <int NT, bool GATE_UP, typename XT>
+template <int NT, bool GATE_UP, typename XT, int SPLIT>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
+  static_assert(SPLIT >= 1 && (GATE_UP ? SPLIT == 1 : SPLIT <= (int)kDownSplit), "K-parts of down units");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr uint32_t CJ = kGemvKgPerWave;
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
@@ -1203,7 +1205,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
   const uint32_t nrt = a.nrt;
   // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
-  const uint32_t nsplit = (!GATE_UP && a.ksplit > 1u) ? a.ksplit : 1u;
+  constexpr uint32_t nsplit = (uint32_t)SPLIT;  // a.ksplit, fixed at compile time
   const uint32_t nunits = nrt * nsplit;
   // one round trip: num_active and the record table (the table is staged through the B area)
   const uint32_t na = (uint32_t)*a.num_active;
@@ -1213,8 +1215,21 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const uint32_t nv = a.nrec * (kRecWords / 4u);
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
-  uint32_t ai = 0, lo = 0, ntw = 0;  // active slot, units lo .. lo + ntw - 1
-  if (!gemv_share<GATE_UP>(blockIdx.x, gridDim.x, na, nunits, a.num_cus, ai, lo, ntw)) return;  // workgroup-uniform
+  // this workgroup's units: lo + us * i, i < ntw (workgroup-uniform return when it has none)
+  uint32_t ai = 0, lo = 0, ntw = 0, us = 1;
+  if (a.weighted) {
+    if (!gemv_share<GATE_UP>(blockIdx.x, gridDim.x, na, nunits, a.num_cus, ai, lo, ntw)) return;
+  } else {
+    // strided: workgroup g = ai * wpe + part owns units part, part + wpe, ... of slot ai, so an
+    // expert's workgroups sweep its weights together (few pages hot at a time)
+    if (na == 0u) return;
+    const uint32_t wpe = max(1u, min(gridDim.x / na, nunits));
+    ai = blockIdx.x / wpe;
+    if (ai >= na) return;
+    lo = blockIdx.x - ai * wpe;
+    us = wpe;
+    ntw = (nunits - lo + wpe - 1u) / wpe;
+  }
   __syncthreads();
   const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
@@ -1231,7 +1246,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t nst = (H + CJ - 1u) / CJ;           // steps per unit
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
-  auto unit_h = [&](uint32_t u) { return nsplit == 1u ? 0u : u / nrt; };
+  auto unit_h = [&](uint32_t u) { return nsplit == 1u ? 0u : (nsplit == 2u ? (u >= nrt ? 1u : 0u) : u / nrt); };
   auto unit_rt = [&](uint32_t u) { return u - unit_h(u) * nrt; };
 
   // K-group of slot j of step st; lanes outside the tile load the tile's first 16 bytes instead
@@ -1323,9 +1338,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
   };
 
-  // this wave's units: lo + i for i = wv, wv + 4, ... < ntw (first unit clamped into the
+  // this wave's units: lo + us * i for i = wv, wv + 4, ... < ntw (first unit clamped into the
   // expert for the start-up loads of a wave without units)
-  const uint32_t my_first = lo + wv, tstride = 4u;
+  const uint32_t my_first = lo + us * wv, tstride = 4u * us;
   const uint32_t my_tiles = wv < ntw ? (ntw - wv + 3u) / 4u : 0u;
   const uint32_t first_c = min(my_first, nunits - 1u);
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
@@ -1521,12 +1536,14 @@ hipError_t configure_kernels() {
   BX_ATTR((router_rows_kernel<uint16_t, uint16_t>));
   BX_ATTR(topk_kernel);
   BX_ATTR(dispatch_kernel);
-  BX_ATTR((expert_gemv_kernel<1, true, uint16_t>));
-  BX_ATTR((expert_gemv_kernel<1, true, float>));
-  BX_ATTR((expert_gemv_kernel<1, false, float>));
-  BX_ATTR((expert_gemv_kernel<3, true, uint16_t>));
-  BX_ATTR((expert_gemv_kernel<3, true, float>));
-  BX_ATTR((expert_gemv_kernel<3, false, float>));
+  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1>));
+  BX_ATTR((expert_gemv_kernel<1, true, float, 1>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, 1>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit>));
+  BX_ATTR((expert_gemv_kernel<3, true, uint16_t, 1>));
+  BX_ATTR((expert_gemv_kernel<3, true, float, 1>));
+  BX_ATTR((expert_gemv_kernel<3, false, float, 1>));
+  BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplit>));
 #undef BX_ATTR
   return err;
 }
@@ -1624,20 +1641,26 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
   const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
+  if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit) return hipErrorInvalidValue;
+  const bool split = !gate_up && a.ksplit > 1u;
   if (nt == 1) {
-    if (!gate_up)
-      expert_gemv_kernel<1, false, float><<<g, block, lds, s>>>(a);
+    if (split)
+      expert_gemv_kernel<1, false, float, kDownSplit><<<g, block, lds, s>>>(a);
+    else if (!gate_up)
+      expert_gemv_kernel<1, false, float, 1><<<g, block, lds, s>>>(a);
     else if (x_bf16)
-      expert_gemv_kernel<1, true, uint16_t><<<g, block, lds, s>>>(a);
+      expert_gemv_kernel<1, true, uint16_t, 1><<<g, block, lds, s>>>(a);
     else
-      expert_gemv_kernel<1, true, float><<<g, block, lds, s>>>(a);
+      expert_gemv_kernel<1, true, float, 1><<<g, block, lds, s>>>(a);
   } else if (nt == 3) {
-    if (!gate_up)
-      expert_gemv_kernel<3, false, float><<<g, block, lds, s>>>(a);
+    if (split)
+      expert_gemv_kernel<3, false, float, kDownSplit><<<g, block, lds, s>>>(a);
+    else if (!gate_up)
+      expert_gemv_kernel<3, false, float, 1><<<g, block, lds, s>>>(a);
     else if (x_bf16)
-      expert_gemv_kernel<3, true, uint16_t><<<g, block, lds, s>>>(a);
+      expert_gemv_kernel<3, true, uint16_t, 1><<<g, block, lds, s>>>(a);
     else
-      expert_gemv_kernel<3, true, float><<<g, block, lds, s>>>(a);
+      expert_gemv_kernel<3, true, float, 1><<<g, block, lds, s>>>(a);
   } else {
     return hipErrorInvalidValue;
   }

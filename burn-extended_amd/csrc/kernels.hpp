@@ -71,6 +71,7 @@ struct GemvArgs {
   const int32_t *exrec;   // [E, kRecWords] per-active-expert records
   uint32_t nrec;          // records loaded: min(E, n * topk), every slot that can be active
   uint32_t num_cus;       // CUs of the device (dispatch rounds of the grid, see gemv_share)
+  uint32_t weighted;      // 1: gemv_share's contiguous round-weighted shares; 0: strided shares
   uint32_t topk;
   // B operand rows: gate_up xn [n, Kp] (x dtype), down act [n*k, Kp] f32 (segment order)
   const void *brows;

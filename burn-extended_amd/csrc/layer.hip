@@ -284,9 +284,9 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[2] = take(nk * ka / 32);
     w.aq[3] = take(nk * ka / 32);
   }
-  // expert GEMV batches (n < kGemmMinTokens) split the down projection's K range in up to
-  // kDownSplit parts: a partial-sum buffer each
-  w.ypart = take(nk * L.Dp * 4 * (n < kGemmMinTokens ? kDownSplit : 1));
+  // decode-sized batches split the down projection's K range in up to kDownSplit parts: a
+  // partial-sum buffer each
+  w.ypart = take(nk * L.Dp * 4 * (n <= kSmallRouteMaxTokens ? kDownSplit : 1));
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   w.total = off;
   return w;
@@ -730,10 +730,10 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   }
   const int nt = xb ? 1 : 3;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
-  // down projection: every row tile's K range in ksplit fixed parts of whole K-groups (separate
-  // work units, so the units of a batch are a fraction of a tile each and spread evenly over the
-  // waves)
-  const uint32_t ksplit = n < kGemmMinTokens ? std::min<uint32_t>(kDownSplit, (L->w2.nb + 3u) / 4u) : 1u;
+  // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
+  // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
+  // evenly over the waves; measured slower from 64 tokens on)
+  const uint32_t ksplit = (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
@@ -773,6 +773,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     g.limit = L->limit;
     g.nrec = cf.nrec;
     g.num_cus = (uint32_t)L->num_cus;
+    g.weighted = n <= kSmallRouteMaxTokens ? 1u : 0u;  // measured: strided shares faster from 64 tokens on
     if (!gate_up && ksplit > 1u) {
       g.ksplit = ksplit;
       g.out_half = n * L->K * L->Dp;
