@@ -49,6 +49,15 @@ constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
 // stay in flight: __syncthreads() would wait for every outstanding load (its fence covers the
 // direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
 // accesses across.
+// Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four lane groups q of a token column), by
+// the permlane swaps between rows 16 and 32 lanes apart.
+__device__ __forceinline__ float max_lanes_16_32(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto p2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p2[0]), __uint_as_float(p2[1]));
+}
+
 __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
@@ -60,8 +69,11 @@ __device__ __forceinline__ void ring_barrier() {
 size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64; }
 
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
-// take a contiguous run of items, then item = token tile gt * nrb + row block rb (rb fastest):
-// the workgroups sharing a token tile's B run together on one XCD.  A workgroup (8 waves, one
+// take a contiguous run of Q = ceil(N / 8) of the N realised items (N = nrb * token tiles, read
+// from tile_off[E]; the grid is sized for the most tiles routing can produce, and sizing the runs
+// by the grid left the last XCD a small remainder while the other seven did all the work), then
+// item = token tile gt * nrb + row block rb (rb fastest): the workgroups sharing a token tile's B
+// run together on one XCD.  A workgroup (8 waves, one
 // per CU) computes kGemmRows weight rows (16 row tiles) x kGemmTok tokens; wave w computes rows
 // 64 (w / 2) .. and tokens 64 (w % 2) .. (4 x 4 MFMA tiles, two terms each).  K-groups stream
 // through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (56 wave
@@ -73,8 +85,10 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   int32_t *slot_l = rows_l + kGemmTok;                     // [kGemmTok] down: slot
   int32_t *info_l = slot_l + kGemmTok;                     // [0] expert [1] tile of it
 
-  const uint32_t G = gridDim.x, b = blockIdx.x;
-  const uint32_t it = (b & 7u) * (G >> 3) + (b >> 3);  // G is a multiple of 8
+  const uint32_t b = blockIdx.x;
+  const uint32_t N = a.nrb * (uint32_t)a.tile_off[a.E], Q = (N + 7u) / 8u;  // 8 * Q <= gridDim.x
+  const uint32_t it = (b & 7u) * Q + (b >> 3);
+  if ((b >> 3) >= Q || it >= N) return;  // workgroup-uniform: no item
   const uint32_t gt = it / a.nrb, rb = it - gt * a.nrb;
   if (threadIdx.x == 0) info_l[0] = -1;
   __syncthreads();
@@ -208,6 +222,15 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     }
   };
 
+  // the epilogue's bias rows (4 row tiles of this wave), requested before the first stage so that
+  // they have long arrived when the K-loop ends (loads complete in order: the first stage wait
+  // covers them)
+  f32x4_t bias4[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
+    bias4[rt] = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
+  }
   stage(0, 0);
   stage(min(1u, nkg - 1u), 1);
   __builtin_amdgcn_s_waitcnt(vmcnt_only(7));  // stage 0 landed (this wave issued 7 after it)
@@ -248,7 +271,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       for (int rt = 0; rt < 4; ++rt) {
         const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;  // W1 row
         const bool rv = rb * kRowTiles + wr * 4u + (uint32_t)rt < a.nrt;
-        const f32x4_t bb = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
+        const f32x4_t bb = bias4[rt];
         const uint32_t f0 = fb + (uint32_t)rt * 8u + 2u * q;
         float v0 = swiglu_clamp_f(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1], a.alpha, a.limit);
         float v1 = swiglu_clamp_f(acc[rt][tt][2] + bb[2], acc[rt][tt][3] + bb[3], a.alpha, a.limit);
@@ -258,8 +281,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         o[2 * rt + 1] = v1;
         amax = fmaxf(amax, fmaxf(fabsf(v0), fabsf(v1)));
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+      amax = max_lanes_16_32(amax);
       const uint32_t sbh = mx8_scale_byte(amax);
       const float ih = sbh ? mx8_inv_scale(sbh) : 0.0f, sh = e8m0_to_f32(sbh);
       uint32_t ch[4];
@@ -271,8 +293,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         res[2 * k + 1] = o[2 * k + 1] - fp8_to_f32<1>(ch[k]) * sh;
         rmax = fmaxf(rmax, fmaxf(fabsf(res[2 * k]), fabsf(res[2 * k + 1])));
       }
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+      rmax = max_lanes_16_32(rmax);
       const uint32_t sbl = mx8_scale_byte(rmax);
       const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
       if (tok < ntok) {
@@ -315,7 +336,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       for (int rt = 0; rt < 4; ++rt) {
         if (rb * kRowTiles + wr * 4u + (uint32_t)rt >= a.nrt) continue;
         const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
-        const f32x4_t bb = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + r0);
+        const f32x4_t bb = bias4[rt];
         if (r0 + 3u < a.out_rows) {
           *(float4 *)(orow + r0) = make_float4(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1],
                                                acc[rt][tt][2] + bb[2], acc[rt][tt][3] + bb[3]);
