@@ -49,6 +49,16 @@ constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
 // stay in flight: __syncthreads() would wait for every outstanding load (its fence covers the
 // direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
 // accesses across.
+// Clamped SwiGLU with the hardware exp2 and reciprocal (about 1 ulp each): the epilogue feeds it
+// straight into the two-term MXFP8 quantisation (2^-8-level), so the precise expf and division
+// of swiglu_clamp_f would only cost VALU time there.
+__device__ __forceinline__ float swiglu_clamp_fast(float g, float l, float alpha, float limit) {
+  const float xg = fminf(g, limit);
+  const float xl = fmaxf(-limit, fminf(l, limit));
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * xg));
+  return (xg * sig) * (xl + 1.0f);
+}
+
 // Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four lane groups q of a token column), by
 // the permlane swaps between rows 16 and 32 lanes apart.
 __device__ __forceinline__ float max_lanes_16_32(float v) {
@@ -273,8 +283,8 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         const bool rv = rb * kRowTiles + wr * 4u + (uint32_t)rt < a.nrt;
         const f32x4_t bb = bias4[rt];
         const uint32_t f0 = fb + (uint32_t)rt * 8u + 2u * q;
-        float v0 = swiglu_clamp_f(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1], a.alpha, a.limit);
-        float v1 = swiglu_clamp_f(acc[rt][tt][2] + bb[2], acc[rt][tt][3] + bb[3], a.alpha, a.limit);
+        float v0 = swiglu_clamp_fast(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1], a.alpha, a.limit);
+        float v1 = swiglu_clamp_fast(acc[rt][tt][2] + bb[2], acc[rt][tt][3] + bb[3], a.alpha, a.limit);
         v0 = (rv && f0 < a.act_feats) ? v0 : 0.0f;
         v1 = (rv && f0 + 1u < a.act_feats) ? v1 : 0.0f;
         o[2 * rt] = v0;
