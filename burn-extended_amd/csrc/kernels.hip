@@ -1447,30 +1447,52 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 // down projection already wrote yslot = down_p + b2[e_p] token-major.  Every load of a thread is
 // independent of the others (one memory round trip); four outputs per thread.
 // ---------------------------------------------------------------------------------------------
-template <typename XT>
+template <typename XT, int NP>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const uint32_t t = blockIdx.y;
   const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4u;
   if (d0 >= a.D) return;
   const uint32_t nv = min(4u, a.D - d0);
   const XT *x = (const XT *)a.x;
-  float xv[4];
+  // four whole values (D % 4 == 0, 16-byte aligned x and y): one 8- or 16-byte access for x and y
+  const bool vec = nv == 4u && (a.D & 3u) == 0u && (((uintptr_t)a.x | (uintptr_t)a.y) & 15u) == 0u;
+  float xv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.add_residual && vec) {
+    const XT *xp = x + (size_t)t * a.D + d0;
+    if constexpr (sizeof(XT) == 2) {
+      const uint2 r = *(const uint2 *)xp;
+      xv[0] = bf16_bits_to_f32((uint16_t)r.x);
+      xv[1] = bf16_bits_to_f32((uint16_t)(r.x >> 16));
+      xv[2] = bf16_bits_to_f32((uint16_t)r.y);
+      xv[3] = bf16_bits_to_f32((uint16_t)(r.y >> 16));
+    } else {
+      const float4 r = *(const float4 *)xp;
+      xv[0] = r.x;
+      xv[1] = r.y;
+      xv[2] = r.z;
+      xv[3] = r.w;
+    }
+  } else if (a.add_residual) {
 #pragma unroll
-  for (uint32_t j = 0; j < 4u; ++j) xv[j] = (a.add_residual && j < nv) ? load_val(x, (size_t)t * a.D + d0 + j) : 0.0f;
+    for (uint32_t j = 0; j < 4u; ++j) xv[j] = j < nv ? load_val(x, (size_t)t * a.D + d0 + j) : 0.0f;
+  }
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (uint32_t p0 = 0; p0 < a.K; p0 += 8u) {
     float wv[8];
-    float4 yv[8];
+    float4 yv[8], yh[NP > 1 ? NP - 1 : 1][8];
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
       const uint32_t p = min(p0 + u, a.K - 1u);
       wv[u] = a.topk_w[(size_t)t * a.K + p];
       yv[u] = *(const float4 *)(a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 4 == 0, d0 < Dp
-      for (uint32_t h = 1; h < a.nparts; ++h) {
-        const float4 y2 = *(const float4 *)(a.ypart + h * a.part_stride + ((size_t)t * a.K + p) * a.Dp + d0);
-        yv[u] = make_float4(yv[u].x + y2.x, yv[u].y + y2.y, yv[u].z + y2.z, yv[u].w + y2.w);
-      }
+#pragma unroll
+      for (int h = 1; h < NP; ++h) yh[h - 1][u] = *(const float4 *)(a.ypart + h * a.part_stride + ((size_t)t * a.K + p) * a.Dp + d0);
     }
+#pragma unroll
+    for (int h = 1; h < NP; ++h)
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u)
+        yv[u] = make_float4(yv[u].x + yh[h - 1][u].x, yv[u].y + yh[h - 1][u].y, yv[u].z + yh[h - 1][u].z, yv[u].w + yh[h - 1][u].w);
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
       if (p0 + u >= a.K) break;
@@ -1481,7 +1503,17 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
   }
   XT *y = (XT *)a.y;
-  for (uint32_t j = 0; j < nv; ++j) store_val(y, (size_t)t * a.D + d0 + j, xv[j] + acc[j]);
+  if (vec) {
+    XT *yp = y + (size_t)t * a.D + d0;
+    if constexpr (sizeof(XT) == 2) {
+      *(uint2 *)yp = make_uint2((uint32_t)f32_to_bf16_bits(xv[0] + acc[0]) | ((uint32_t)f32_to_bf16_bits(xv[1] + acc[1]) << 16),
+                                (uint32_t)f32_to_bf16_bits(xv[2] + acc[2]) | ((uint32_t)f32_to_bf16_bits(xv[3] + acc[3]) << 16));
+    } else {
+      *(float4 *)yp = make_float4(xv[0] + acc[0], xv[1] + acc[1], xv[2] + acc[2], xv[3] + acc[3]);
+    }
+  } else {
+    for (uint32_t j = 0; j < nv; ++j) store_val(y, (size_t)t * a.D + d0 + j, xv[j] + acc[j]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1669,10 +1701,18 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
 
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
-  if (x_bf16)
-    combine_kernel<uint16_t><<<grid, block, 0, s>>>(a);
-  else
-    combine_kernel<float><<<grid, block, 0, s>>>(a);
+  if (a.nparts != 1u && a.nparts != kDownSplit) return hipErrorInvalidValue;
+  if (a.nparts == 1u) {
+    if (x_bf16)
+      combine_kernel<uint16_t, 1><<<grid, block, 0, s>>>(a);
+    else
+      combine_kernel<float, 1><<<grid, block, 0, s>>>(a);
+  } else {
+    if (x_bf16)
+      combine_kernel<uint16_t, kDownSplit><<<grid, block, 0, s>>>(a);
+    else
+      combine_kernel<float, kDownSplit><<<grid, block, 0, s>>>(a);
+  }
   return hipGetLastError();
 }
 
