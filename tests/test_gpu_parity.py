@@ -211,6 +211,30 @@ def test_forward_tiny_f32(M, oracle, layout, ue8):
     assert err <= TOL_F32
 
 
+@pytest.mark.parametrize("dtype,n", [("bf16", 5), ("f32", 20)])
+def test_forward_odd_width_unaligned_rows(M, oracle, dtype, n):
+    """D = 202 (not a multiple of 4 or 8) and x / y rows that start 1 element past an aligned
+    address: the element-wise paths of the router and combine, against the oracle."""
+    from burnext_amd import synth
+    print(f"odd width dtype={dtype} n={n}", flush=True)
+    D = 202
+    L = _make(synth, D, 64, 4, 2, seed=4, dtype=dtype)
+    x = synth.make_tokens(n, D, seed=6, dtype=dtype)
+    ref = M.to_device_x(x, dtype).reshape(-1)
+    xb = torch.empty(ref.numel() + 1, dtype=ref.dtype, device=ref.device)
+    xb[1:] = ref
+    xt = xb[1:].view(n, D)
+    yb = torch.empty_like(xb)
+    yt = yb[1:].view(n, D)
+    layer = M.MoeLayer(L)
+    layer.forward(xt, out=yt)
+    torch.cuda.synchronize()
+    y_ref, _, _ = oracle.moe_forward(L, x)
+    err = oracle.max_abs_rel(_np(yt), y_ref)
+    layer.close()
+    assert err <= (TOL_F32 if dtype == "f32" else TOL_BF16), err
+
+
 @pytest.mark.parametrize("flags", [0, 1, 2, 3])
 def test_forward_flags_f32(M, oracle, flags):
     from burnext_amd import synth
