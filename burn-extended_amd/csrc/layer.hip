@@ -225,15 +225,21 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   const TiledMx &t = gate_up ? L.w1 : L.w2;
   GemvCfg c{};
   const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
-  // LDS rows reserved for one token pass: 8 at decode sizes and whenever routing leaves at most 4
-  // tokens per expert on average (3 workgroups per CU at D = 2880; a segment above 8 tokens takes a
-  // second pass over its expert's weights), 16 for larger batches (1 workgroup per CU).  Measured:
-  // 120B T = 64 (2 tokens per expert) 478 -> 373 us per step with 8.
-  const bool small_segments = n <= 16 || n * L.K <= 4ull * L.E;
-  uint32_t mt = (uint32_t)std::min<uint64_t>(small_segments ? 8 : 16, n);
-  c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
+  // LDS rows reserved for one token pass (a segment with more tokens takes another pass over its
+  // expert's weights): 8 at decode sizes and whenever routing leaves at most 4 tokens per expert on
+  // average (3 workgroups per CU at D = 2880), else the most that still lets 2 workgroups share a
+  // CU (14 at D = 2880), at most 16.  Memory parallelism beats the extra passes (measured, per
+  // step: 120B T = 64 478 -> 373 us with 8 instead of 16; 20B T = 64 / 128 / 200 282 / 292 / 410
+  // -> 192 / 243 / 335 us with 14 instead of 16).
   const uint64_t max_active = std::min<uint64_t>(L.E, n * L.K);
   c.nrec = (uint32_t)max_active;
+  const bool small_segments = n <= 16 || n * L.K <= 4ull * L.E;
+  uint32_t mt = 8;
+  if (!small_segments)
+    for (mt = 16; mt > 8 && gemv_total_lds_bytes(nt, mt, t.nb, c.nrec) > 80 * 1024; --mt) {
+    }
+  mt = (uint32_t)std::min<uint64_t>(mt, n);
+  c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
   const size_t lds = gemv_total_lds_bytes(nt, c.mt, t.nb, c.nrec);
   const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, (160 * 1024) / std::max<size_t>(lds, 1)));
   c.grid = (uint32_t)std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L.num_cus * per_cu, max_active * t.nrt));
