@@ -253,10 +253,17 @@ struct WsLayout {
   bool gemm;                        // the grouped-GEMM regions are present
 };
 
-// bf16 batches of at least this many tokens run the grouped GEMM (expert segments of ~n*k/E
-// tokens fill its 128-token tiles); smaller ones, and every f32 batch (the GEMM's two MXFP8
-// terms carry bf16-level precision), run the expert GEMVs.
-constexpr uint64_t kGemmMinTokens = 256;
+// bf16 batches of at least kGemmMinTokens tokens with at least kGemmMinPerExpert routed tokens per
+// expert on average run the grouped GEMM (its 128-token tiles are then mostly full); the others,
+// and every f32 batch (the GEMM's two MXFP8 terms carry bf16-level precision), run the expert
+// GEMVs.  Measured crossover (per step): 20B (E = 32) GEMV 192 / 243 / 335 us against GEMM 242 /
+// 243 / 246 us at 64 / 128 / 200 tokens; 120B (E = 128) GEMV 489 / 435 us against GEMM 755 / 761
+// us at 128 / 200 tokens.
+constexpr uint64_t kGemmMinTokens = 128;
+constexpr uint64_t kGemmMinPerExpert = 16;
+inline bool use_gemm_path(const burnext_moe_layer &L, uint64_t n) {
+  return n >= kGemmMinTokens && n * L.K >= kGemmMinPerExpert * L.E;
+}
 
 // Row bytes of two-term MXFP8 rows over K = cols of a tiled projection (whole 128-wide K-groups).
 inline uint32_t qrow_bytes(const TiledMx &t) { return ((t.nb + 3u) / 4u) * 128u; }
@@ -278,7 +285,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   w.exrec = take((uint64_t)L.E * kRecWords * 4);
   w.perm = take(nk * 4);
   w.pos_of = take(nk * 4);
-  w.gemm = n >= kGemmMinTokens;
+  w.gemm = use_gemm_path(L, n);
   w.xn = take(n * L.Dp * 4);  // normalised rows, x dtype (f32 size covers both)
   w.act = take(nk * L.Fp * 4);
   if (w.gemm) {
@@ -514,7 +521,7 @@ burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, ui
   return st == BURNEXT_OK ? ok() : st;
 }
 
-// Grouped-GEMM path (n >= kGemmMinTokens): router (+ two-term MXFP8 rows of xn), top-k,
+// Grouped-GEMM path (use_gemm_path): router (+ two-term MXFP8 rows of xn), top-k,
 // dispatch (+ token-tile prefix), gate_up GEMM (SwiGLU, quantised act rows), down GEMM (slot rows).
 burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64_t n, bool norm, const WsPtrs &p,
                             hipStream_t s) {
