@@ -279,7 +279,6 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       float amax = 0.0f;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;  // W1 row
         const bool rv = rb * kRowTiles + wr * 4u + (uint32_t)rt < a.nrt;
         const f32x4_t bb = bias4[rt];
         const uint32_t f0 = fb + (uint32_t)rt * 8u + 2u * q;

@@ -217,6 +217,71 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     }
   }
 
+  __syncthreads();  // rr visible
+  // normalised rows xn = x * (1/r) * gamma (x without RmsNorm) for the expert GEMV in the x dtype,
+  // zero padded to Dp, and (grouped GEMM) their two-term MXFP8 form zero padded to the K-group
+  // length.  Every expert group shares the writing (chunk or block i of the token block by group
+  // i mod gridDim.y), before the dot products so the stores drain meanwhile.
+  auto gamma8 = [&](uint32_t c0, float g[8]) {  // gamma[c0 .. c0 + 8), ones beyond D
+    if (VEC && c0 < D) {  // D % 8 == 0: the whole chunk is inside
+      const float4 g0 = *(const float4 *)(a.gamma + c0), g1 = *(const float4 *)(a.gamma + c0 + 4);
+      g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w; g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+    } else {
+#pragma unroll
+      for (uint32_t j = 0; j < 8u; ++j) g[j] = c0 + j < D ? a.gamma[c0 + j] : 1.0f;
+    }
+  };
+  const uint32_t wstart = threadIdx.x + blockDim.x * blockIdx.y, wstep = blockDim.x * gridDim.y;
+  if (a.xn) {
+    XT *xn = (XT *)a.xn;
+    const uint32_t cpr = a.Dp / 8u;  // Dp is a multiple of 32
+    for (uint32_t ch = wstart; ch < nh * cpr; ch += wstep) {
+      const uint32_t tt = ch / cpr, c0 = (ch - tt * cpr) * 8u;
+      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
+      float g[8], v[8];
+      if (a.apply_norm) gamma8(c0, g);
+#pragma unroll
+      for (uint32_t j = 0; j < 8u; ++j) {
+        const uint32_t c = c0 + j;
+        float u = 0.0f;
+        if (c < D) {
+          u = xs[(size_t)tt * Dpad + tpos(c)];
+          if (a.apply_norm) u = (u * ir) * g[j];
+        }
+        v[j] = u;
+      }
+      store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
+    }
+  }
+  if (a.xq.hi) {
+    // one 32-value block per thread-iteration
+    const uint32_t nbk = a.xq.kq >> 5;
+    for (uint32_t f = wstart; f < nh * nbk; f += wstep) {
+      const uint32_t tt = f / nbk, bk = f - tt * nbk;
+      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
+      float v[32], amax = 0.0f;
+#pragma unroll
+      for (uint32_t q = 0; q < 4u; ++q) {
+        float g[8];
+        if (a.apply_norm) gamma8(bk * 32u + 8u * q, g);
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) {
+          const uint32_t c = bk * 32u + 8u * q + j;
+          float u = 0.0f;
+          if (c < D) {
+            u = xs[(size_t)tt * Dpad + tpos(c)];
+            if (a.apply_norm) u = (u * ir) * g[j];
+          }
+          v[8u * q + j] = u;
+          amax = fmaxf(amax, fabsf(u));
+        }
+      }
+      const size_t row = t0 + tt;
+      mx8_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * a.xq.kq + bk * 32u,
+                     a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
+    }
+  }
+
   // 3. dot products
   float acc0[8], acc1[8];
 #pragma unroll
@@ -262,53 +327,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     }
     wave_sum_butterfly_n<8>(acc0);
     if (has1) wave_sum_butterfly_n<8>(acc1);
-  }
-  __syncthreads();  // rr visible
-  if (blockIdx.y == 0 && a.xn) {
-    // normalised rows for the expert GEMV: xn = x * (1/r) * gamma (x without RmsNorm) in the
-    // x dtype, zero padded to Dp
-    XT *xn = (XT *)a.xn;
-    const uint32_t cpr = a.Dp / 8u;  // Dp is a multiple of 32
-    for (uint32_t ch = threadIdx.x; ch < nh * cpr; ch += blockDim.x) {
-      const uint32_t tt = ch / cpr, c0 = (ch - tt * cpr) * 8u;
-      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
-      float v[8];
-#pragma unroll
-      for (uint32_t j = 0; j < 8u; ++j) {
-        const uint32_t c = c0 + j;
-        float u = 0.0f;
-        if (c < D) {
-          u = xs[(size_t)tt * Dpad + tpos(c)];
-          if (a.apply_norm) u = (u * ir) * a.gamma[c];
-        }
-        v[j] = u;
-      }
-      store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
-    }
-  }
-  if (blockIdx.y == 0 && a.xq.hi) {
-    // two-term MXFP8 rows of xn for the grouped GEMM: one 32-value block per thread-iteration,
-    // zero beyond D up to the K-group padding
-    const uint32_t nbk = a.xq.kq >> 5;
-    for (uint32_t f = threadIdx.x; f < nh * nbk; f += blockDim.x) {
-      const uint32_t tt = f / nbk, bk = f - tt * nbk;
-      const float ir = a.apply_norm ? 1.0f / rr[tt] : 1.0f;
-      float v[32], amax = 0.0f;
-#pragma unroll
-      for (uint32_t j = 0; j < 32u; ++j) {
-        const uint32_t c = bk * 32u + j;
-        float u = 0.0f;
-        if (c < D) {
-          u = xs[(size_t)tt * Dpad + tpos(c)];
-          if (a.apply_norm) u = (u * ir) * a.gamma[c];
-        }
-        v[j] = u;
-        amax = fmaxf(amax, fabsf(u));
-      }
-      const size_t row = t0 + tt;
-      mx8_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * a.xq.kq + bk * 32u,
-                     a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
-    }
   }
   if (has0 && lane < nh) {
     // lane tt writes token tt's logits (all lanes hold the reduced values)
@@ -727,7 +745,6 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
   constexpr uint32_t W = kDispatchChunk / 32u;  // bitmap words per expert
   __shared__ int32_t call[kMaxExperts], cbef[kMaxExperts], segs[kMaxExperts], aidx[kMaxExperts], base[kMaxExperts];
   __shared__ uint32_t bm[kMaxExperts * W];
-  __shared__ int32_t na_l;
   const uint32_t tid = threadIdx.x, c = blockIdx.x, E = a.E, K = a.K, n = a.n;
   const uint32_t t = c * kDispatchChunk + tid;
   const uint32_t nchunk = gridDim.x;
@@ -775,7 +792,6 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
         if (a.tile_off) a.tile_off[E] = toff + (call[e] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
         const int32_t na = ra + (call[e] > 0);
         *a.num_active = na;
-        na_l = na;
         for (uint32_t e3 = (uint32_t)na; e3 < E; ++e3) a.active[e3] = -1;
       }
     }

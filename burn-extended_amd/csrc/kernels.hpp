@@ -171,7 +171,10 @@ __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, 
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
 constexpr uint32_t kRouterThreads = 256;
-constexpr uint32_t kRouterRowsMinTokens = 512;  // router_rows_kernel from this batch size on
+// router_rows_kernel from this batch size on: its time is one workgroup's pass over all E router
+// rows (37 us at E = 32, 104 us at E = 128, D = 2880) while router_kernel's grows with n * E;
+// measured crossover between 1000 and 1200 tokens for both E
+constexpr uint32_t kRouterRowsMinTokens = 1152;
 constexpr uint32_t kRowsThreads = 512;
 constexpr uint32_t kTopkThreads = 512;
 constexpr uint32_t kDispatchThreads = 1024;
