@@ -313,13 +313,15 @@ def test_forward_prefill_sampled_rows(M, oracle):
 
 
 # ---------------------------------------------------------------------------------------------
-# grouped-GEMM path (bf16 batches of >= 256 tokens): every output row against the oracle
+# grouped-GEMM path (bf16 batches of >= 128 tokens with >= 16 routed tokens per expert on
+# average): every output row against the oracle
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("D,F,E,K,n,layout,ue8,zipf", [
     (256, 256, 4, 2, 300, "interleaved", 0, False),   # partial token tiles, 2 experts per token
     (200, 96, 6, 3, 257, "halves", 14, False),        # K not a multiple of 128 or 32, tail K-groups
     (512, 384, 8, 2, 1024, "interleaved", 0, True),   # skewed segments (multi-tile experts)
     (2880, 2880, 32, 4, 512, "interleaved", 0, False),
+    (2880, 2880, 32, 4, 128, "interleaved", 0, False),  # smallest batch on the GEMM path (n*k = 16 E)
 ])
 def test_forward_gemm_path_all_rows(M, oracle, D, F, E, K, n, layout, ue8, zipf):
     from burnext_amd import synth
