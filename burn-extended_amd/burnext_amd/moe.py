@@ -98,7 +98,7 @@ class MoeLayer:
             _ptr(arrs["w2_blocks"]), _ptr(arrs["w2_scales"]), _ptr(b1), _ptr(b2), dt, _ptr(rw), _ptr(rb), dt,
             _ptr(g), dt, layout, device, ctypes.byref(h)))
         self.handle = h
-        self._ws = None
+        self._ws = {}  # stream handle -> (buffer, bytes, alignment offset)
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
@@ -116,14 +116,20 @@ class MoeLayer:
         N.check(N.lib().burnext_moe_workspace_size(self.handle, n_tokens, ctypes.byref(b)))
         return b.value
 
-    def workspace(self, n_tokens: int) -> torch.Tensor:
-        """A 256-byte-aligned device workspace for n_tokens (cached, grown on demand)."""
+    def workspace(self, n_tokens: int, stream=None) -> torch.Tensor:
+        """A 256-byte-aligned device workspace for n_tokens, cached per stream and grown on demand.
+
+        Calls on one stream reuse it in stream order; another stream gets its own buffer (allocated
+        on that stream), since forwards that run concurrently must not share a workspace."""
+        s = torch.cuda.current_stream(self.device) if stream is None else stream
         need = self.workspace_size(n_tokens)
-        if self._ws is None or self._ws[1] < need:
-            raw = torch.empty(need + 256, dtype=torch.uint8, device=f"cuda:{self.device}")
-            off = (-raw.data_ptr()) % 256
-            self._ws = (raw, need, off)
-        raw, _, off = self._ws
+        cur = self._ws.get(s.cuda_stream)
+        if cur is None or cur[1] < need:
+            with torch.cuda.stream(s):
+                raw = torch.empty(need + 256, dtype=torch.uint8, device=f"cuda:{self.device}")
+            cur = (raw, need, (-raw.data_ptr()) % 256)
+            self._ws[s.cuda_stream] = cur
+        raw, _, off = cur
         return raw[off:off + need]
 
     def forward(self, x: torch.Tensor, flags: int = N.FORWARD_DEFAULT, out: torch.Tensor | None = None,
@@ -131,7 +137,7 @@ class MoeLayer:
         assert x.is_cuda and x.is_contiguous() and x.shape[-1] == self.data.d_model
         n = x.numel() // self.data.d_model
         y = torch.empty_like(x) if out is None else out
-        ws = self.workspace(n) if workspace is None else workspace
+        ws = self.workspace(n, stream) if workspace is None else workspace
         N.check(N.lib().burnext_moe_forward(self.handle, ctypes.c_void_p(x.data_ptr()), _x_dtype(x),
                                             ctypes.c_void_p(y.data_ptr()), n, flags,
                                             ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
@@ -142,7 +148,7 @@ class MoeLayer:
         idx = torch.empty((n, self.k), dtype=torch.int32, device=x.device)
         w = torch.empty((n, self.k), dtype=torch.float32, device=x.device)
         lg = torch.empty((n, self.data.num_experts), dtype=torch.float32, device=x.device)
-        ws = self.workspace(n)
+        ws = self.workspace(n, stream)
         N.check(N.lib().burnext_moe_route(self.handle, ctypes.c_void_p(x.data_ptr()), _x_dtype(x), n, flags,
                                           ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(w.data_ptr()),
                                           ctypes.c_void_p(lg.data_ptr()), ctypes.c_void_p(ws.data_ptr()),
@@ -153,7 +159,7 @@ class MoeLayer:
         n = topk_idx.shape[0]
         seg = torch.empty(self.data.num_experts + 1, dtype=torch.int32, device=topk_idx.device)
         perm = torch.empty(n * self.k, dtype=torch.int32, device=topk_idx.device)
-        ws = self.workspace(n)
+        ws = self.workspace(n, stream)
         N.check(N.lib().burnext_moe_dispatch(self.handle, ctypes.c_void_p(topk_idx.data_ptr()), n,
                                              ctypes.c_void_p(seg.data_ptr()), ctypes.c_void_p(perm.data_ptr()),
                                              ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
