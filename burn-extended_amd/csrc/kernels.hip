@@ -622,6 +622,61 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
   }
 }
 
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
+}
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+// Inclusive prefix sum over the wave's lanes: row_shr 1, 2, 4, 8 inside each row of 16 (lanes
+// without a source add 0), then the totals of the rows below (lanes 15, 31, 47).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_u<0x111>(v);  // row_shr:1
+  v += dpp_u<0x112>(v);  // row_shr:2
+  v += dpp_u<0x114>(v);  // row_shr:4
+  v += dpp_u<0x118>(v);  // row_shr:8
+  const uint32_t r0 = readlane_u(v, 15), r1 = readlane_u(v, 31), r2 = readlane_u(v, 47);
+  const uint32_t row = (threadIdx.x & 63u) >> 4;
+  return v + (row == 0u ? 0u : row == 1u ? r0 : row == 2u ? r0 + r1 : r0 + r1 + r2);
+}
+// The same inside each half-wave of 32 lanes (lanes 0-31 and 32-63 scanned separately).
+__device__ __forceinline__ uint32_t half_wave_incl_scan(uint32_t v) {
+  v += dpp_u<0x111>(v);
+  v += dpp_u<0x112>(v);
+  v += dpp_u<0x114>(v);
+  v += dpp_u<0x118>(v);
+  const uint32_t r0 = readlane_u(v, 15), r2 = readlane_u(v, 47);
+  const uint32_t row = (threadIdx.x & 63u) >> 4;
+  return v + (row == 1u ? r0 : row == 3u ? r2 : 0u);
+}
+
+// Exclusive prefix sums over the experts e < E (E <= 256) of their entry counts c_e, of
+// [c_e > 0] and of ceil(c_e / kGemmTok), for thread e (threads 0 .. 255 of a workgroup of at least
+// 256): wave scans, then the totals of the waves below from LDS (tot_l: 12 ints).  Called by
+// every thread of the workgroup (two barriers); threads from 256 on get zeros.
+__device__ void expert_prefix(const int32_t *cnt, uint32_t E, int32_t *tot_l, int32_t &off, int32_t &ra, int32_t &toff) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const int32_t c = (tid < E && tid < kMaxExperts) ? cnt[tid] : 0;
+  const uint32_t v0 = (uint32_t)c, v1 = c > 0 ? 1u : 0u, v2 = (uint32_t)((c + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok);
+  const uint32_t i0 = wave_incl_scan(v0), i1 = wave_incl_scan(v1), i2 = wave_incl_scan(v2);
+  if (w < 4u && lane == 63u) {
+    tot_l[3u * w] = (int32_t)i0;
+    tot_l[3u * w + 1u] = (int32_t)i1;
+    tot_l[3u * w + 2u] = (int32_t)i2;
+  }
+  __syncthreads();
+  int32_t b0 = 0, b1 = 0, b2 = 0;
+  for (uint32_t w2 = 0; w2 < w && w2 < 4u; ++w2) {
+    b0 += tot_l[3u * w2];
+    b1 += tot_l[3u * w2 + 1u];
+    b2 += tot_l[3u * w2 + 2u];
+  }
+  off = b0 + (int32_t)(i0 - v0);
+  ra = b1 + (int32_t)(i1 - v1);
+  toff = b2 + (int32_t)(i2 - v2);
+  __syncthreads();  // tot_l free again
+}
+
 // ---------------------------------------------------------------------------------------------
 // Dispatch by one workgroup (any batch size).  Stable counting sort of the flat entries t*K+p by
 // expert: the rank of (t, e) inside expert e's segment is the number of earlier tokens that chose
@@ -632,12 +687,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint32_t E, int32_t *seg_off,
                                int32_t *perm, int32_t *pos_of, int32_t *active, int32_t *num_active,
                                int32_t *exrec, int32_t *tile_off, int32_t *lds) {
-  const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;
+  const uint32_t tid = threadIdx.x, nth = blockDim.x, words = nth >> 5;  // 32 words: nth = 1024
   int32_t *cnt = lds, *base = lds + E;
   uint32_t *bm = (uint32_t *)(lds + 2 * E);
   int32_t *wpre = lds + 2 * E + E * words;
   int32_t *aidx = wpre + E * words;  // active slot of each expert
   int32_t *segs = aidx + E;          // segment start of each expert
+  int32_t *tot_l = segs + E + 1;     // [12] wave totals of expert_prefix
   for (uint32_t e = tid; e < E; e += nth) cnt[e] = 0;
   __syncthreads();
   for (uint32_t i = tid; i < n * K; i += nth) {
@@ -645,14 +701,11 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
     if (e >= 0 && (uint32_t)e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  // exclusive scan and active list, each expert's thread summing the counts below it
-  for (uint32_t e = tid; e < E; e += nth) {
-    int32_t off = 0, ra = 0, toff = 0;
-    for (uint32_t e2 = 0; e2 < e; ++e2) {
-      off += cnt[e2];
-      ra += cnt[e2] > 0;
-      toff += (cnt[e2] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
-    }
+  // exclusive scans and active list (expert e by thread e)
+  int32_t off, ra, toff;
+  expert_prefix(cnt, E, tot_l, off, ra, toff);
+  if (tid < E) {
+    const uint32_t e = tid;
     if (tile_off) tile_off[e] = toff;
     seg_off[e] = off;
     base[e] = off;
@@ -686,11 +739,13 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
       }
     }
     __syncthreads();
-    for (uint32_t i = tid; i < E * words; i += nth) {
-      const uint32_t e = i / words, w = i % words;
-      int32_t s = 0;
-      for (uint32_t w2 = 0; w2 < w; ++w2) s += __popc(bm[e * words + w2]);
-      wpre[i] = s;
+    // popcount prefixes over each expert's 32 bitmap words: word i by lane i mod 64 of a
+    // half-wave scan (every wave runs the same number of rounds)
+    for (uint32_t i0 = 0; i0 < E * words; i0 += nth) {
+      const uint32_t i = i0 + tid;
+      const uint32_t v = i < E * words ? (uint32_t)__popc(bm[i]) : 0u;
+      const uint32_t incl = half_wave_incl_scan(v);
+      if (i < E * words) wpre[i] = (int32_t)(incl - v);
     }
     __syncthreads();
     if (t < n) {
@@ -715,7 +770,7 @@ __device__ void block_dispatch(const int32_t *idx, uint32_t n, uint32_t K, uint3
 }
 
 size_t dispatch_lds_bytes(uint32_t E, uint32_t threads) {
-  return sizeof(int32_t) * ((size_t)E * (4 + 2 * (threads / 32)) + 4);
+  return sizeof(int32_t) * ((size_t)E * (4 + 2 * (threads / 32)) + 16);
 }
 
 // Dispatch of a large batch in two launches over chunks of kDispatchChunk tokens (workgroup c owns
@@ -743,22 +798,26 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_count_kernel(Dispatch
 
 __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchArgs a) {
   constexpr uint32_t W = kDispatchChunk / 32u;  // bitmap words per expert
+  static_assert(kDispatchChunk >= kMaxExperts, "expert_prefix: thread e handles expert e");
   __shared__ int32_t call[kMaxExperts], cbef[kMaxExperts], segs[kMaxExperts], aidx[kMaxExperts], base[kMaxExperts];
   __shared__ uint32_t bm[kMaxExperts * W];
+  __shared__ int32_t tot_l[12];
   const uint32_t tid = threadIdx.x, c = blockIdx.x, E = a.E, K = a.K, n = a.n;
   const uint32_t t = c * kDispatchChunk + tid;
   const uint32_t nchunk = gridDim.x;
-  for (uint32_t e = tid; e < E; e += kDispatchChunk) {
-    int32_t all = 0, bef = 0;
-    for (uint32_t c2 = 0; c2 < nchunk; ++c2) {
-      const int32_t v = a.chunk_cnt[(size_t)c2 * E + e];
-      all += v;
-      bef += c2 < c ? v : 0;
-    }
-    call[e] = all;
-    cbef[e] = bef;
-  }
+  for (uint32_t e = tid; e < E; e += kDispatchChunk) call[e] = cbef[e] = 0;
   for (uint32_t i = tid; i < E * W; i += kDispatchChunk) bm[i] = 0u;
+  __syncthreads();
+  // every chunk's counts, all loads issued together: totals and earlier-chunk sums (LDS integer
+  // atomics, order-independent)
+  for (uint32_t i = tid; i < nchunk * E; i += kDispatchChunk) {
+    const uint32_t c2 = i / E, e = i - c2 * E;
+    const int32_t v = a.chunk_cnt[i];
+    if (v != 0) {
+      atomicAdd(&call[e], v);
+      if (c2 < c) atomicAdd(&cbef[e], v);
+    }
+  }
   __syncthreads();
   if (t < n) {
     for (uint32_t p = 0; p < K; ++p) {
@@ -767,14 +826,11 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
     }
   }
   __syncthreads();
-  // exclusive scan over experts (each expert's thread sums the counts below it)
-  for (uint32_t e = tid; e < E; e += kDispatchChunk) {
-    int32_t off = 0, ra = 0, toff = 0;
-    for (uint32_t e2 = 0; e2 < e; ++e2) {
-      off += call[e2];
-      ra += call[e2] > 0;
-      toff += (call[e2] + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok;
-    }
+  // exclusive scans over experts (expert e by thread e)
+  int32_t off, ra, toff;
+  expert_prefix(call, E, tot_l, off, ra, toff);
+  if (tid < E) {
+    const uint32_t e = tid;
     segs[e] = off;
     aidx[e] = ra;
     base[e] = off + cbef[e];
@@ -831,12 +887,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 //    the active list and records, wave t token t's segment positions (earlier tokens first).
 // Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
-}
-template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
 // (h, l) = the larger of the 64-bit keys (h, l) and (h2, l2), high word first
 __device__ __forceinline__ void key_max(uint32_t &h, uint32_t &l, uint32_t h2, uint32_t l2) {
   const bool g = h2 > h || (h2 == h && l2 > l);
@@ -865,17 +915,6 @@ __device__ __forceinline__ void wave_max_key(uint32_t &h, uint32_t &l) {
     l = pl[0];
     key_max(h, l, ph[1], pl[1]);
   }
-}
-// Inclusive prefix sum over the wave's lanes: row_shr 1, 2, 4, 8 inside each row of 16 (lanes
-// without a source add 0), then the totals of the rows below (lanes 15, 31, 47).
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  v += dpp_u<0x111>(v);  // row_shr:1
-  v += dpp_u<0x112>(v);  // row_shr:2
-  v += dpp_u<0x114>(v);  // row_shr:4
-  v += dpp_u<0x118>(v);  // row_shr:8
-  const uint32_t r0 = readlane_u(v, 15), r1 = readlane_u(v, 31), r2 = readlane_u(v, 47);
-  const uint32_t row = (threadIdx.x & 63u) >> 4;
-  return v + (row == 0u ? 0u : row == 1u ? r0 : row == 2u ? r0 + r1 : r0 + r1 + r2);
 }
 
 // Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
