@@ -561,67 +561,6 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Top-k by rank: the rank of expert e among a token's logits is the number of experts that beat
-// it under `beats` (larger value, NaN lowest, ties to the lower index); ranks < K are the
-// selection, in order.  Softmax over the selected logits: w_p = exp(v_p - v_0) / sum_q
-// exp(v_q - v_0), the sum taken q = 0..K-1 ascending from 0.
-// ---------------------------------------------------------------------------------------------
-// kr: the packed keys topk_key(lr[e], e) of the token's experts
-__device__ __forceinline__ void rank_select(const float *lr, const uint64_t *kr, uint32_t E, uint32_t K, uint32_t e,
-                                            int32_t *sel, float *selv) {
-  const uint64_t ke = kr[e];
-  uint32_t rank = 0;
-  for (uint32_t e2 = 0; e2 < E; ++e2) rank += kr[e2] > ke ? 1u : 0u;
-  if (rank < K) {
-    sel[rank] = (int32_t)e;
-    selv[rank] = lr[e];
-  }
-}
-
-__device__ __forceinline__ float softmax_weight(const float *selv, uint32_t K, uint32_t p) {
-  const float m = selv[0];
-  float s = 0.0f;
-  for (uint32_t q = 0; q < K; ++q) s += expf(selv[q] - m);
-  return expf(selv[p] - m) / s;
-}
-
-// per-wave LDS of topk_kernel: keys [E] u64, logits [E], sel [K], selv [K], 8-byte aligned stride
-__host__ __device__ inline size_t topk_wave_bytes(uint32_t E, uint32_t K) {
-  return ((size_t)12 * E + 8 * (size_t)K + 7) / 8 * 8;
-}
-size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads) { return (size_t)(threads / 64) * topk_wave_bytes(E, K); }
-
-// One wave per token; the workgroup's waves work on separate LDS rows, so only wave-level
-// ordering is needed between the phases (block barriers keep it simple and uniform).
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-  const uint32_t t = blockIdx.x * (blockDim.x >> 6) + w;
-  // per wave: keys [E] (8-byte aligned first), logits [E], sel [K], selv [K]
-  uint64_t *kr = (uint64_t *)(smem + (size_t)w * topk_wave_bytes(a.E, a.K));
-  float *lr = (float *)(kr + a.E);
-  int32_t *sel = (int32_t *)(lr + a.E);
-  float *selv = (float *)(sel + a.K);
-  const bool live = t < a.n;
-  if (live)
-    for (uint32_t e = lane; e < a.E; e += 64) {
-      const float v = a.logits[(size_t)t * a.E + e];
-      lr[e] = v;
-      kr[e] = topk_key(v, e);
-    }
-  __syncthreads();
-  if (live)
-    for (uint32_t e = lane; e < a.E; e += 64) rank_select(lr, kr, a.E, a.K, e, sel, selv);
-  __syncthreads();
-  if (live) {
-    for (uint32_t p = lane; p < a.K; p += 64) {
-      a.topk_idx[(size_t)t * a.K + p] = sel[p];
-      a.topk_w[(size_t)t * a.K + p] = softmax_weight(selv, a.K, p);
-    }
-  }
-}
-
 __device__ __forceinline__ uint32_t readlane_u(uint32_t v, uint32_t k) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)k);
 }
@@ -676,6 +615,97 @@ __device__ void expert_prefix(const int32_t *cnt, uint32_t E, int32_t *tot_l, in
   toff = b2 + (int32_t)(i2 - v2);
   __syncthreads();  // tot_l free again
 }
+
+// (h, l) = the larger of the 64-bit keys (h, l) and (h2, l2), high word first
+__device__ __forceinline__ void key_max(uint32_t &h, uint32_t &l, uint32_t h2, uint32_t l2) {
+  const bool g = h2 > h || (h2 == h && l2 > l);
+  h = g ? h2 : h;
+  l = g ? l2 : l;
+}
+// Maximum of the 64-bit keys (h, l) over the wave, in every lane: quad permutations (lanes
+// l ^ 1, l ^ 2), row rotations by 4 and 8 (the row's four quads), then the permlane swaps
+// between rows 16 and 32 apart.
+__device__ __forceinline__ void wave_max_key(uint32_t &h, uint32_t &l) {
+  key_max(h, l, dpp_u<0xB1>(h), dpp_u<0xB1>(l));    // quad_perm [1,0,3,2]
+  key_max(h, l, dpp_u<0x4E>(h), dpp_u<0x4E>(l));    // quad_perm [2,3,0,1]
+  key_max(h, l, dpp_u<0x124>(h), dpp_u<0x124>(l));  // row_ror:4
+  key_max(h, l, dpp_u<0x128>(h), dpp_u<0x128>(l));  // row_ror:8
+  {
+    const auto ph = __builtin_amdgcn_permlane16_swap(h, h, false, false);
+    const auto pl = __builtin_amdgcn_permlane16_swap(l, l, false, false);
+    h = ph[0];
+    l = pl[0];
+    key_max(h, l, ph[1], pl[1]);
+  }
+  {
+    const auto ph = __builtin_amdgcn_permlane32_swap(h, h, false, false);
+    const auto pl = __builtin_amdgcn_permlane32_swap(l, l, false, false);
+    h = ph[0];
+    l = pl[0];
+    key_max(h, l, ph[1], pl[1]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Top-k and softmax, one wave per token: lane l holds experts l + 64 j (j < J); K rounds of a
+// wave-wide maximum of the packed keys topk_key (larger value, NaN lowest, ties to the lower index)
+// not yet taken select the experts of ranks 0 .. K-1 in order.  Softmax over the selected logits:
+// w_p = exp(v_p - v_0) / sum_q exp(v_q - v_0), the sum taken q = 0..K-1 ascending from 0.
+// Same selection and weights as route_small_body.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float softmax_weight(const float *selv, uint32_t K, uint32_t p) {
+  const float m = selv[0];
+  float s = 0.0f;
+  for (uint32_t q = 0; q < K; ++q) s += expf(selv[q] - m);
+  return expf(selv[p] - m) / s;
+}
+
+template <int J>  // E <= 64 J
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
+  __shared__ float selv_l[kTopkThreads / 64u][kMaxTopK];
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t t = blockIdx.x * (blockDim.x >> 6) + w;
+  if (t >= a.n) return;  // wave-uniform, and no workgroup barrier follows
+  const uint32_t E = a.E, K = a.K;
+  float v[J];
+  uint32_t kh[J], kl[J], rank[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    v[j] = e < E ? a.logits[(size_t)t * E + e] : 0.0f;
+    const uint64_t key = topk_key(v[j], e);
+    kh[j] = (uint32_t)(key >> 32);
+    kl[j] = (uint32_t)key;
+    rank[j] = ~0u;
+  }
+  for (uint32_t r = 0; r < K; ++r) {
+    uint32_t bh = 0u, bl = 0u;  // below every real key (the low word ~index is never 0)
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const bool cand = lane + 64u * j < E && rank[j] == ~0u;
+      if (cand && (kh[j] > bh || (kh[j] == bh && kl[j] > bl))) {
+        bh = kh[j];
+        bl = kl[j];
+      }
+    }
+    wave_max_key(bh, bl);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (lane + 64u * j < E && kh[j] == bh && kl[j] == bl) rank[j] = r;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    if (e < E && rank[j] < K) {
+      selv_l[w][rank[j]] = v[j];
+      a.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's selv_l writes complete (lgkmcnt(0) only)
+  __builtin_amdgcn_wave_barrier();
+  for (uint32_t p = lane; p < K; p += 64u) a.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[w], K, p);
+}
+
 
 // ---------------------------------------------------------------------------------------------
 // Dispatch by one workgroup (any batch size).  Stable counting sort of the flat entries t*K+p by
@@ -887,35 +917,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 //    the active list and records, wave t token t's segment positions (earlier tokens first).
 // Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
-// (h, l) = the larger of the 64-bit keys (h, l) and (h2, l2), high word first
-__device__ __forceinline__ void key_max(uint32_t &h, uint32_t &l, uint32_t h2, uint32_t l2) {
-  const bool g = h2 > h || (h2 == h && l2 > l);
-  h = g ? h2 : h;
-  l = g ? l2 : l;
-}
-// Maximum of the 64-bit keys (h, l) over the wave, in every lane: quad permutations (lanes
-// l ^ 1, l ^ 2), row rotations by 4 and 8 (the row's four quads), then the permlane swaps
-// between rows 16 and 32 apart.
-__device__ __forceinline__ void wave_max_key(uint32_t &h, uint32_t &l) {
-  key_max(h, l, dpp_u<0xB1>(h), dpp_u<0xB1>(l));    // quad_perm [1,0,3,2]
-  key_max(h, l, dpp_u<0x4E>(h), dpp_u<0x4E>(l));    // quad_perm [2,3,0,1]
-  key_max(h, l, dpp_u<0x124>(h), dpp_u<0x124>(l));  // row_ror:4
-  key_max(h, l, dpp_u<0x128>(h), dpp_u<0x128>(l));  // row_ror:8
-  {
-    const auto ph = __builtin_amdgcn_permlane16_swap(h, h, false, false);
-    const auto pl = __builtin_amdgcn_permlane16_swap(l, l, false, false);
-    h = ph[0];
-    l = pl[0];
-    key_max(h, l, ph[1], pl[1]);
-  }
-  {
-    const auto ph = __builtin_amdgcn_permlane32_swap(h, h, false, false);
-    const auto pl = __builtin_amdgcn_permlane32_swap(l, l, false, false);
-    h = ph[0];
-    l = pl[0];
-    key_max(h, l, ph[1], pl[1]);
-  }
-}
 
 // Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
 struct RouteOut {
@@ -1621,7 +1622,6 @@ hipError_t configure_kernels() {
   BX_ATTR((router_rows_kernel<float, uint16_t>));
   BX_ATTR((router_rows_kernel<uint16_t, float>));
   BX_ATTR((router_rows_kernel<uint16_t, uint16_t>));
-  BX_ATTR(topk_kernel);
   BX_ATTR(dispatch_kernel);
   BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1>));
   BX_ATTR((expert_gemv_kernel<1, true, float, 1>));
@@ -1706,8 +1706,15 @@ hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hip
 }
 
 hipError_t launch_topk(const TopkArgs &a, hipStream_t s) {
+  if (a.E == 0 || a.E > kMaxExperts || a.K == 0 || a.K > kMaxTopK || a.K > a.E) return hipErrorInvalidValue;
   const uint32_t wpb = kTopkThreads / 64;
-  topk_kernel<<<dim3((a.n + wpb - 1) / wpb), dim3(kTopkThreads), topk_lds_bytes(a.E, a.K, kTopkThreads), s>>>(a);
+  const dim3 grid((a.n + wpb - 1) / wpb), block(kTopkThreads);
+  if (a.E <= 64)
+    topk_kernel<1><<<grid, block, 0, s>>>(a);
+  else if (a.E <= 128)
+    topk_kernel<2><<<grid, block, 0, s>>>(a);
+  else
+    topk_kernel<4><<<grid, block, 0, s>>>(a);
   return hipGetLastError();
 }
 

@@ -155,7 +155,6 @@ struct DequantArgs {
 };
 
 size_t router_lds_bytes(uint32_t tb, uint32_t Dpad);
-size_t topk_lds_bytes(uint32_t E, uint32_t K, uint32_t threads);
 size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
