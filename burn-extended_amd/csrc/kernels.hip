@@ -346,8 +346,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Prefill router (D % 8 == 0, D, Dp and the MXFP8 row length <= 512 * kFrontChunks, 16-byte
-// aligned rows).  Workgroup of kRowsThreads: wave w holds tokens 2 (8 b + w) .. +2 in registers
-// (f32); the router rows pass through LDS as f32 in stages of kRowsExperts experts (double
+// aligned rows).  Workgroup of kRowsThreads: wave w holds tokens T (8 b + w) .. +T in registers
+// (f32, T = 2 or 4); the router rows pass through LDS as f32 in stages of kRowsExperts experts (double
 // buffered, filled by all threads, one barrier per stage), so each row is converted once per
 // workgroup and read by every wave from LDS.  LDS row layout: element 512 i + 8 l + j at
 // 512 i + 256 (j / 4) + 4 l + j % 4, so lane l's two float4 of its chunk are conflict-free.
@@ -356,14 +356,13 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 // equal router_kernel's bit for bit.  The two-term MXFP8 rows come from the registers: a 32-value
 // block is the 8-value chunks of lanes 4 b .. 4 b + 3, its maxima taken over those four lanes.
 // ---------------------------------------------------------------------------------------------
-constexpr int kRowsTokens = 2;     // tokens per wave
 constexpr int kRowsExperts = 4;    // experts per LDS stage
 constexpr uint32_t kRowsSpan = 512u * kFrontChunks;  // f32 LDS row stride
 size_t router_rows_lds_bytes() { return sizeof(float) * (2u * kRowsExperts * kRowsSpan + kMaxExperts); }
 
-template <typename XT, typename WT>
+template <typename XT, typename WT, int T>  // T tokens per wave (2, or 4 for the largest batches)
 __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a) {
-  constexpr int T = kRowsTokens, G = kRowsExperts, RC = kFrontChunks;
+  constexpr int G = kRowsExperts, RC = kFrontChunks;
   constexpr uint32_t FC = (G * kRowsSpan / 8u + kRowsThreads - 1u) / kRowsThreads;  // fill chunks per thread
   extern __shared__ __align__(16) float wls[];  // [2][G][kRowsSpan], then rb [E]
   float *rbl = wls + 2u * G * kRowsSpan;
@@ -1618,10 +1617,14 @@ hipError_t configure_kernels() {
   BX_ATTR((router_kernel<float, uint16_t, false>));
   BX_ATTR((router_kernel<uint16_t, float, false>));
   BX_ATTR((router_kernel<uint16_t, uint16_t, false>));
-  BX_ATTR((router_rows_kernel<float, float>));
-  BX_ATTR((router_rows_kernel<float, uint16_t>));
-  BX_ATTR((router_rows_kernel<uint16_t, float>));
-  BX_ATTR((router_rows_kernel<uint16_t, uint16_t>));
+  BX_ATTR((router_rows_kernel<float, float, 2>));
+  BX_ATTR((router_rows_kernel<float, float, 4>));
+  BX_ATTR((router_rows_kernel<float, uint16_t, 2>));
+  BX_ATTR((router_rows_kernel<float, uint16_t, 4>));
+  BX_ATTR((router_rows_kernel<uint16_t, float, 2>));
+  BX_ATTR((router_rows_kernel<uint16_t, float, 4>));
+  BX_ATTR((router_rows_kernel<uint16_t, uint16_t, 2>));
+  BX_ATTR((router_rows_kernel<uint16_t, uint16_t, 4>));
   BX_ATTR(dispatch_kernel);
   BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1>));
   BX_ATTR((expert_gemv_kernel<1, true, float, 1>));
@@ -1643,20 +1646,29 @@ static void router_launch(const RouterArgs &a, bool vec, dim3 grid, size_t lds, 
     router_kernel<XT, WT, false><<<grid, dim3(kRouterThreads), lds, s>>>(a);
 }
 
-hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, hipStream_t s) {
+template <typename XT, typename WT>
+static void rows_launch(const RouterArgs &a, int tokens_per_wave, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (tokens_per_wave == 4)
+    router_rows_kernel<XT, WT, 4><<<grid, block, lds, s>>>(a);
+  else
+    router_rows_kernel<XT, WT, 2><<<grid, block, lds, s>>>(a);
+}
+
+hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, int tokens_per_wave, hipStream_t s) {
+  if (tokens_per_wave != 2 && tokens_per_wave != 4) return hipErrorInvalidValue;
   if (a.D % 8u != 0 || a.D > kRowsSpan || (a.xn && a.Dp > kRowsSpan) || (a.xq.hi && a.xq.kq > kRowsSpan))
     return hipErrorInvalidValue;
-  const uint32_t tpb = kRowsTokens * (kRowsThreads / 64u);
+  const uint32_t tpb = (uint32_t)tokens_per_wave * (kRowsThreads / 64u);
   const dim3 grid((a.n + tpb - 1) / tpb), block(kRowsThreads);
   const size_t lds = router_rows_lds_bytes();
   if (x_bf16 && w_bf16)
-    router_rows_kernel<uint16_t, uint16_t><<<grid, block, lds, s>>>(a);
+    rows_launch<uint16_t, uint16_t>(a, tokens_per_wave, grid, block, lds, s);
   else if (x_bf16)
-    router_rows_kernel<uint16_t, float><<<grid, block, lds, s>>>(a);
+    rows_launch<uint16_t, float>(a, tokens_per_wave, grid, block, lds, s);
   else if (w_bf16)
-    router_rows_kernel<float, uint16_t><<<grid, block, lds, s>>>(a);
+    rows_launch<float, uint16_t>(a, tokens_per_wave, grid, block, lds, s);
   else
-    router_rows_kernel<float, float><<<grid, block, lds, s>>>(a);
+    rows_launch<float, float>(a, tokens_per_wave, grid, block, lds, s);
   return hipGetLastError();
 }
 

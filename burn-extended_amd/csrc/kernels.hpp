@@ -190,8 +190,8 @@ constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-work
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
 // router_rows_kernel: D % 8 == 0 and D, Dp (with xn) and xq.kq (with xq) <= 512 * kFrontChunks,
-// 16-byte aligned x and router rows
-hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
+// 16-byte aligned x and router rows; 2 or 4 tokens per wave (16 or 32 per workgroup)
+hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, int tokens_per_wave, hipStream_t s);
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);
 hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
 hipError_t launch_topk(const TopkArgs &a, hipStream_t s);

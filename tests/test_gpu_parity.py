@@ -93,12 +93,18 @@ ROUTE_CASES = [
     (2880, 128, 4, 64, "bf16", True, False),
     (2880, 128, 4, 1, "f32", True, True),
     (200, 7, 3, 37, "f32", True, False),
-    # prefill-sized batches (token rows held in registers)
+    # mid-size batches (token block staged in LDS)
     (2880, 32, 4, 1027, "bf16", True, False),
     (2880, 32, 4, 1024, "bf16", True, True),
     (2880, 128, 4, 512, "bf16", False, False),
     (1000, 7, 3, 600, "f32", True, True),
     (200, 9, 2, 513, "f32", False, False),
+    # prefill-sized batches (token rows held in registers, 2 per wave; 4 per wave from 32 tokens
+    # per CU on)
+    (2880, 32, 4, 1200, "bf16", True, False),
+    (1000, 7, 3, 1300, "f32", True, True),
+    (2880, 128, 4, 8200, "bf16", True, True),
+    (200, 9, 2, 9000, "f32", False, False),
 ]
 
 
