@@ -335,23 +335,26 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       }
     }
   } else {
-    // token-major slot rows t * topk + p, expert bias b2 added once
+    // token-major slot rows t * topk + p in bf16 (the layer output is bf16 on this path), expert
+    // bias b2 added once
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
       if (tok >= ntok) continue;
-      float *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
+      uint16_t *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         if (rb * kRowTiles + wr * 4u + (uint32_t)rt >= a.nrt) continue;
         const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
         const f32x4_t bb = bias4[rt];
+        uint16_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = f32_to_bf16_bits(acc[rt][tt][r] + bb[r]);
         if (r0 + 3u < a.out_rows) {
-          *(float4 *)(orow + r0) = make_float4(acc[rt][tt][0] + bb[0], acc[rt][tt][1] + bb[1],
-                                               acc[rt][tt][2] + bb[2], acc[rt][tt][3] + bb[3]);
+          *(uint2 *)(orow + r0) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
         } else {
           for (uint32_t r = 0; r < 4u; ++r)
-            if (r0 + r < a.out_rows) orow[r0 + r] = acc[rt][tt][r] + bb[r];
+            if (r0 + r < a.out_rows) orow[r0 + r] = o[r];
         }
       }
     }

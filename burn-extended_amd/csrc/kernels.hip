@@ -1499,11 +1499,13 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 
 // ---------------------------------------------------------------------------------------------
 // Combine: y[t, d] = (add_residual ? x[t, d] : 0) + sum_{p asc} yslot[t*K + p, d] * w_p, where the
-// down projection already wrote yslot = down_p + b2[e_p] token-major.  Every load of a thread is
-// independent of the others (one memory round trip); four outputs per thread.
+// down projection already wrote yslot = down_p + b2[e_p] token-major (f32, in NP K-parts, or bf16
+// when PB).  Every load of a thread is independent of the others (one memory round trip); four
+// outputs per thread.
 // ---------------------------------------------------------------------------------------------
-template <typename XT, int NP>
+template <typename XT, int NP, bool PB>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+  static_assert(!PB || NP == 1, "bf16 slot rows come in one part");
   const uint32_t t = blockIdx.y;
   const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4u;
   if (d0 >= a.D) return;
@@ -1539,9 +1541,16 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     for (uint32_t u = 0; u < 8u; ++u) {
       const uint32_t p = min(p0 + u, a.K - 1u);
       wv[u] = a.topk_w[(size_t)t * a.K + p];
-      yv[u] = *(const float4 *)(a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 4 == 0, d0 < Dp
+      const size_t row = ((size_t)t * a.K + p) * a.Dp + d0;  // Dp % 4 == 0, d0 < Dp
+      if constexpr (PB) {
+        const uint2 r = *(const uint2 *)((const uint16_t *)a.ypart + row);
+        yv[u] = make_float4(bf16_bits_to_f32((uint16_t)r.x), bf16_bits_to_f32((uint16_t)(r.x >> 16)),
+                            bf16_bits_to_f32((uint16_t)r.y), bf16_bits_to_f32((uint16_t)(r.y >> 16)));
+      } else {
+        yv[u] = *(const float4 *)((const float *)a.ypart + row);
+      }
 #pragma unroll
-      for (int h = 1; h < NP; ++h) yh[h - 1][u] = *(const float4 *)(a.ypart + h * a.part_stride + ((size_t)t * a.K + p) * a.Dp + d0);
+      for (int h = 1; h < NP; ++h) yh[h - 1][u] = *(const float4 *)((const float *)a.ypart + h * a.part_stride + row);
     }
 #pragma unroll
     for (int h = 1; h < NP; ++h)
@@ -1776,16 +1785,22 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
   if (a.nparts != 1u && a.nparts != kDownSplit) return hipErrorInvalidValue;
-  if (a.nparts == 1u) {
+  if (a.part_bf16 && a.nparts != 1u) return hipErrorInvalidValue;
+  if (a.part_bf16) {
     if (x_bf16)
-      combine_kernel<uint16_t, 1><<<grid, block, 0, s>>>(a);
+      combine_kernel<uint16_t, 1, true><<<grid, block, 0, s>>>(a);
     else
-      combine_kernel<float, 1><<<grid, block, 0, s>>>(a);
+      combine_kernel<float, 1, true><<<grid, block, 0, s>>>(a);
+  } else if (a.nparts == 1u) {
+    if (x_bf16)
+      combine_kernel<uint16_t, 1, false><<<grid, block, 0, s>>>(a);
+    else
+      combine_kernel<float, 1, false><<<grid, block, 0, s>>>(a);
   } else {
     if (x_bf16)
-      combine_kernel<uint16_t, kDownSplit><<<grid, block, 0, s>>>(a);
+      combine_kernel<uint16_t, kDownSplit, false><<<grid, block, 0, s>>>(a);
     else
-      combine_kernel<float, kDownSplit><<<grid, block, 0, s>>>(a);
+      combine_kernel<float, kDownSplit, false><<<grid, block, 0, s>>>(a);
   }
   return hipGetLastError();
 }

@@ -130,7 +130,7 @@ struct GemmArgs {
   QRows b;                 // B rows: gate_up xq (token rows), down act (segment rows)
   QRows act;               // gate_up output: SwiGLU rows in segment order, quantised
   uint32_t act_feats;      // gate_up: F (features written; [F, act.kq) zero-filled)
-  float *out;              // down: token-major slot rows [n*k, out_stride] f32
+  uint16_t *out;           // down: token-major slot rows [n*k, out_stride] bf16
   uint32_t out_stride;
   float alpha, limit;
 };
@@ -138,9 +138,10 @@ struct GemmArgs {
 struct CombineArgs {
   const void *x;
   void *y;
-  const float *ypart;  // token-major slot rows [n*K, Dp], expert bias included
-  uint32_t nparts;     // K-parts of ypart (1 = complete rows), parts part_stride floats apart,
+  const void *ypart;   // token-major slot rows [n*K, Dp], expert bias included: f32, or bf16 (part_bf16)
+  uint32_t nparts;     // K-parts of ypart (1 = complete rows), parts part_stride elements apart,
   uint64_t part_stride;  // summed in order before the weighting
+  int part_bf16;       // bf16 slot rows (the grouped GEMM's down output; nparts 1)
   const float *topk_w;
   uint32_t n, D, Dp, K;
   int add_residual;

@@ -508,12 +508,13 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
 
 // The weighted combine + residual of every path (token-major slot rows in p.ypart).
 burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
-                       const WsPtrs &p, hipStream_t s, uint32_t nparts = 1) {
+                       const WsPtrs &p, hipStream_t s, uint32_t nparts = 1, bool part_bf16 = false) {
   CombineArgs c{};
   c.x = x;
   c.y = y;
   c.ypart = p.ypart;
   c.nparts = nparts;
+  c.part_bf16 = part_bf16 ? 1 : 0;
   c.part_stride = n * L->K * L->Dp;
   c.topk_w = p.topk_w;
   c.n = (uint32_t)n;
@@ -563,7 +564,7 @@ burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64
     g.b = up ? p.xq : p.aq;
     g.act = p.aq;
     g.act_feats = L->F;
-    g.out = p.ypart;
+    g.out = (uint16_t *)p.ypart;
     g.out_stride = L->Dp;
     g.alpha = L->alpha;
     g.limit = L->limit;
@@ -750,7 +751,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   if (w.gemm && xb) {
     st = forward_gemm(L, x, xb, n, norm, p, s);
     if (st != BURNEXT_OK) return st;
-    return combine(L, x, y, xb, n, flags, p, s);
+    return combine(L, x, y, xb, n, flags, p, s, 1, true);  // bf16 slot rows from the down GEMM
   }
   const int nt = xb ? 1 : 3;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
