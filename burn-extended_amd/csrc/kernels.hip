@@ -1782,11 +1782,56 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   return hipGetLastError();
 }
 
+// Combine of the grouped-GEMM path (bf16 x, y and slot rows, D % 8 == 0, 16-byte aligned x and
+// y): eight outputs per thread, 16-byte loads and stores; the same per-element arithmetic and
+// order as combine_kernel.
+__device__ __forceinline__ void bf16x8_to_f32(const uint4 r, float (&v)[8]) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[2 * k] = bf16_bits_to_f32((uint16_t)w[k]);
+    v[2 * k + 1] = bf16_bits_to_f32((uint16_t)(w[k] >> 16));
+  }
+}
+__global__ __launch_bounds__(256) void combine_rows8_kernel(CombineArgs a) {
+  const uint32_t t = blockIdx.y;
+  const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8u;
+  if (d0 >= a.D) return;
+  float xv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.add_residual) bf16x8_to_f32(*(const uint4 *)((const uint16_t *)a.x + (size_t)t * a.D + d0), xv);
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t p0 = 0; p0 < a.K; p0 += 8u) {
+    float wv[8];
+    uint4 yr[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t p = min(p0 + u, a.K - 1u);
+      wv[u] = a.topk_w[(size_t)t * a.K + p];
+      yr[u] = *(const uint4 *)((const uint16_t *)a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 32 == 0
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      if (p0 + u >= a.K) break;
+      float yv[8];
+      bf16x8_to_f32(yr[u], yv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = acc[j] + yv[j] * wv[u];
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    o[k] = (uint32_t)f32_to_bf16_bits(xv[2 * k] + acc[2 * k]) | ((uint32_t)f32_to_bf16_bits(xv[2 * k + 1] + acc[2 * k + 1]) << 16);
+  *(uint4 *)((uint16_t *)a.y + (size_t)t * a.D + d0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
   if (a.nparts != 1u && a.nparts != kDownSplit) return hipErrorInvalidValue;
   if (a.part_bf16 && a.nparts != 1u) return hipErrorInvalidValue;
-  if (a.part_bf16) {
+  if (a.part_bf16 && x_bf16 && a.D % 8u == 0u && (((uintptr_t)a.x | (uintptr_t)a.y) & 15u) == 0u) {
+    combine_rows8_kernel<<<dim3((a.D + 2047u) / 2048u, a.n), dim3(256), 0, s>>>(a);
+  } else if (a.part_bf16) {
     if (x_bf16)
       combine_kernel<uint16_t, 1, true><<<grid, block, 0, s>>>(a);
     else
