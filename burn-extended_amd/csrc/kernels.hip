@@ -1250,7 +1250,8 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // reason.  No branch surrounds a weight load.
 template <int NT, bool GATE_UP, typename XT, int SPLIT>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
-  static_assert(SPLIT >= 1 && (GATE_UP ? SPLIT == 1 : SPLIT <= (int)kDownSplit), "K-parts of down units");
+  static_assert(SPLIT >= 1 && (GATE_UP ? (SPLIT == 1 || SPLIT == (int)kGateUpSplit) : SPLIT <= (int)kDownSplit),
+                "K-parts of the units");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr uint32_t CJ = kGemvKgPerWave;
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
@@ -1459,7 +1460,18 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
     if (bval) {
       const uint32_t r0 = rt * 16u + 4u * q;
-      if constexpr (GATE_UP) {
+      if constexpr (GATE_UP && SPLIT > 1) {
+        // raw pre-activation rows of K-part h (b1 in part 0), segment-order slot rows
+        const int pos = seg0 + (int)(m0 + i16);
+        float *o = a.out + h * a.out_half + (size_t)pos * a.out_stride + r0;
+        const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : bias4;
+        if (r0 + 3u < a.out_rows) {
+          *(float4 *)o = make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
+        } else {
+          for (uint32_t r = 0; r < 4u; ++r)
+            if (r0 + r < a.out_rows) o[r] = acc[r] + b4[r];
+        }
+      } else if constexpr (GATE_UP) {
         const int pos = seg0 + (int)(m0 + i16);
         const uint32_t f0 = r0 >> 1;
         const float o0 = swiglu_clamp_f(acc[0] + bias4[0], acc[1] + bias4[1], a.alpha, a.limit);
@@ -1637,10 +1649,14 @@ hipError_t configure_kernels() {
   BX_ATTR(dispatch_kernel);
   BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1>));
   BX_ATTR((expert_gemv_kernel<1, true, float, 1>));
+  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, kGateUpSplit>));
+  BX_ATTR((expert_gemv_kernel<1, true, float, kGateUpSplit>));
   BX_ATTR((expert_gemv_kernel<1, false, float, 1>));
   BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit>));
   BX_ATTR((expert_gemv_kernel<3, true, uint16_t, 1>));
   BX_ATTR((expert_gemv_kernel<3, true, float, 1>));
+  BX_ATTR((expert_gemv_kernel<3, true, uint16_t, kGateUpSplit>));
+  BX_ATTR((expert_gemv_kernel<3, true, float, kGateUpSplit>));
   BX_ATTR((expert_gemv_kernel<3, false, float, 1>));
   BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplit>));
 #undef BX_ATTR
@@ -1752,17 +1768,23 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
-  const uint64_t nunits = (uint64_t)a.nrt * (!gate_up && a.ksplit > 1u ? a.ksplit : 1u);
+  const uint64_t nunits = (uint64_t)a.nrt * (a.ksplit > 1u ? a.ksplit : 1u);
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
   const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit) return hipErrorInvalidValue;
+  if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
   const bool split = !gate_up && a.ksplit > 1u;
+  const bool usplit = gate_up && a.ksplit > 1u;
   if (nt == 1) {
     if (split)
       expert_gemv_kernel<1, false, float, kDownSplit><<<g, block, lds, s>>>(a);
     else if (!gate_up)
       expert_gemv_kernel<1, false, float, 1><<<g, block, lds, s>>>(a);
+    else if (usplit && x_bf16)
+      expert_gemv_kernel<1, true, uint16_t, kGateUpSplit><<<g, block, lds, s>>>(a);
+    else if (usplit)
+      expert_gemv_kernel<1, true, float, kGateUpSplit><<<g, block, lds, s>>>(a);
     else if (x_bf16)
       expert_gemv_kernel<1, true, uint16_t, 1><<<g, block, lds, s>>>(a);
     else
@@ -1772,6 +1794,10 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
       expert_gemv_kernel<3, false, float, kDownSplit><<<g, block, lds, s>>>(a);
     else if (!gate_up)
       expert_gemv_kernel<3, false, float, 1><<<g, block, lds, s>>>(a);
+    else if (usplit && x_bf16)
+      expert_gemv_kernel<3, true, uint16_t, kGateUpSplit><<<g, block, lds, s>>>(a);
+    else if (usplit)
+      expert_gemv_kernel<3, true, float, kGateUpSplit><<<g, block, lds, s>>>(a);
     else if (x_bf16)
       expert_gemv_kernel<3, true, uint16_t, 1><<<g, block, lds, s>>>(a);
     else
@@ -1779,6 +1805,27 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// SwiGLU of the summed gate_up K-parts (interleaved rows: 2f gate, 2f + 1 linear), one output
+// per thread.
+__global__ __launch_bounds__(256) void swiglu_parts_kernel(SwigluPartsArgs a) {
+  const uint32_t r = blockIdx.y, f = blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= a.F) return;
+  const float *p = a.parts + (size_t)r * a.rows_p + 2u * f;
+  float g = 0.0f, l = 0.0f;
+  for (uint32_t h = 0; h < a.nparts; ++h) {
+    const float2 v = *(const float2 *)(p + h * a.part_stride);
+    g = g + v.x;
+    l = l + v.y;
+  }
+  a.act[(size_t)r * a.act_stride + f] = swiglu_clamp_f(g, l, a.alpha, a.limit);
+}
+
+hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s) {
+  if (a.rows == 0 || a.F == 0 || 2u * a.F > a.rows_p || (a.rows_p & 1u) || (a.part_stride & 1u)) return hipErrorInvalidValue;
+  swiglu_parts_kernel<<<dim3((a.F + 255u) / 256u, a.rows), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }
 

@@ -78,8 +78,10 @@ struct GemvArgs {
   float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
-  // down only: every row tile's K range split into ksplit (0 or 1: none) fixed parts, separate
-  // work units; part h's partial sums go to out + h * out_half (b2 in part 0), combine adds them
+  // every row tile's K range split into ksplit (0 or 1: none) fixed parts, separate work units;
+  // part h's partial sums go to out + h * out_half (bias in part 0).  down: slot rows, combine
+  // adds the parts; gate_up: raw pre-activation rows [n*k, out_stride] of the out_rows W1 rows,
+  // finished by swiglu_parts_kernel
   uint32_t ksplit;
   uint64_t out_half;
 };
@@ -147,6 +149,16 @@ struct CombineArgs {
   int add_residual;
 };
 
+// act[r, f] = SwiGLU(sum_h part_h[r, 2f], sum_h part_h[r, 2f + 1]) (h ascending) for the
+// gate_up K-parts of a decode-sized batch.
+struct SwigluPartsArgs {
+  const float *parts;  // [nparts][rows, rows_p]
+  uint64_t part_stride;
+  float *act;          // [rows, act_stride]
+  uint32_t nparts, rows, F, rows_p, act_stride;
+  float alpha, limit;
+};
+
 struct DequantArgs {
   const uint8_t *blocks, *scales;
   void *out;
@@ -185,6 +197,9 @@ constexpr uint32_t kGemvThreads = 256;
 // and down (measured: flatter weights for down, where the K-halves already even out the waves)
 constexpr uint32_t kRoundWeight[2][4] = {{20, 10, 4, 2}, {20, 16, 11, 8}};
 constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert GEMV (decode-sized batches; 3, 4 and 6 measured slower)
+// K-parts per gate_up row tile when a batch touches so few experts that whole row tiles leave most
+// waves idle (gate_up then writes partial pre-activations, swiglu_parts_kernel finishes them)
+constexpr uint32_t kGateUpSplit = 4;
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
@@ -199,6 +214,7 @@ hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s);
+hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s);
 hipError_t configure_gemm_kernels();
 size_t gemm_lds_bytes();

@@ -246,10 +246,19 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   return c;
 }
 
+// Decode-sized batches that touch so few experts that their gate_up row tiles are fewer than 8 per
+// CU (2/3 of a tile per wave) split every tile's K range in kGateUpSplit parts: a wave then streams
+// 6 instead of 23 K-groups at D = 2880 (120B T = 1: 4 experts, 1440 row tiles for 3072 waves).
+inline bool gate_up_split(const burnext_moe_layer &L, uint64_t n) {
+  return n <= kSmallRouteMaxTokens && std::min<uint64_t>(L.E, n * L.K) * L.w1.nrt < 8ull * (uint64_t)L.num_cus &&
+         (L.w1.nb + 3u) / 4u >= kGateUpSplit;
+}
+
 // Workspace carve-up for n tokens (every region 256-byte aligned).
 struct WsLayout {
   uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, xn, act, ypart, dcnt, total;
   uint64_t tile_off, xq[4], aq[4];  // grouped-GEMM path: tile prefix, xq / act rows (hi lo shi slo)
+  uint64_t upart;                   // gate_up K-parts of a few-expert decode batch (gate_up_split)
   bool gemm;                        // the grouped-GEMM regions are present
 };
 
@@ -304,6 +313,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   // partial-sum buffer each
   w.ypart = take(nk * L.Dp * 4 * (n <= kSmallRouteMaxTokens ? kDownSplit : 1));
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
+  if (gate_up_split(L, n)) w.upart = take((uint64_t)kGateUpSplit * nk * L.w1.rows_p * 4);
   w.total = off;
   return w;
 }
@@ -317,6 +327,7 @@ struct WsPtrs {
   int32_t *exrec;
   void *xn;
   float *act, *ypart;
+  float *upart;  // gate_up K-parts [kGateUpSplit][n*k, w1.rows_p] (gate_up_split)
   int32_t *tile_off;
   int32_t *dcnt;  // per-chunk expert counts of the multi-workgroup dispatch
   QRows xq, aq;
@@ -343,6 +354,7 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
   p.ypart = (float *)(b + w.ypart);
+  p.upart = w.upart ? (float *)(b + w.upart) : nullptr;
   p.dcnt = (int32_t *)(b + w.dcnt);
   return p;
 }
@@ -759,6 +771,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
   // evenly over the waves; measured slower from 64 tokens on)
   const uint32_t ksplit = (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
+  const bool up_split = gate_up_split(*L, n) && p.upart;
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
@@ -803,11 +816,34 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
       g.ksplit = ksplit;
       g.out_half = n * L->K * L->Dp;
     }
+    if (gate_up && up_split) {  // raw pre-activation K-parts, finished by swiglu_parts_kernel
+      g.ksplit = kGateUpSplit;
+      g.out = p.upart;
+      g.out_stride = L->w1.rows_p;
+      g.out_rows = 2 * L->F;
+      g.out_half = n * L->K * L->w1.rows_p;
+    }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
+  if (up_split) {
+    SwigluPartsArgs sa{};
+    sa.parts = p.upart;
+    sa.part_stride = n * L->K * L->w1.rows_p;
+    sa.act = p.act;
+    sa.nparts = kGateUpSplit;
+    sa.rows = (uint32_t)(n * L->K);
+    sa.F = L->F;
+    sa.rows_p = L->w1.rows_p;
+    sa.act_stride = L->Fp;
+    sa.alpha = L->alpha;
+    sa.limit = L->limit;
+    ProfScope ps(L, s, kKGateUp);
+    st = check_launch(launch_swiglu_parts(sa, s), "gate_up SwiGLU launch");
+    if (st != BURNEXT_OK) return st;
+  }
   st = gemv(false);
   if (st != BURNEXT_OK) return st;
 

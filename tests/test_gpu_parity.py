@@ -375,6 +375,25 @@ def test_moe_basic_zero_weights_residual(M):
     layer.close()
 
 
+@pytest.mark.parametrize("D,F,E,K,n,dtype", [
+    (2880, 2880, 128, 4, 1, "bf16"),  # 120B-shaped single token: 4 experts, gate_up in K-parts
+    (512, 384, 8, 2, 1, "f32"),       # f32 activations (3 bf16 terms) through the K-parts
+    (512, 384, 8, 2, 3, "bf16"),
+])
+def test_forward_gate_up_k_split(M, oracle, D, F, E, K, n, dtype):
+    """Decode batches touching few experts: gate_up writes K-part pre-activations and a separate
+    kernel sums them (in order) and applies the clamped SwiGLU."""
+    from burnext_amd import synth
+    L = _make(synth, D, F, E, K, seed=13, dtype=dtype, with_gamma=True)
+    x = synth.make_tokens(n, D, seed=14, dtype=dtype)
+    print(f"gate_up K-split case D={D} F={F} E={E} K={K} n={n} {dtype}", flush=True)
+    y, y_ref = _forward_case(M, oracle, L, x, dtype)
+    err = oracle.max_abs_rel(y, y_ref)
+    print(f"  max-abs-rel {err:.3e}")
+    assert np.isfinite(y).all()
+    assert err <= (TOL_F32 if dtype == "f32" else TOL_BF16)
+
+
 def test_forward_deterministic(M):
     from burnext_amd import synth
     L = _make(synth, 2880, 2880, 32, 4, seed=2, dtype="bf16")
