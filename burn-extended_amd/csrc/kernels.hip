@@ -1250,7 +1250,7 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // reason.  No branch surrounds a weight load.
 template <int NT, bool GATE_UP, typename XT, int SPLIT>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
-  static_assert(SPLIT >= 1 && (GATE_UP ? (SPLIT == 1 || SPLIT == (int)kGateUpSplit) : SPLIT <= (int)kDownSplit),
+  static_assert(SPLIT >= 1 && (GATE_UP ? (SPLIT == 1 || SPLIT == (int)kGateUpSplit) : (SPLIT <= (int)kDownSplit || SPLIT == (int)kDownSplitFew)),
                 "K-parts of the units");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr uint32_t CJ = kGemvKgPerWave;
@@ -1653,12 +1653,14 @@ hipError_t configure_kernels() {
   BX_ATTR((expert_gemv_kernel<1, true, float, kGateUpSplit>));
   BX_ATTR((expert_gemv_kernel<1, false, float, 1>));
   BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplitFew>));
   BX_ATTR((expert_gemv_kernel<3, true, uint16_t, 1>));
   BX_ATTR((expert_gemv_kernel<3, true, float, 1>));
   BX_ATTR((expert_gemv_kernel<3, true, uint16_t, kGateUpSplit>));
   BX_ATTR((expert_gemv_kernel<3, true, float, kGateUpSplit>));
   BX_ATTR((expert_gemv_kernel<3, false, float, 1>));
   BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplit>));
+  BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplitFew>));
 #undef BX_ATTR
   return err;
 }
@@ -1772,12 +1774,14 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
   const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
-  if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit) return hipErrorInvalidValue;
+  if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
   const bool split = !gate_up && a.ksplit > 1u;
   const bool usplit = gate_up && a.ksplit > 1u;
   if (nt == 1) {
-    if (split)
+    if (split && a.ksplit == kDownSplitFew)
+      expert_gemv_kernel<1, false, float, kDownSplitFew><<<g, block, lds, s>>>(a);
+    else if (split)
       expert_gemv_kernel<1, false, float, kDownSplit><<<g, block, lds, s>>>(a);
     else if (!gate_up)
       expert_gemv_kernel<1, false, float, 1><<<g, block, lds, s>>>(a);
@@ -1790,7 +1794,9 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
     else
       expert_gemv_kernel<1, true, float, 1><<<g, block, lds, s>>>(a);
   } else if (nt == 3) {
-    if (split)
+    if (split && a.ksplit == kDownSplitFew)
+      expert_gemv_kernel<3, false, float, kDownSplitFew><<<g, block, lds, s>>>(a);
+    else if (split)
       expert_gemv_kernel<3, false, float, kDownSplit><<<g, block, lds, s>>>(a);
     else if (!gate_up)
       expert_gemv_kernel<3, false, float, 1><<<g, block, lds, s>>>(a);
@@ -1874,7 +1880,7 @@ __global__ __launch_bounds__(256) void combine_rows8_kernel(CombineArgs a) {
 
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
-  if (a.nparts != 1u && a.nparts != kDownSplit) return hipErrorInvalidValue;
+  if (a.nparts != 1u && a.nparts != kDownSplit && a.nparts != kDownSplitFew) return hipErrorInvalidValue;
   if (a.part_bf16 && a.nparts != 1u) return hipErrorInvalidValue;
   if (a.part_bf16 && x_bf16 && a.D % 8u == 0u && (((uintptr_t)a.x | (uintptr_t)a.y) & 15u) == 0u) {
     combine_rows8_kernel<<<dim3((a.D + 2047u) / 2048u, a.n), dim3(256), 0, s>>>(a);
@@ -1888,6 +1894,11 @@ hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
       combine_kernel<uint16_t, 1, false><<<grid, block, 0, s>>>(a);
     else
       combine_kernel<float, 1, false><<<grid, block, 0, s>>>(a);
+  } else if (a.nparts == kDownSplitFew) {
+    if (x_bf16)
+      combine_kernel<uint16_t, kDownSplitFew, false><<<grid, block, 0, s>>>(a);
+    else
+      combine_kernel<float, kDownSplitFew, false><<<grid, block, 0, s>>>(a);
   } else {
     if (x_bf16)
       combine_kernel<uint16_t, kDownSplit, false><<<grid, block, 0, s>>>(a);

@@ -200,6 +200,7 @@ constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert G
 // K-parts per gate_up row tile when a batch touches so few experts that whole row tiles leave most
 // waves idle (gate_up then writes partial pre-activations, swiglu_parts_kernel finishes them)
 constexpr uint32_t kGateUpSplit = 4;
+constexpr uint32_t kDownSplitFew = 4;  // K-parts per down row tile for the same batches
 constexpr uint32_t kMaxTopK = 32;
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel

@@ -311,7 +311,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   }
   // decode-sized batches split the down projection's K range in up to kDownSplit parts: a
   // partial-sum buffer each
-  w.ypart = take(nk * L.Dp * 4 * (n <= kSmallRouteMaxTokens ? kDownSplit : 1));
+  w.ypart = take(nk * L.Dp * 4 * (gate_up_split(L, n) ? kDownSplitFew : n <= kSmallRouteMaxTokens ? kDownSplit : 1));
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   if (gate_up_split(L, n)) w.upart = take((uint64_t)kGateUpSplit * nk * L.w1.rows_p * 4);
   w.total = off;
@@ -770,8 +770,10 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
   // evenly over the waves; measured slower from 64 tokens on)
-  const uint32_t ksplit = (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
   const bool up_split = gate_up_split(*L, n) && p.upart;
+  // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
+  const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
+                        : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
   st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
