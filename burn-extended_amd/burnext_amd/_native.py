@@ -27,8 +27,8 @@ GATE_UP_INTERLEAVED = 1
 APPLY_RMSNORM = 1
 ADD_RESIDUAL = 2
 FORWARD_DEFAULT = APPLY_RMSNORM | ADD_RESIDUAL
-NUM_KERNELS = 6
-KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine"]
+NUM_KERNELS = 7
+KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine", "swiglu"]
 
 # Every symbol include/burnext_moe.h declares.
 EXPORTS = ["burnext_moe_layer_create", "burnext_moe_layer_destroy", "burnext_moe_workspace_size",

@@ -396,7 +396,7 @@ struct ProfScope {
   }
 };
 
-enum KernelId { kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5 };
+enum KernelId { kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5, kKSwiglu = 6 };
 
 burnext_status check_launch(hipError_t e, const char *what) {
   if (e != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
@@ -842,7 +842,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     sa.act_stride = L->Fp;
     sa.alpha = L->alpha;
     sa.limit = L->limit;
-    ProfScope ps(L, s, kKGateUp);
+    ProfScope ps(L, s, kKSwiglu);
     st = check_launch(launch_swiglu_parts(sa, s), "gate_up SwiGLU launch");
     if (st != BURNEXT_OK) return st;
   }

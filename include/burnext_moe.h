@@ -133,9 +133,10 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
 /* Per-kernel timing hook (HIP events around each launch of forward on its stream).
  * enable != 0 starts recording; read returns, per kernel id, accumulated milliseconds and
  * launch counts since the last read (it synchronises on the recorded events) and resets.
- * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine (batches of at most 16
- * tokens run top-k and dispatch as one kernel, recorded under id 1; id 2 then records nothing). */
-#define BURNEXT_NUM_KERNELS 6
+ * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine, 6 SwiGLU of the gate_up
+ * K-parts (batches of at most 16 tokens run top-k and dispatch as one kernel, recorded under id 1;
+ * id 2 then records nothing; id 6 records only decode batches that touch few experts). */
+#define BURNEXT_NUM_KERNELS 7
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t layer, int enable);
 burnext_status burnext_moe_profile_read(burnext_moe_layer_t layer, double *ms_total, uint64_t *launches,
                                         int n_kernels);
