@@ -1,15 +1,20 @@
 """Benchmark of the MI355X MoE feed-forward (MXFP4 experts) on one GPU.
 
-Default workload: GPT-OSS-20B-shaped MoE layer, decode (T=8 tokens, D=F=2880, E=32, top-4, bf16
-activations, MXFP4 expert weights, seeded synthetic data).  One step = one full layer forward
+Headline workload: GPT-OSS-20B-shaped MoE layer, decode (C2: T=8 tokens, D=F=2880, E=32, top-4,
+bf16 activations, MXFP4 expert weights, seeded synthetic data).  One step = one full layer forward
 (RmsNorm -> router -> top-k/softmax -> dispatch -> gate_up+SwiGLU -> down -> combine + residual)
-with inputs already resident in HBM.  Four device copies of the layer are rotated so that the
-256 MB Infinity Cache cannot serve a step's ~280 MB of expert weights from the previous step.
+with inputs already resident in HBM.  Several device copies of the layer are rotated so that the
+256 MB Infinity Cache cannot serve a step's expert weights from the previous step.
 
-Prints ONE JSON line (rank 0): metric/value/unit plus a `roofline` object for the dominant kernel
-(algorithmic bytes / FLOPs from the realised routing, divided by that kernel's average duration
-measured with HIP events on the launch stream) and a `cpu_baseline` object (the CPU restatement
-of the reference algorithm, timed on a bounded sample of the same workload on the host cores).
+The same run also measures the metric's prefill half (C3: T=4096 with the calibrated Zipf router
+bias) as the `prefill` object, and the GPT-OSS-120B-shaped layer (C4: E=128) at T = 1, 64 and 8192
+as `sweep_120b`.  `--workload NAME` measures one workload alone (profiling runs).
+
+Prints ONE JSON line: metric/value/unit plus, per workload, a `roofline` object for the dominant
+kernel (algorithmic bytes or FLOPs from the realised routing, divided by that kernel's average
+execution time: HIP events bound to each kernel dispatch, the kernel's own begin/end timestamps as
+rocprofv3's kernel trace reports them) and a `cpu_baseline` object (the CPU restatement of the
+reference algorithm, timed on a bounded sample of the same workload on the host cores).
 """
 from __future__ import annotations
 
@@ -26,14 +31,16 @@ sys.path.insert(0, str(ROOT / "burn-extended_amd"))
 METRIC = "MoE-layer tokens/s + HBM GB/s (decode) / FP4 MFMA util (prefill), 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 FP4_PEAK_TFLOPS = 10100.0
+ZIPF_S = 1.1
 
 WORKLOADS = {
-    "20b_decode": dict(D=2880, F=2880, E=32, K=4, T=8, zipf=False),
-    "20b_prefill": dict(D=2880, F=2880, E=32, K=4, T=4096, zipf=True),
-    "120b_t1": dict(D=2880, F=2880, E=128, K=4, T=1, zipf=False),
-    "120b_t64": dict(D=2880, F=2880, E=128, K=4, T=64, zipf=False),
-    "120b_t8192": dict(D=2880, F=2880, E=128, K=4, T=8192, zipf=False),
+    "20b_decode": dict(D=2880, F=2880, E=32, K=4, T=8, zipf=False, copies=4),
+    "20b_prefill": dict(D=2880, F=2880, E=32, K=4, T=4096, zipf=True, copies=4),
+    "120b_t1": dict(D=2880, F=2880, E=128, K=4, T=1, zipf=False, copies=8),
+    "120b_t64": dict(D=2880, F=2880, E=128, K=4, T=64, zipf=False, copies=4),
+    "120b_t8192": dict(D=2880, F=2880, E=128, K=4, T=8192, zipf=False, copies=4),
 }
+TIMING = "kernel dispatch begin/end (HIP event pair bound to each dispatch by hipExtLaunchKernel)"
 
 
 def parse():
@@ -41,10 +48,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="20b_decode", choices=sorted(WORKLOADS))
-    ap.add_argument("--copies", type=int, default=4, help="device copies of the layer rotated per step")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--workload", default=None, choices=sorted(WORKLOADS),
+                    help="measure this workload alone (default: 20b_decode headline + prefill + 120B sweep)")
+    ap.add_argument("--copies", type=int, default=0, help="device copies of the layer rotated per step (0: per workload)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of each CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-120b", action="store_true", help="skip the 120B sweep of the default run")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     return ap.parse_args()
@@ -64,32 +73,38 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}), flush=True)
 
 
-def main():
-    args = parse()
-    if args.copy_probe:
-        copy_probe(args.copy_probe)
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (one MI355X per run); "
-              "run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_data(name):
+    from burnext_amd import synth
+    wl = WORKLOADS[name]
+    bias = synth.zipf_router_bias(wl["E"], ZIPF_S, gamma=synth.ZIPF_GAMMA_C3, seed=0) if wl["zipf"] else None
+    return synth.make_layer(wl["D"], wl["F"], wl["E"], wl["K"], seed=0, dtype="bf16", router_bias=bias)
+
+
+def make_layers(data, copies, dev=0):
+    from burnext_amd import moe
+    layers = []
+    for i in range(copies):
+        layers.append(moe.MoeLayer(data, device=dev))
+    log(f"{copies} device copies of the E={data.num_experts} layer resident")
+    return layers
+
+
+def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
+    """Times `steps` layer forwards (after `warmup`) on resident inputs; returns the workload's
+    figures: tokens/s, per-kernel execution times, the dominant kernel's roofline, routing."""
     import numpy as np
     import torch
 
     from burnext_amd import moe, synth
 
-    wl = WORKLOADS[args.workload]
+    wl = WORKLOADS[name]
     D, F, E, K, T = wl["D"], wl["F"], wl["E"], wl["K"], wl["T"]
-    dev = 0
-    torch.cuda.set_device(dev)
-    bias = synth.zipf_router_bias(E, 1.1, gamma=1.0, seed=0) if wl["zipf"] else None
-    data = synth.make_layer(D, F, E, K, seed=0, dtype="bf16", router_bias=bias)
-    layers = []
-    for i in range(max(1, args.copies)):
-        layers.append(moe.MoeLayer(data, device=dev))
-        print(f"[bench] layer copy {i + 1}/{max(1, args.copies)} resident", file=sys.stderr, flush=True)
     x_np = synth.make_tokens(T, D, seed=0, dtype="bf16")
-    x = moe.to_device_x(x_np, "bf16", dev)
+    x = moe.to_device_x(x_np, "bf16", 0)
     y = torch.empty_like(x)
     ws = layers[0].workspace(T)
 
@@ -102,35 +117,34 @@ def main():
     def step(i):
         layers[i % len(layers)].forward(x, out=y, workspace=ws)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     end.record()
     torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
-    ms_step = ms_total / args.steps
+    ms_step = start.elapsed_time(end) / steps
 
-    # per-kernel durations: HIP event pairs recorded by the library around each launch on the
-    # launch stream, over a second pass of the same steps
+    # per-kernel execution times over a second pass of the same steps
     for L in layers:
         L.profile_enable(True)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     kern = {}
     for L in layers:
         L.profile_enable(False)
-        for name, (ms, cnt) in L.profile_read().items():
-            a = kern.setdefault(name, [0.0, 0])
+        for k, (ms, cnt) in L.profile_read().items():
+            a = kern.setdefault(k, [0.0, 0])
             a[0] += ms
             a[1] += cnt
     kavg_us = {k: (v[0] / v[1] * 1e3) for k, v in kern.items() if v[1]}
+    log(f"{name}: {ms_step * 1e3:.1f} us/step, kernels {', '.join(f'{k} {v:.1f}' for k, v in kavg_us.items())}")
 
-    # algorithmic bytes per launch (realised routing; bf16 biases/router/activations)
+    # algorithmic bytes / FLOPs per launch (realised routing; bf16 biases, router, activations)
     nk = T * K
     w1_bytes = 2 * F * ((D + 1) // 2) + 2 * F * ((D + 31) // 32) + 2 * F * 2
     w2_bytes = D * ((F + 1) // 2) + D * ((F + 31) // 32)
@@ -142,56 +156,51 @@ def main():
     }
     kflops = {"gate_up": 2 * nk * 2 * F * D, "down": 2 * nk * D * F}
     layer_bytes = synth.decode_bytes(data, touched, T, 2)
-    dominant = max(kavg_us, key=kavg_us.get)
-    traffic = measured_traffic(args.workload, dominant)
-    if T >= 1024:
-        fl = kflops.get(dominant, 0)
-        ach = fl / (kavg_us[dominant] * 1e-6) / 1e12
-        roof = {"bound": "mfma", "kernel": dominant, "achieved": round(ach, 2), "peak": FP4_PEAK_TFLOPS,
+    stage_us = dict(kavg_us)
+    gate_label = "gate_up"
+    if "swiglu" in stage_us:  # few-expert decode: the gate_up stage is the K-part GEMV + its SwiGLU kernel
+        stage_us["gate_up"] = stage_us["gate_up"] + stage_us.pop("swiglu")
+        gate_label = "gate_up+swiglu"
+    dominant = max((k for k in stage_us if k in kbytes), key=stage_us.get)
+    label = gate_label if dominant == "gate_up" else dominant
+    traffic = measured_traffic(name, dominant)
+    prefill = T >= 1024
+    if prefill:
+        fl = kflops[dominant]
+        ach = fl / (stage_us[dominant] * 1e-6) / 1e12
+        roof = {"bound": "mfma", "kernel": label, "achieved": round(ach, 2), "peak": FP4_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / FP4_PEAK_TFLOPS, 4), "traffic": traffic,
-                "algorithmic_flops_per_launch": fl, "avg_launch_us": round(kavg_us[dominant], 2)}
+                "algorithmic_flops_per_launch": fl, "avg_launch_us": round(stage_us[dominant], 2), "timing": TIMING}
     else:
-        b = kbytes.get(dominant, 0)
-        ach = b / (kavg_us[dominant] * 1e-6) / 1e9
-        roof = {"bound": "hbm", "kernel": dominant, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        b = kbytes[dominant]
+        ach = b / (stage_us[dominant] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": label, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes_per_launch": b,
-                "avg_launch_us": round(kavg_us[dominant], 2)}
-
+                "avg_launch_us": round(stage_us[dominant], 2), "timing": TIMING}
     out = {
-        "metric": METRIC,
         "value": round(T / (ms_step * 1e-3), 1),
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) bf16 activations, MXFP4 weights with random e2m1 codes and e8m0 "
-                "scales 119..123, random-init router/biases)",
-        "config": {"workload": f"gpt-oss-20b MoE layer {args.workload}" if E == 32 else f"gpt-oss-120b MoE layer {args.workload}",
-                   "tokens": T, "d_model": D, "ffn_hidden": F, "experts": E, "top_k": K,
-                   "weights": "mxfp4 (e2m1 + e8m0 per 32)", "activations": "bf16", "gate_up_layout": "interleaved",
-                   "layer_copies_rotated": len(layers), "touched_experts": touched,
-                   "max_segment": int(counts.max())},
+        "config": {"workload": f"gpt-oss-{'20b' if E == 32 else '120b'} MoE layer {name}", "tokens": T, "d_model": D,
+                   "ffn_hidden": F, "experts": E, "top_k": K, "weights": "mxfp4 (e2m1 + e8m0 per 32)",
+                   "activations": "bf16", "gate_up_layout": "interleaved", "layer_copies_rotated": len(layers),
+                   "touched_experts": touched, "max_segment": int(counts.max())},
         "layer_hbm_gbs": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
         "layer_hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "layer_algorithmic_bytes": layer_bytes,
         "kernels_avg_us": {k: round(v, 2) for k, v in kavg_us.items()},
         "roofline": roof,
     }
-    if T >= 1024:
-        fl = 6 * T * K * F * D
-        out["layer_fp4_mfma_util"] = round(fl / (ms_step * 1e-3) / 1e12 / FP4_PEAK_TFLOPS, 4)
-
-    print(f"[bench] timed {args.steps} steps: {ms_step * 1e3:.1f} us/step", file=sys.stderr, flush=True)
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(data, x_np, args.cpu_seconds)
-    for L in layers:
-        L.close()
-    print(json.dumps(out), flush=True)
+    if prefill:
+        out["layer_fp4_mfma_util"] = round(6 * T * K * F * D / (ms_step * 1e-3) / 1e12 / FP4_PEAK_TFLOPS, 4)
+    if wl["zipf"]:
+        by_rank = synth.zipf_rank_counts_from_idx(idx_np, E, seed=0)
+        out["config"]["router_bias"] = f"zipf s={ZIPF_S} gamma={synth.ZIPF_GAMMA_C3} (calibrated)"
+        out["segment_histogram_by_zipf_rank"] = by_rank.tolist()
+        out["segment_ideal_by_zipf_rank"] = [int(round(v)) for v in synth.zipf_ideal_counts(E, ZIPF_S, T, K)]
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline(data, x_np, cpu_seconds)
+    return out
 
 
 def measured_traffic(workload, kernel):
@@ -212,7 +221,7 @@ def measured_traffic(workload, kernel):
 def cpu_baseline(data, x_np, budget_s):
     """Reference algorithm restated on the CPU (oracle/moe_oracle.c, literal loop structure of
     src/moe/mod.rs:129-411 with b2 added once), OpenMP over the host cores, on whole layer
-    forwards of the same tokens until the time budget is spent."""
+    forwards of the same tokens (the first 256 of a larger batch) until the time budget is spent."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
 
@@ -226,9 +235,10 @@ def cpu_baseline(data, x_np, budget_s):
         el = time.perf_counter() - t0
         if el >= budget_s or n_fwd >= 50:
             break
+    what = f"{rows.shape[0]} tokens" if T <= 256 else f"the first {rows.shape[0]} of the {T} tokens"
     return {"value": round(n_fwd * rows.shape[0] / el, 2), "unit": "tokens/s", "cores": O.num_threads(),
             "kind": "port",
-            "sample": f"{n_fwd} layer forward(s) of {rows.shape[0]} tokens of this workload in {el:.1f} s "
+            "sample": f"{n_fwd} layer forward(s) of {what} of this workload in {el:.1f} s "
                       f"(reference algorithm restated in C, f32, dense W1 per used expert)",
             "cpu": _cpu_model()}
 
@@ -241,6 +251,58 @@ def _cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def main():
+    args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (one MI355X per run); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    torch.cuda.set_device(0)
+    head = args.workload or "20b_decode"
+    data = make_data(head)
+    layers = make_layers(data, args.copies or WORKLOADS[head]["copies"])
+    res = measure(head, layers, data, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
+    for L in layers:
+        L.close()
+    del layers
+    out = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (seeded N(0,1) bf16 activations, MXFP4 weights with random e2m1 codes and e8m0 "
+                   "scales 119..123, random-init router/biases)"}
+    out.update(res)
+    if args.workload is None:
+        # the metric's prefill half (C3), same run
+        pdata = make_data("20b_prefill")
+        layers = make_layers(pdata, WORKLOADS["20b_prefill"]["copies"])
+        out["prefill"] = measure("20b_prefill", layers, pdata, args.steps, args.warmup, not args.no_cpu,
+                                 args.cpu_seconds)
+        for L in layers:
+            L.close()
+        del layers
+        if not args.no_120b:
+            # 120B (C4): one set of layer copies serves the three batch sizes
+            bdata = make_data("120b_t64")
+            layers = make_layers(bdata, WORKLOADS["120b_t1"]["copies"])
+            sweep = {}
+            for name in ("120b_t1", "120b_t64", "120b_t8192"):
+                use = layers[:WORKLOADS[name]["copies"]]
+                r = measure(name, use, bdata, args.steps, args.warmup, False, 0)
+                sweep[name.split("_")[1]] = {k: r[k] for k in ("value", "unit", "ms_per_step", "layer_hbm_frac",
+                                                                "layer_fp4_mfma_util", "kernels_avg_us", "roofline",
+                                                                "config") if k in r}
+            out["sweep_120b"] = sweep
+            for L in layers:
+                L.close()
+            del layers
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -1,6 +1,7 @@
 """Builds the HIP library libburnext_moe.so (gfx950) in-tree: burn-extended_amd/lib/."""
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import pathlib
 import shutil
@@ -23,12 +24,12 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-tar
 
 def build(verbose: bool = False) -> pathlib.Path:
     LIB_DIR.mkdir(exist_ok=True)
-    objs = []
-    for src in SOURCES:
-        obj = LIB_DIR / (src.rsplit(".", 1)[0] + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-        _run(cmd, verbose)
-        objs.append(str(obj))
+    objs = [str(LIB_DIR / (src.rsplit(".", 1)[0] + ".o")) for src in SOURCES]
+    cmds = [[HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", obj] for src, obj in zip(SOURCES, objs)]
+    # the translation units compile independently: one hipcc process each
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "--offload-arch=gfx950", "-o", str(tmp), *objs, "-lpthread"], verbose)
     shutil.move(str(tmp), str(LIB))

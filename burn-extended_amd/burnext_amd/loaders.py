@@ -142,9 +142,23 @@ def _modelbin_layout(h: ModelBinHeader) -> _ModelBinLayout:
     return _ModelBinLayout(norm, gate, experts, off)
 
 
-def load_modelbin_moe(path, layers=None, gate_up_layout: str = "halves") -> list[MoeLayerData]:
+GATE_UP_LAYOUTS = ("interleaved", "halves")
+
+
+def load_modelbin_moe(path, layers=None, gate_up_layout: str = "interleaved") -> list[MoeLayerData]:
     """The MoE layers of a model.bin as ``MoeLayerData`` (bf16 biases / router / norm, scales as
-    stored with ``ue8_offset`` 14).  ``layers``: indices to load (default all)."""
+    stored with ``ue8_offset`` 14).  ``layers``: indices to load (default all).
+
+    ``gate_up_layout`` names the row order of the stored mlp1 (W1) rows and b1:
+      * "interleaved" (default): row 2f is the gate and row 2f + 1 the linear unit of feature f.
+        The exporter copies GPT-OSS checkpoint rows verbatim (src/bin/gptoss_export.rs:553-555)
+        and the checkpoints interleave them (the crate's own swiglu_clamp pairs them so,
+        src/activation/mod.rs:5-12), so this is the layer a real model.bin holds.
+      * "halves": rows [0, F) gate and [F, 2F) linear -- the pairing the reference's resident
+        kernel applies to whatever it is given (src/quant/gpu.rs:112-113, src/moe/mod.rs:336-337).
+        Opt in to reproduce that kernel's outputs on a real file bit for bit in row pairing."""
+    if gate_up_layout not in GATE_UP_LAYOUTS:
+        raise ValueError(f"gate_up_layout must be one of {GATE_UP_LAYOUTS}, got {gate_up_layout!r}")
     h = read_modelbin_header(path)
     lay = _modelbin_layout(h)
     mm = np.memmap(path, dtype=np.uint8, mode="r")

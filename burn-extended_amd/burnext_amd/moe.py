@@ -71,12 +71,13 @@ def _stream(stream) -> ctypes.c_void_p:
 class MoeLayer:
     """One device-resident MoE layer (burnext_moe_layer_create / _destroy)."""
 
-    def __init__(self, data: MoeLayerData, device: int = 0, gate_up_layout: str | None = None):
+    def __init__(self, data: MoeLayerData, device: int = 0, gate_up_layout: str | None = None, disabled: bool = False):
         self.data = data
         self.device = device
         D, F, E, K = data.d_model, data.ffn_hidden, data.num_experts, data.experts_per_token
         self.k = min(max(K, 1), E)
-        cfg = N.MoeConfigC(D, F, E, K, data.swiglu_alpha, data.swiglu_limit, data.rms_eps, 0)
+        cfg = N.MoeConfigC(D, F, E, K, data.swiglu_alpha, data.swiglu_limit, data.rms_eps,
+                           1 if disabled else 0)
         d1 = N.MxFp4Desc.for_matrix(E, 2 * F, D, data.ue8_offset)
         d2 = N.MxFp4Desc.for_matrix(E, D, F, data.ue8_offset)
         arrs = {k: np.ascontiguousarray(getattr(data, k)) for k in ("w1_blocks", "w1_scales", "w2_blocks", "w2_scales")}
@@ -164,6 +165,21 @@ class MoeLayer:
                                              ctypes.c_void_p(seg.data_ptr()), ctypes.c_void_p(perm.data_ptr()),
                                              ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
         return seg, perm
+
+    def route_dispatch(self, x: torch.Tensor, flags: int = N.APPLY_RMSNORM, stream=None):
+        """Routing and dispatch as the forward runs them for this batch size (for n <= 16 the
+        fused one-workgroup kernel): (topk_idx, topk_w, seg_offsets, perm)."""
+        n = x.numel() // self.data.d_model
+        idx = torch.empty((n, self.k), dtype=torch.int32, device=x.device)
+        w = torch.empty((n, self.k), dtype=torch.float32, device=x.device)
+        seg = torch.empty(self.data.num_experts + 1, dtype=torch.int32, device=x.device)
+        perm = torch.empty(n * self.k, dtype=torch.int32, device=x.device)
+        ws = self.workspace(n, stream)
+        N.check(N.lib().burnext_moe_route_dispatch(
+            self.handle, ctypes.c_void_p(x.data_ptr()), _x_dtype(x), n, flags, ctypes.c_void_p(idx.data_ptr()),
+            ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(seg.data_ptr()), ctypes.c_void_p(perm.data_ptr()),
+            ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+        return idx, w, seg, perm
 
     def profile_enable(self, on: bool = True) -> None:
         N.check(N.lib().burnext_moe_profile_enable(self.handle, 1 if on else 0))

@@ -147,6 +147,59 @@ def zipf_router_bias(num_experts: int, s: float = 1.1, gamma: float = 1.0, seed:
     return (-s * np.log(r.astype(np.float64)) * gamma).astype(np.float32)
 
 
+# gamma of the C3 prefill router bias: calibrate_zipf_gamma() on the benchmark's seed-0 layer and
+# tokens (T = 4096, D = 2880, E = 32, k = 4).  Realised routed entries by popularity rank: 2764,
+# 2054, 1514, ..., 100, 98 against the ideal s = 1.1 shares 4096 (capped: a token takes an expert
+# once), 2168, 1388, ..., 106, 102.
+ZIPF_GAMMA_C3 = 0.70
+
+
+def zipf_rank_counts_from_idx(idx: np.ndarray, num_experts: int, seed: int = 0) -> np.ndarray:
+    """Routed entries per expert of a top-k index array, listed by the expert's Zipf popularity
+    rank 1..E of zipf_router_bias(seed)."""
+    c = np.bincount(np.asarray(idx).ravel(), minlength=num_experts)
+    rank = _rng(seed, _S_ZIPF).permutation(num_experts)
+    out = np.zeros(num_experts, np.int64)
+    out[rank] = c
+    return out
+
+
+def zipf_rank_counts(logits: np.ndarray, k: int, num_experts: int, seed: int = 0) -> np.ndarray:
+    """zipf_rank_counts_from_idx of the top-k (largest first, ties to the lower index) of each row
+    of ``logits``."""
+    return zipf_rank_counts_from_idx(np.argsort(-logits, axis=1, kind="stable")[:, :k], num_experts, seed)
+
+
+def zipf_ideal_counts(num_experts: int, s: float, tokens: int, k: int) -> np.ndarray:
+    """Ideal routed entries by rank: tokens * k * r^-s / H, capped at `tokens` (an expert is taken at
+    most once per token)."""
+    r = np.arange(1, num_experts + 1, dtype=np.float64)
+    p = r ** -s / np.sum(r ** -s)
+    return np.minimum(p * tokens * k, tokens)
+
+
+def calibrate_zipf_gamma(layer: MoeLayerData, x: np.ndarray, s: float = 1.1, seed: int = 0,
+                         grid=np.arange(0.30, 2.001, 0.05)) -> tuple[float, np.ndarray]:
+    """The gamma of zipf_router_bias whose realised routing of tokens ``x`` (float64 router on the
+    RMS-normed rows, bf16 bias) is closest to the ideal Zipf(s) entry counts in log space.
+    Returns (gamma, realised counts by rank)."""
+    T, E, K = x.shape[0], layer.num_experts, layer.experts_per_token
+    x64 = x.astype(np.float64)
+    xn = x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + layer.rms_eps)
+    if layer.gamma_f32 is not None:
+        xn = xn * layer.gamma_f32.astype(np.float64)
+    base = xn @ layer.router_w_f32.astype(np.float64).T
+    ideal = np.log(zipf_ideal_counts(E, s, T, K))
+    best = None
+    for g in grid:
+        b = round_bf16(zipf_router_bias(E, s, gamma=float(g), seed=seed)).astype(np.float64)
+        c = zipf_rank_counts(base + b, K, E, seed)
+        err = float(np.sum((np.log(np.maximum(c, 0.5)) - ideal) ** 2))
+        if best is None or err < best[0]:
+            best = (err, round(float(g), 2), c)
+    return best[1], best[2]
+
+
 # Benchmark configurations (D, F, E, k, T, activation dtype).
 CONFIGS = {
     "tiny": dict(d_model=256, ffn_hidden=256, num_experts=2, experts_per_token=2, tokens=16, dtype="f32"),
@@ -169,5 +222,6 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
-__all__ = ["MoeLayerData", "make_layer", "make_tokens", "zipf_router_bias", "f32_to_bf16_bits", "bf16_bits_to_f32",
+__all__ = ["MoeLayerData", "make_layer", "make_tokens", "zipf_router_bias", "ZIPF_GAMMA_C3", "calibrate_zipf_gamma",
+           "zipf_rank_counts", "zipf_rank_counts_from_idx", "zipf_ideal_counts", "f32_to_bf16_bits", "bf16_bits_to_f32",
            "round_bf16", "CONFIGS", "decode_bytes", "ceil_div", "math"]

@@ -371,9 +371,9 @@ hipError_t configure_gemm_kernels() {
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s) {
   if (grid == 0 || (grid & 7u) != 0 || a.nrb == 0 || a.b.kq % 128u != 0) return hipErrorInvalidValue;
   if (gate_up)
-    expert_gemm_kernel<true><<<dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s>>>(a);
+    (void)launch_kernel(expert_gemm_kernel<true>, dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s, a);
   else
-    expert_gemm_kernel<false><<<dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s>>>(a);
+    (void)launch_kernel(expert_gemm_kernel<false>, dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s, a);
   return hipGetLastError();
 }
 

@@ -1668,17 +1668,17 @@ hipError_t configure_kernels() {
 template <typename XT, typename WT>
 static void router_launch(const RouterArgs &a, bool vec, dim3 grid, size_t lds, hipStream_t s) {
   if (vec)
-    router_kernel<XT, WT, true><<<grid, dim3(kRouterThreads), lds, s>>>(a);
+    (void)launch_kernel(router_kernel<XT, WT, true>, grid, dim3(kRouterThreads), lds, s, a);
   else
-    router_kernel<XT, WT, false><<<grid, dim3(kRouterThreads), lds, s>>>(a);
+    (void)launch_kernel(router_kernel<XT, WT, false>, grid, dim3(kRouterThreads), lds, s, a);
 }
 
 template <typename XT, typename WT>
 static void rows_launch(const RouterArgs &a, int tokens_per_wave, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   if (tokens_per_wave == 4)
-    router_rows_kernel<XT, WT, 4><<<grid, block, lds, s>>>(a);
+    (void)launch_kernel(router_rows_kernel<XT, WT, 4>, grid, block, lds, s, a);
   else
-    router_rows_kernel<XT, WT, 2><<<grid, block, lds, s>>>(a);
+    (void)launch_kernel(router_rows_kernel<XT, WT, 2>, grid, block, lds, s, a);
 }
 
 hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, int tokens_per_wave, hipStream_t s) {
@@ -1721,11 +1721,11 @@ hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
   // at least 8 waves: the work-map writes spread over the whole workgroup
   const dim3 block(64 * max(a.n, 8u));
   if (a.E <= 64)
-    small_route_kernel<1><<<dim3(1), block, 0, s>>>(a);
+    (void)launch_kernel(small_route_kernel<1>, dim3(1), block, 0, s, a);
   else if (a.E <= 128)
-    small_route_kernel<2><<<dim3(1), block, 0, s>>>(a);
+    (void)launch_kernel(small_route_kernel<2>, dim3(1), block, 0, s, a);
   else
-    small_route_kernel<4><<<dim3(1), block, 0, s>>>(a);
+    (void)launch_kernel(small_route_kernel<4>, dim3(1), block, 0, s, a);
   return hipGetLastError();
 }
 
@@ -1734,13 +1734,13 @@ hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hip
     return hipErrorInvalidValue;
   const dim3 g(a.E), b(64 * ((a.n + 1) / 2));
   if (x_bf16 && w_bf16)
-    router_small_kernel<uint16_t, uint16_t><<<g, b, 0, s>>>(a);
+    (void)launch_kernel(router_small_kernel<uint16_t, uint16_t>, g, b, 0, s, a);
   else if (x_bf16)
-    router_small_kernel<uint16_t, float><<<g, b, 0, s>>>(a);
+    (void)launch_kernel(router_small_kernel<uint16_t, float>, g, b, 0, s, a);
   else if (w_bf16)
-    router_small_kernel<float, uint16_t><<<g, b, 0, s>>>(a);
+    (void)launch_kernel(router_small_kernel<float, uint16_t>, g, b, 0, s, a);
   else
-    router_small_kernel<float, float><<<g, b, 0, s>>>(a);
+    (void)launch_kernel(router_small_kernel<float, float>, g, b, 0, s, a);
   return hipGetLastError();
 }
 
@@ -1749,11 +1749,11 @@ hipError_t launch_topk(const TopkArgs &a, hipStream_t s) {
   const uint32_t wpb = kTopkThreads / 64;
   const dim3 grid((a.n + wpb - 1) / wpb), block(kTopkThreads);
   if (a.E <= 64)
-    topk_kernel<1><<<grid, block, 0, s>>>(a);
+    (void)launch_kernel(topk_kernel<1>, grid, block, 0, s, a);
   else if (a.E <= 128)
-    topk_kernel<2><<<grid, block, 0, s>>>(a);
+    (void)launch_kernel(topk_kernel<2>, grid, block, 0, s, a);
   else
-    topk_kernel<4><<<grid, block, 0, s>>>(a);
+    (void)launch_kernel(topk_kernel<4>, grid, block, 0, s, a);
   return hipGetLastError();
 }
 
@@ -1761,10 +1761,10 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
   if (a.n >= kDispatchWideMinTokens) {
     if (!a.chunk_cnt) return hipErrorInvalidValue;
     const dim3 grid((a.n + kDispatchChunk - 1) / kDispatchChunk), block(kDispatchChunk);
-    dispatch_count_kernel<<<grid, block, 0, s>>>(a);
-    dispatch_wide_kernel<<<grid, block, 0, s>>>(a);
+    (void)launch_kernel(dispatch_count_kernel, grid, block, 0, s, a);
+    (void)launch_kernel(dispatch_wide_kernel, grid, block, 0, s, a);
   } else {
-    dispatch_kernel<<<dim3(1), dim3(kDispatchThreads), dispatch_lds_bytes(a.E, kDispatchThreads), s>>>(a);
+    (void)launch_kernel(dispatch_kernel, dim3(1), dim3(kDispatchThreads), dispatch_lds_bytes(a.E, kDispatchThreads), s, a);
   }
   return hipGetLastError();
 }
@@ -1780,34 +1780,34 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   const bool usplit = gate_up && a.ksplit > 1u;
   if (nt == 1) {
     if (split && a.ksplit == kDownSplitFew)
-      expert_gemv_kernel<1, false, float, kDownSplitFew><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, false, float, kDownSplitFew>, g, block, lds, s, a);
     else if (split)
-      expert_gemv_kernel<1, false, float, kDownSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, false, float, kDownSplit>, g, block, lds, s, a);
     else if (!gate_up)
-      expert_gemv_kernel<1, false, float, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, false, float, 1>, g, block, lds, s, a);
     else if (usplit && x_bf16)
-      expert_gemv_kernel<1, true, uint16_t, kGateUpSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
     else if (usplit)
-      expert_gemv_kernel<1, true, float, kGateUpSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, true, float, kGateUpSplit>, g, block, lds, s, a);
     else if (x_bf16)
-      expert_gemv_kernel<1, true, uint16_t, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, true, uint16_t, 1>, g, block, lds, s, a);
     else
-      expert_gemv_kernel<1, true, float, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<1, true, float, 1>, g, block, lds, s, a);
   } else if (nt == 3) {
     if (split && a.ksplit == kDownSplitFew)
-      expert_gemv_kernel<3, false, float, kDownSplitFew><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, false, float, kDownSplitFew>, g, block, lds, s, a);
     else if (split)
-      expert_gemv_kernel<3, false, float, kDownSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, false, float, kDownSplit>, g, block, lds, s, a);
     else if (!gate_up)
-      expert_gemv_kernel<3, false, float, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, false, float, 1>, g, block, lds, s, a);
     else if (usplit && x_bf16)
-      expert_gemv_kernel<3, true, uint16_t, kGateUpSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
     else if (usplit)
-      expert_gemv_kernel<3, true, float, kGateUpSplit><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, true, float, kGateUpSplit>, g, block, lds, s, a);
     else if (x_bf16)
-      expert_gemv_kernel<3, true, uint16_t, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, true, uint16_t, 1>, g, block, lds, s, a);
     else
-      expert_gemv_kernel<3, true, float, 1><<<g, block, lds, s>>>(a);
+      (void)launch_kernel(expert_gemv_kernel<3, true, float, 1>, g, block, lds, s, a);
   } else {
     return hipErrorInvalidValue;
   }
@@ -1831,7 +1831,7 @@ __global__ __launch_bounds__(256) void swiglu_parts_kernel(SwigluPartsArgs a) {
 
 hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s) {
   if (a.rows == 0 || a.F == 0 || 2u * a.F > a.rows_p || (a.rows_p & 1u) || (a.part_stride & 1u)) return hipErrorInvalidValue;
-  swiglu_parts_kernel<<<dim3((a.F + 255u) / 256u, a.rows), dim3(256), 0, s>>>(a);
+  (void)launch_kernel(swiglu_parts_kernel, dim3((a.F + 255u) / 256u, a.rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1883,27 +1883,27 @@ hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   if (a.nparts != 1u && a.nparts != kDownSplit && a.nparts != kDownSplitFew) return hipErrorInvalidValue;
   if (a.part_bf16 && a.nparts != 1u) return hipErrorInvalidValue;
   if (a.part_bf16 && x_bf16 && a.D % 8u == 0u && (((uintptr_t)a.x | (uintptr_t)a.y) & 15u) == 0u) {
-    combine_rows8_kernel<<<dim3((a.D + 2047u) / 2048u, a.n), dim3(256), 0, s>>>(a);
+    (void)launch_kernel(combine_rows8_kernel, dim3((a.D + 2047u) / 2048u, a.n), dim3(256), 0, s, a);
   } else if (a.part_bf16) {
     if (x_bf16)
-      combine_kernel<uint16_t, 1, true><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<uint16_t, 1, true>, grid, block, 0, s, a);
     else
-      combine_kernel<float, 1, true><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<float, 1, true>, grid, block, 0, s, a);
   } else if (a.nparts == 1u) {
     if (x_bf16)
-      combine_kernel<uint16_t, 1, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<uint16_t, 1, false>, grid, block, 0, s, a);
     else
-      combine_kernel<float, 1, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<float, 1, false>, grid, block, 0, s, a);
   } else if (a.nparts == kDownSplitFew) {
     if (x_bf16)
-      combine_kernel<uint16_t, kDownSplitFew, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<uint16_t, kDownSplitFew, false>, grid, block, 0, s, a);
     else
-      combine_kernel<float, kDownSplitFew, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<float, kDownSplitFew, false>, grid, block, 0, s, a);
   } else {
     if (x_bf16)
-      combine_kernel<uint16_t, kDownSplit, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<uint16_t, kDownSplit, false>, grid, block, 0, s, a);
     else
-      combine_kernel<float, kDownSplit, false><<<grid, block, 0, s>>>(a);
+      (void)launch_kernel(combine_kernel<float, kDownSplit, false>, grid, block, 0, s, a);
   }
   return hipGetLastError();
 }
@@ -1913,7 +1913,7 @@ hipError_t launch_dequant(const DequantArgs &a, hipStream_t s) {
   uint64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (blocks == 0) return hipSuccess;
-  dequant_kernel<<<dim3((uint32_t)blocks), dim3(256), 0, s>>>(a);
+  (void)launch_kernel(dequant_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -1,9 +1,31 @@
 // kernels.hpp -- argument blocks and host-side launchers of the MoE kernels (gfx950).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace burnext {
+
+// Per-launch timing.  While a LaunchTimer is installed on the calling thread (the layer's
+// profiling scope), every launcher below binds a fresh HIP event pair to each kernel dispatch
+// through hipExtLaunchKernel: the events then carry that dispatch's own begin and end timestamps
+// (the kernel's execution time, the figure rocprofv3's kernel trace reports), not the stream
+// positions around it.  Without a timer the launch is a plain hipLaunchKernel.
+struct LaunchTimer {
+  virtual bool pair(hipEvent_t &start, hipEvent_t &stop) = 0;  // false: launch untimed
+  virtual ~LaunchTimer() = default;
+};
+extern thread_local LaunchTimer *g_launch_timer;
+
+template <typename A>
+inline hipError_t launch_kernel(void (*k)(A), dim3 grid, dim3 block, size_t lds, hipStream_t s, const A &a) {
+  A arg = a;
+  void *args[] = {(void *)&arg};
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (g_launch_timer && g_launch_timer->pair(e0, e1))
+    return hipExtLaunchKernel((const void *)k, grid, block, args, lds, s, e0, e1, 0);
+  return hipLaunchKernel((const void *)k, grid, block, args, lds, s);
+}
 
 // Two-term MXFP8 rows (see mx_device.hpp): kq code bytes per row and term, K padded to whole
 // 128-wide K-groups with zero codes and zero scale bytes, natural K order; kq / 32 scale bytes

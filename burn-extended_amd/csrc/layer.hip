@@ -17,6 +17,10 @@
 
 using namespace burnext;
 
+namespace burnext {
+thread_local LaunchTimer *g_launch_timer = nullptr;
+}
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -277,6 +281,21 @@ inline bool use_gemm_path(const burnext_moe_layer &L, uint64_t n) {
 // Row bytes of two-term MXFP8 rows over K = cols of a tiled projection (whole 128-wide K-groups).
 inline uint32_t qrow_bytes(const TiledMx &t) { return ((t.nb + 3u) / 4u) * 128u; }
 
+// Largest batch m <= min(n, kSmallRouteMaxTokens) that still splits gate_up in K-parts (0: none).
+// gate_up_split holds for m = 1 .. some bound, since the touched-expert bound min(E, m k) grows
+// with m.
+uint64_t max_split_tokens(const burnext_moe_layer &L, uint64_t n) {
+  uint64_t ms = 0;
+  for (uint64_t m = 1; m <= std::min<uint64_t>(n, kSmallRouteMaxTokens); ++m)
+    if (gate_up_split(L, m)) ms = m;
+  return ms;
+}
+
+// Workspace regions for n tokens.  Every region is sized for the largest need of any batch of
+// m <= n tokens, so burnext_moe_workspace_size(n) is non-decreasing in n and one workspace sized
+// for the largest batch serves every smaller one: the K-part buffers of decode-sized batches
+// (ypart in kDownSplitFew or kDownSplit parts, upart) are larger per token than a bigger batch's
+// single-part ypart.
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   WsLayout w{};
   uint64_t off = 0;
@@ -286,6 +305,7 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     return o;
   };
   const uint64_t nk = n * L.K;
+  const uint64_t ms = max_split_tokens(L, n), ns = std::min<uint64_t>(n, kSmallRouteMaxTokens);
   w.rms = take(n * 4);
   w.logits = take(n * L.E * 4);
   w.topk_idx = take(nk * 4);
@@ -309,11 +329,12 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[2] = take(nk * ka / 32);
     w.aq[3] = take(nk * ka / 32);
   }
-  // decode-sized batches split the down projection's K range in up to kDownSplit parts: a
-  // partial-sum buffer each
-  w.ypart = take(nk * L.Dp * 4 * (gate_up_split(L, n) ? kDownSplitFew : n <= kSmallRouteMaxTokens ? kDownSplit : 1));
+  // decode-sized batches split the down projection's K range in parts (kDownSplitFew when gate_up
+  // is split too, else kDownSplit): a partial-sum buffer each, sized for the largest m <= n
+  const uint64_t yrows = std::max({nk, ns * L.K * kDownSplit, ms * L.K * kDownSplitFew});
+  w.ypart = take(yrows * L.Dp * 4);
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
-  if (gate_up_split(L, n)) w.upart = take((uint64_t)kGateUpSplit * nk * L.w1.rows_p * 4);
+  if (ms) w.upart = take((uint64_t)kGateUpSplit * ms * L.K * L.w1.rows_p * 4);
   w.total = off;
   return w;
 }
@@ -374,25 +395,32 @@ uint32_t router_tb(const burnext_moe_layer &L, uint64_t n, uint32_t epw) {
   return tb;
 }
 
-// Records a HIP event pair around a launch when profiling is on.
-struct ProfScope {
+// While profiling is on, binds a HIP event pair to every kernel dispatch launched in its scope
+// (hipExtLaunchKernel through the thread's LaunchTimer), recorded under kernel id k: the pair
+// measures each dispatch's own execution, as rocprofv3's kernel trace does.
+struct ProfScope final : LaunchTimer {
   burnext_moe_layer *L;
-  hipStream_t s;
   int k;
-  hipEvent_t a = nullptr, b = nullptr;
-  ProfScope(burnext_moe_layer *L_, hipStream_t s_, int k_) : L(L_), s(s_), k(k_) {
-    if (!L->profiling) return;
-    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
-      a = b = nullptr;
-      return;
-    }
-    (void)hipEventRecord(a, s);
+  LaunchTimer *prev;
+  bool on;
+  ProfScope(burnext_moe_layer *L_, hipStream_t, int k_)
+      : L(L_), k(k_), prev(g_launch_timer), on(L_->profiling) {
+    if (on) g_launch_timer = this;
   }
-  ~ProfScope() {
-    if (!a) return;
-    (void)hipEventRecord(b, s);
+  ~ProfScope() override {
+    if (on) g_launch_timer = prev;
+  }
+  bool pair(hipEvent_t &a, hipEvent_t &b) override {
+    a = b = nullptr;
+    if (hipEventCreate(&a) != hipSuccess) return false;
+    if (hipEventCreate(&b) != hipSuccess) {
+      (void)hipEventDestroy(a);
+      a = nullptr;
+      return false;
+    }
     std::lock_guard<std::mutex> lk(L->prof_mu);
     L->prof.push_back({a, b, k});
+    return true;
   }
 };
 
@@ -892,6 +920,41 @@ burnext_status burnext_moe_dispatch(burnext_moe_layer_t L, const int32_t *topk_i
   if (st != BURNEXT_OK) return st;
   const WsPtrs p = ws_ptrs(*L, w, workspace);
   st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
+  return st == BURNEXT_OK ? ok() : st;
+}
+
+burnext_status burnext_moe_route_dispatch(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, uint64_t n,
+                                          uint32_t flags, int32_t *topk_idx, float *topk_w, int32_t *seg_offsets,
+                                          int32_t *perm, void *workspace, uint64_t ws_bytes, void *stream) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
+  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  if (n == 0) return ok();
+  if (!x || !topk_idx || !topk_w || !seg_offsets || !perm)
+    return fail(BURNEXT_INVALID_ARG, "null x / topk_idx / topk_w / seg_offsets / perm");
+  hipStream_t s = (hipStream_t)stream;
+  DeviceGuard guard(L->device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  WsLayout w;
+  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
+  if (st != BURNEXT_OK) return st;
+  WsPtrs p = ws_ptrs(*L, w, workspace);
+  // the caller's buffers take the places of the workspace's segment offsets and entry list, so
+  // the kernels write them exactly as in a forward of this batch size
+  int32_t *active = p.active, *num_active = p.num_active;
+  p.seg_off = seg_offsets;
+  p.perm = perm;
+  const bool xb = x_dtype == BURNEXT_BF16, norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, nullptr, s)
+                                  : run_router(L, x, xb, n, norm, p.rms, p.logits, nullptr, s);
+  if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
+    st = run_small_route(L, n, p, p.logits, topk_idx, topk_w, s);
+  } else if (st == BURNEXT_OK) {
+    st = run_topk(L, n, p.logits, topk_idx, topk_w, s);
+    if (st == BURNEXT_OK)
+      st = run_dispatch(L, n, topk_idx, seg_offsets, perm, p.pos_of, active, num_active, p.exrec, p.dcnt, s);
+  }
   return st == BURNEXT_OK ? ok() : st;
 }
 

@@ -12,6 +12,8 @@
  *   burnext_moe_workspace_size (new: the reference allocates per call, src/moe/mod.rs:262,326)
  *   burnext_moe_route          gate Linear + topk_with_indices + softmax  src/moe/mod.rs:110,271-276
  *   burnext_moe_dispatch       per-expert routing masks               src/moe/mod.rs:279-288
+ *   burnext_moe_route_dispatch top-k + softmax + routing masks, as the forward runs them
+ *                                                                     src/moe/mod.rs:271-288
  *   burnext_mxfp4_dequant      dequant_mxfp4_bytes                    src/loader/mxfp4.rs:56-79
  *   burnext_moe_layer_destroy  drop of Arc<MoeQuantLayerResident>     src/moe/mod.rs:56
  *   burnext_last_error         (new: the reference panics, src/moe/mod.rs:111-113)
@@ -102,7 +104,9 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
 
 void burnext_moe_layer_destroy(burnext_moe_layer_t layer);
 
-/* Workspace bytes needed by forward/route/dispatch for up to n_tokens tokens. */
+/* Workspace bytes needed by forward/route/dispatch for any batch of up to n_tokens tokens: the
+ * size is non-decreasing in n_tokens, so one workspace sized for the largest batch serves every
+ * smaller one. */
 burnext_status burnext_moe_workspace_size(burnext_moe_layer_t layer, uint64_t n_tokens, uint64_t *bytes);
 
 /* y[n, D] = flags-selected MoE forward of x[n, D]; x and y share x_dtype and may not alias. */
@@ -123,6 +127,15 @@ burnext_status burnext_moe_route(burnext_moe_layer_t layer, const void *x, burne
 burnext_status burnext_moe_dispatch(burnext_moe_layer_t layer, const int32_t *topk_idx, uint64_t n_tokens,
                                     int32_t *seg_offsets, int32_t *perm, void *workspace, uint64_t ws_bytes,
                                     void *stream);
+
+/* Routing and dispatch exactly as burnext_moe_forward runs them for a batch of n_tokens
+ * (src/moe/mod.rs:110,271-288): for n <= 16 the one-workgroup kernel that fuses top-k, softmax and
+ * the expert-contiguous dispatch; above, the top-k kernel then the dispatch kernels.  Outputs as
+ * burnext_moe_route (topk_idx, topk_w) and burnext_moe_dispatch (seg_offsets[E+1], perm[n*k]). */
+burnext_status burnext_moe_route_dispatch(burnext_moe_layer_t layer, const void *x, burnext_dtype x_dtype,
+                                          uint64_t n_tokens, uint32_t flags, int32_t *topk_idx, float *topk_w,
+                                          int32_t *seg_offsets, int32_t *perm, void *workspace, uint64_t ws_bytes,
+                                          void *stream);
 
 /* Dequantises a [desc.experts * desc.rows, desc.cols] MXFP4 matrix to f32 (exact
  * LUT[code] * 2^(s-127), s = stored - ue8_offset mod 256) or bf16 (same values; e2m1 times a

@@ -147,21 +147,20 @@ void oracle_router(const float *xn, int64_t n, int64_t d, const float *w, const 
 void oracle_route_logits(const float *x, int64_t n, int64_t d, const float *gamma, float eps, int apply_rmsnorm,
                          const float *w, const float *b, int64_t e, float *logits) {
   float *gw = (float *)malloc(sizeof(float) * (size_t)(d > 0 ? d : 1));
+  float *r = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+  /* r_t once per token (the same bits every expert's logit would recompute) */
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < n; ++t) r[t] = apply_rmsnorm ? sqrtf(lane_dot(x + t * d, x + t * d, d) / (float)d + eps) : 1.0f;
   for (int64_t j = 0; j < e; ++j) {
     for (int64_t c = 0; c < d; ++c) gw[c] = (apply_rmsnorm && gamma) ? gamma[c] * w[j * d + c] : w[j * d + c];
+#pragma omp parallel for schedule(static)
     for (int64_t t = 0; t < n; ++t) {
-      const float *xr = x + t * d;
-      const float u = lane_dot(xr, gw, d);
-      float lgt;
-      if (apply_rmsnorm) {
-        const float r = sqrtf(lane_dot(xr, xr, d) / (float)d + eps);
-        lgt = u / r;
-      } else {
-        lgt = u;
-      }
+      const float u = lane_dot(x + t * d, gw, d);
+      const float lgt = apply_rmsnorm ? u / r[t] : u;
       logits[t * e + j] = lgt + (b ? b[j] : 0.0f);
     }
   }
+  free(r);
   free(gw);
 }
 

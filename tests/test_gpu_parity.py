@@ -157,14 +157,39 @@ def test_route_small_ties_nan_signed_zero(M, oracle, E, K, n):
     L.router_b_f32[:] = b
     layer = M.MoeLayer(L)
     x = synth.make_tokens(n, 64, dtype="f32")
-    idx, w, lg = layer.route(M.to_device_x(x, "f32"))
+    # the forward's own routing of a decode-sized batch: one kernel fuses top-k, softmax and the
+    # expert-contiguous dispatch
+    idx, w, seg, perm = layer.route_dispatch(M.to_device_x(x, "f32"))
     torch.cuda.synchronize()
     lg_ref = oracle.route_logits(x, L.router_w_f32, L.router_b_f32, L.gamma_f32, L.rms_eps, True)
     idx_ref, w_ref = oracle.topk_softmax(lg_ref, K)
     assert np.array_equal(idx.cpu().numpy(), idx_ref)
     np.testing.assert_allclose(_np(w), w_ref, rtol=4e-7 * 8, atol=0)
-    seg, perm = layer.dispatch(idx)
     seg_ref, perm_ref, _ = oracle.dispatch(idx_ref, E)
+    assert np.array_equal(seg.cpu().numpy(), seg_ref)
+    assert np.array_equal(perm.cpu().numpy(), perm_ref)
+    layer.close()
+
+
+@pytest.mark.parametrize("D,E,K,n,dtype", [(2880, 32, 4, 8, "bf16"), (2880, 128, 4, 1, "bf16"), (2880, 128, 4, 16, "bf16"),
+                                           (256, 2, 2, 16, "f32"), (200, 7, 3, 13, "f32"), (2880, 32, 4, 64, "bf16"),
+                                           (2880, 128, 4, 1100, "bf16")])
+def test_route_dispatch_as_forward(M, oracle, D, E, K, n, dtype):
+    """Routing + dispatch exactly as the forward runs them (n <= 16: the fused one-workgroup kernel;
+    above: top-k then dispatch): indices, weights, segment offsets and the entry list against the
+    oracle's top-k and counting sort."""
+    from burnext_amd import synth
+    print(f"route+dispatch D={D} E={E} K={K} n={n} {dtype}", flush=True)
+    L = _make(synth, D, 64, E, K, seed=21, dtype=dtype, with_gamma=True)
+    x = synth.make_tokens(n, D, seed=22, dtype=dtype)
+    layer = M.MoeLayer(L)
+    idx, w, seg, perm = layer.route_dispatch(M.to_device_x(x, dtype))
+    torch.cuda.synchronize()
+    lg_ref = oracle.route_logits(x, L.router_w_f32, L.router_b_f32, L.gamma_f32, L.rms_eps, True)
+    idx_ref, w_ref = oracle.topk_softmax(lg_ref, K)
+    seg_ref, perm_ref, _ = oracle.dispatch(idx_ref, E)
+    assert np.array_equal(idx.cpu().numpy(), idx_ref)
+    np.testing.assert_allclose(_np(w), w_ref, rtol=4e-7 * 8, atol=0)
     assert np.array_equal(seg.cpu().numpy(), seg_ref)
     assert np.array_equal(perm.cpu().numpy(), perm_ref)
     layer.close()
@@ -274,6 +299,109 @@ def test_forward_120b_shape_decode(M, oracle):
     assert err <= TOL_BF16
 
 
+def test_forward_120b_t64_all_rows(M, oracle):
+    """Config 4 at T = 64 (D = F = 2880, E = 128, k = 4, bf16, uniform routing): the mid-size GEMV
+    path (router_kernel, top-k kernel, dispatch kernel, strided GEMV shares, one-part combine).
+    Every output row against the oracle, every routing index bit-exact, and the forward's own
+    routing + dispatch against the oracle's."""
+    from burnext_amd import synth
+    L = _make(synth, 2880, 2880, 128, 4, seed=0, dtype="bf16")
+    x = synth.make_tokens(64, 2880, seed=0, dtype="bf16")
+    layer = M.MoeLayer(L)
+    xt = M.to_device_x(x, "bf16")
+    y = _np(layer.forward(xt))
+    idx, _, seg, perm = layer.route_dispatch(xt)
+    torch.cuda.synchronize()
+    y_ref, idx_ref, _ = oracle.moe_forward(L, x)
+    assert np.array_equal(idx.cpu().numpy(), idx_ref)
+    seg_ref, perm_ref, _ = oracle.dispatch(idx_ref, 128)
+    assert np.array_equal(seg.cpu().numpy(), seg_ref) and np.array_equal(perm.cpu().numpy(), perm_ref)
+    err = oracle.max_abs_rel(y, y_ref)
+    moe_err = oracle.max_abs_rel(y - x, y_ref - x)
+    print(f"120b T=64: {len(np.unique(idx_ref))} experts touched, max-abs-rel {err:.3e} (moe part {moe_err:.3e})")
+    assert err <= TOL_BF16 and moe_err <= TOL_BF16
+    layer.close()
+
+
+def test_forward_120b_t8192_gemm_sampled(M, oracle):
+    """Config 4 at T = 8192 (E = 128, uniform routing): the grouped-GEMM path with 128 experts.
+    Routing of all 8192 rows bit-exact; outputs of 40 rows (16 of them from the largest segment)
+    against the oracle."""
+    from burnext_amd import synth
+    T, E = 8192, 128
+    L = _make(synth, 2880, 2880, E, 4, seed=0, dtype="bf16")
+    x = synth.make_tokens(T, 2880, seed=0, dtype="bf16")
+    layer = M.MoeLayer(L)
+    xt = M.to_device_x(x, "bf16")
+    y = _np(layer.forward(xt))
+    idx, _, _ = layer.route(xt)
+    torch.cuda.synchronize()
+    layer.close()
+    lg_ref = oracle.route_logits(x, L.router_w_f32, L.router_b_f32, L.gamma_f32, L.rms_eps, True)
+    idx_all, _ = oracle.topk_softmax(lg_ref, 4)
+    assert np.array_equal(idx.cpu().numpy(), idx_all)
+    counts = np.bincount(idx_all.ravel(), minlength=E)
+    big = np.flatnonzero((idx_all == int(np.argmax(counts))).any(1))
+    rng = np.random.default_rng(1)
+    rows = np.unique(np.concatenate([rng.choice(big, 16, replace=False), rng.choice(T, 24, replace=False)]))
+    y_ref, idx_ref, _ = oracle.moe_forward(L, x[rows])
+    assert np.array_equal(idx_ref, idx_all[rows])
+    err = oracle.max_abs_rel(y[rows], y_ref)
+    moe_err = oracle.max_abs_rel(y[rows] - x[rows], y_ref - x[rows])
+    print(f"120b T=8192: largest segment {counts.max()}, {len(rows)} rows, max-abs-rel {err:.3e} (moe part {moe_err:.3e})")
+    assert np.isfinite(y).all()
+    assert err <= TOL_BF16 and moe_err <= TOL_BF16
+
+
+def _zero_layer(synth, D, F, E, K):
+    """A layer of the given shape with all-zero weights (fast to build; shapes drive the sizes)."""
+    L = synth.make_layer(8, 8, 1, 1, dtype="bf16")
+    bpr1, gpr1, bpr2, gpr2 = (D + 1) // 2, (D + 31) // 32, (F + 1) // 2, (F + 31) // 32
+    L.d_model, L.ffn_hidden, L.num_experts, L.experts_per_token = D, F, E, K
+    L.w1_blocks = np.zeros((E, 2 * F, bpr1), np.uint8)
+    L.w1_scales = np.zeros((E, 2 * F, gpr1), np.uint8)
+    L.w2_blocks = np.zeros((E, D, bpr2), np.uint8)
+    L.w2_scales = np.zeros((E, D, gpr2), np.uint8)
+    L.b1_f32 = np.zeros((E, 2 * F), np.float32)
+    L.b2_f32 = np.zeros((E, D), np.float32)
+    L.router_w_f32 = np.zeros((E, D), np.float32)
+    L.router_b_f32 = np.zeros(E, np.float32)
+    return L
+
+
+@pytest.mark.parametrize("E", [32, 128])
+def test_workspace_size_monotonic(M, E):
+    """burnext_moe_workspace_size(n) never decreases with n (GPT-OSS shapes, n = 1..2048 and a few
+    prefill sizes), and a workspace sized for the largest batch serves a 1-token and a 16-token
+    forward."""
+    from burnext_amd import synth
+    layer = M.MoeLayer(_zero_layer(synth, 2880, 2880, E, 4))
+    sizes = [layer.workspace_size(n) for n in list(range(1, 2049)) + [4096, 8192]]
+    drops = [i for i in range(1, len(sizes)) if sizes[i] < sizes[i - 1]]
+    assert not drops, f"workspace shrinks at n index {drops[:5]}"
+    ws = layer.workspace(2048)
+    for n in (1, 16, 17, 64):
+        x = torch.randn((n, 2880), device="cuda").to(torch.bfloat16)
+        y = layer.forward(x, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y, x)  # zero weights and biases: y = x
+    layer.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_forward_disabled_is_identity(M, dtype):
+    """MoeConfig.disabled (src/moe/mod.rs:106-108): forward returns its input unchanged."""
+    from burnext_amd import synth
+    L = _make(synth, 256, 256, 4, 2, seed=3, dtype=dtype)
+    x = M.to_device_x(synth.make_tokens(9, 256, seed=4, dtype=dtype), dtype)
+    layer = M.MoeLayer(L, disabled=True)
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16) if dtype == "bf16" else y.view(torch.int32),
+                       x.view(torch.int16) if dtype == "bf16" else x.view(torch.int32))
+    layer.close()
+
+
 def test_forward_f32_large_batch_gemv_records(M, oracle):
     """f32 batch above the multi-workgroup dispatch threshold: the expert GEMVs run on the records
     and segment lists that dispatch wrote (some experts hold more tokens than a record lists)."""
@@ -298,10 +426,11 @@ def test_forward_20b_f32_activations(M, oracle):
 
 
 def test_forward_prefill_sampled_rows(M, oracle):
-    """Config 3 shape (T=4096 bf16, Zipf router bias): oracle on a sample of rows (rows are
-    independent), plus routing indices for every row."""
+    """Config 3 shape (T=4096 bf16, Zipf router bias as the benchmark calibrates it): routing
+    indices of every row against the oracle, outputs on a sample of rows (rows are independent)
+    that includes tokens of the largest segment."""
     from burnext_amd import synth
-    bias = synth.zipf_router_bias(32, 1.1, gamma=1.0, seed=0)
+    bias = synth.zipf_router_bias(32, 1.1, gamma=synth.ZIPF_GAMMA_C3, seed=0)
     L = _make(synth, 2880, 2880, 32, 4, seed=0, dtype="bf16", router_bias=bias)
     x = synth.make_tokens(4096, 2880, seed=1, dtype="bf16")
     layer = M.MoeLayer(L)
@@ -309,9 +438,17 @@ def test_forward_prefill_sampled_rows(M, oracle):
     y = _np(layer.forward(xt))
     idx, _, _ = layer.route(xt)
     torch.cuda.synchronize()
-    rows = np.random.default_rng(0).choice(4096, 24, replace=False)
+    # routing of every row against the oracle (logits in the router's order, top-k)
+    lg_ref = oracle.route_logits(x, L.router_w_f32, L.router_b_f32, L.gamma_f32, L.rms_eps, True)
+    idx_all, _ = oracle.topk_softmax(lg_ref, 4)
+    assert np.array_equal(idx.cpu().numpy(), idx_all)
+    # outputs: rows are independent; a sample that includes tokens of the largest segment
+    counts = np.bincount(idx_all.ravel(), minlength=32)
+    big = np.flatnonzero((idx_all == int(np.argmax(counts))).any(1))
+    rng = np.random.default_rng(0)
+    rows = np.unique(np.concatenate([rng.choice(big, 8, replace=False), rng.choice(4096, 24, replace=False)]))
     y_ref, idx_ref, _ = oracle.moe_forward(L, x[rows])
-    assert np.array_equal(idx.cpu().numpy()[rows], idx_ref)
+    assert np.array_equal(idx_ref, idx_all[rows])
     err = oracle.max_abs_rel(y[rows], y_ref)
     print(f"prefill sampled rows: max-abs-rel {err:.3e}")
     assert err <= TOL_BF16
@@ -379,6 +516,8 @@ def test_moe_basic_zero_weights_residual(M):
     (2880, 2880, 128, 4, 1, "bf16"),  # 120B-shaped single token: 4 experts, gate_up in K-parts
     (512, 384, 8, 2, 1, "f32"),       # f32 activations (3 bf16 terms) through the K-parts
     (512, 384, 8, 2, 3, "bf16"),
+    (2880, 2880, 32, 4, 1, "f32"),    # f32 single-token decode: down in 4 K-parts with 3 bf16 terms
+    (640, 640, 8, 2, 1, "bf16"),      # 5 K-groups: the last gate_up / down K-part is empty
 ])
 def test_forward_gate_up_k_split(M, oracle, D, F, E, K, n, dtype):
     """Decode batches touching few experts: gate_up writes K-part pre-activations and a separate

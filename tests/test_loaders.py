@@ -4,6 +4,7 @@ into MoeLayerData.  CPU round trips pin the byte layout; the GPU test runs a lay
 model.bin against the same layer built in memory and against the oracle."""
 from __future__ import annotations
 
+import dataclasses
 import struct
 
 import numpy as np
@@ -53,7 +54,11 @@ def test_modelbin_round_trip(tmp_path, ue8):
         assert b.ue8_offset == 14 and b.experts_per_token == K and b.gate_up_layout == "interleaved"
         assert b.swiglu_limit == 7.0 and abs(b.rms_eps - 1e-5) < 1e-12
         _same_layer(a, b, scale_shift=14 - ue8)  # stored = true + 14 (the exporter's wrapping add)
-    assert loaders.load_modelbin_moe(path)[0].gate_up_layout == "halves"  # the reference kernel's pairing
+    # default: the checkpoints' interleaved rows; the reference kernel's halves pairing is opt-in
+    assert loaders.load_modelbin_moe(path)[0].gate_up_layout == "interleaved"
+    assert loaders.load_modelbin_moe(path, gate_up_layout="halves")[0].gate_up_layout == "halves"
+    with pytest.raises(ValueError):
+        loaders.load_modelbin_moe(path, gate_up_layout="split")
 
 
 def test_modelbin_layout_alignment(tmp_path):
@@ -137,16 +142,24 @@ def test_safetensors_missing_tensor(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["modelbin", "safetensors"])
+@pytest.mark.parametrize("fmt", ["modelbin", "modelbin_halves", "safetensors"])
 def test_loaded_layer_forward_matches(tmp_path, oracle, fmt):
     """A layer read back from disk gives the same outputs, bit for bit, as the in-memory layer it
-    was written from, and agrees with the oracle."""
+    was written from (read with the same gate_up row pairing), and agrees with the oracle.  A
+    model.bin loads with the checkpoints' interleaved pairing by default; "halves" is the opt-in
+    pairing of the reference kernel."""
     from burnext_amd import moe
     src = _layers(1)[0]
     if fmt == "modelbin":
         path = tmp_path / "model.bin"
         loaders.write_modelbin(path, _header(1), [src])
-        got = loaders.load_modelbin_moe(path, gate_up_layout="interleaved")[0]
+        got = loaders.load_modelbin_moe(path)[0]
+        assert got.gate_up_layout == "interleaved"
+    elif fmt == "modelbin_halves":
+        path = tmp_path / "model.bin"
+        loaders.write_modelbin(path, _header(1), [src])
+        got = loaders.load_modelbin_moe(path, gate_up_layout="halves")[0]
+        src = dataclasses.replace(src, gate_up_layout="halves")
     else:
         path = tmp_path / "model.safetensors"
         loaders.write_safetensors(path, _checkpoint(src, 0))

@@ -414,3 +414,19 @@ def test_golden_decode_routing_fixture(oracle):
     assert np.array_equal(lg.view(np.uint32), g["logits"].view(np.uint32))
     idx, w = oracle.topk_softmax(lg, 4)
     assert np.array_equal(idx, g["topk_idx"]) and np.array_equal(w, g["topk_w"])
+
+
+def test_zipf_gamma_calibration():
+    """The C3 router-bias gamma the benchmark uses is the calibration's result on the benchmark's
+    own layer and tokens (float64 routing), and the realised popularity falls with the Zipf rank."""
+    from burnext_amd import synth
+    L = synth.make_layer(2880, 64, 32, 4, seed=0, dtype="bf16")
+    x = synth.make_tokens(4096, 2880, seed=0, dtype="bf16")
+    g, counts = synth.calibrate_zipf_gamma(L, x)
+    assert g == synth.ZIPF_GAMMA_C3
+    assert counts.sum() == 4096 * 4
+    ideal = synth.zipf_ideal_counts(32, 1.1, 4096, 4)
+    assert abs(ideal[-1] - 102.4) < 1 and ideal[0] == 4096
+    # head and tail within a factor 1.6 of the (capped) ideal; monotone on the whole over ranks
+    assert 0.6 < counts[0] / ideal[0] and 0.6 < counts[-1] / ideal[-1] < 1.6
+    assert np.corrcoef(np.log(counts), np.log(ideal))[0, 1] > 0.98
