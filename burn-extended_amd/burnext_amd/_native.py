@@ -32,7 +32,7 @@ KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine", "swi
 
 # Every symbol include/burnext_moe.h declares.
 EXPORTS = ["burnext_moe_layer_create", "burnext_moe_layer_destroy", "burnext_moe_workspace_size",
-           "burnext_moe_forward", "burnext_moe_route", "burnext_moe_dispatch", "burnext_moe_route_dispatch",
+           "burnext_moe_forward", "burnext_moe_forward_noalloc", "burnext_moe_route", "burnext_moe_dispatch", "burnext_moe_route_dispatch",
            "burnext_mxfp4_dequant",
            "burnext_moe_profile_enable", "burnext_moe_profile_read", "burnext_last_error"]
 
@@ -84,6 +84,8 @@ def lib() -> ctypes.CDLL:
         L.burnext_moe_workspace_size.argtypes = [_vp, _u64, ctypes.POINTER(_u64)]
         L.burnext_moe_forward.restype = ctypes.c_int
         L.burnext_moe_forward.argtypes = [_vp, _vp, ctypes.c_int, _vp, _u64, ctypes.c_uint32, _vp, _u64, _vp]
+        L.burnext_moe_forward_noalloc.restype = ctypes.c_int
+        L.burnext_moe_forward_noalloc.argtypes = [_vp, _vp, ctypes.c_int, _vp, _u64, ctypes.c_uint32, _vp]
         L.burnext_moe_route.restype = ctypes.c_int
         L.burnext_moe_route.argtypes = [_vp, _vp, ctypes.c_int, _u64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _u64, _vp]
         L.burnext_moe_dispatch.restype = ctypes.c_int

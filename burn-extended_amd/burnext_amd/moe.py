@@ -144,6 +144,16 @@ class MoeLayer:
                                             ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
         return y
 
+    def forward_noalloc(self, x: torch.Tensor, out: torch.Tensor, flags: int = N.FORWARD_DEFAULT,
+                        stream=None) -> torch.Tensor:
+        """burnext_moe_forward_noalloc: the forward on the library's fixed per-GPU scratch (no
+        workspace, nothing allocated here or in the library; `out` is the caller's)."""
+        assert x.is_cuda and x.is_contiguous() and x.shape[-1] == self.data.d_model
+        n = x.numel() // self.data.d_model
+        N.check(N.lib().burnext_moe_forward_noalloc(self.handle, ctypes.c_void_p(x.data_ptr()), _x_dtype(x),
+                                                    ctypes.c_void_p(out.data_ptr()), n, flags, _stream(stream)))
+        return out
+
     def route(self, x: torch.Tensor, flags: int = N.APPLY_RMSNORM, stream=None):
         n = x.numel() // self.data.d_model
         idx = torch.empty((n, self.k), dtype=torch.int32, device=x.device)

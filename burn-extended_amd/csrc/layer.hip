@@ -395,6 +395,9 @@ uint32_t router_tb(const burnext_moe_layer &L, uint64_t n, uint32_t epw) {
   return tb;
 }
 
+// Set while burnext_moe_forward_noalloc runs: its launches are never timed (timing creates events).
+thread_local bool g_untimed = false;
+
 // While profiling is on, binds a HIP event pair to every kernel dispatch launched in its scope
 // (hipExtLaunchKernel through the thread's LaunchTimer), recorded under kernel id k: the pair
 // measures each dispatch's own execution, as rocprofv3's kernel trace does.
@@ -404,7 +407,7 @@ struct ProfScope final : LaunchTimer {
   LaunchTimer *prev;
   bool on;
   ProfScope(burnext_moe_layer *L_, hipStream_t, int k_)
-      : L(L_), k(k_), prev(g_launch_timer), on(L_->profiling) {
+      : L(L_), k(k_), prev(g_launch_timer), on(L_->profiling && !g_untimed) {
     if (on) g_launch_timer = this;
   }
   ~ProfScope() override {
@@ -632,6 +635,37 @@ burnext_status check_ws(burnext_moe_layer *L, uint64_t n, void *ws, uint64_t ws_
 
 constexpr uint64_t kMaxTokens = 1ull << 22;
 
+// Scratch of burnext_moe_forward_noalloc: one fixed device array per GPU (it lives in this file's
+// code object, so every device the library runs on holds its own copy until the process ends).
+// Host code never passes `scratch` itself to a kernel -- on the host that name is only a stand-in
+// for the symbol -- but the device address hipGetSymbolAddress returns for the current device.
+constexpr uint64_t kScratchBytes = 16ull << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (which must be current), looked up once per device.
+burnext_status scratch_address(int device, void **out);
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+burnext_status scratch_address(int device, void **out) {
+  if (device < 0 || device >= kMaxDevices) return fail(BURNEXT_UNSUPPORTED, "device index above 63");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(BURNEXT_DEVICE_ERROR, std::string("hipGetSymbolAddress of the scratch array failed: ") +
+                                            hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return BURNEXT_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -742,6 +776,10 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
       L->router_wg = dgw;
       L->router_wg_bf16 = false;
     }
+  }
+  if (st == BURNEXT_OK) {
+    void *sp = nullptr;
+    st = scratch_address(device, &sp);
   }
   if (st == BURNEXT_OK) {
     int cus = 0;
@@ -878,6 +916,34 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
   if (st != BURNEXT_OK) return st;
 
   return combine(L, x, y, xb, n, flags, p, s, ksplit);
+}
+
+burnext_status burnext_moe_forward_noalloc(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, void *y,
+                                           uint64_t n, uint32_t flags, void *stream) {
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  const uint64_t need = ws_layout(*L, n).total;
+  if (need > kScratchBytes) {
+    char buf[200];
+    snprintf(buf, sizeof(buf),
+             "burnext_moe_forward_noalloc: %llu tokens need %llu bytes of scratch; its fixed scratch holds %llu "
+             "(use burnext_moe_forward with a workspace)",
+             (unsigned long long)n, (unsigned long long)need, (unsigned long long)kScratchBytes);
+    return fail(BURNEXT_UNSUPPORTED, buf);
+  }
+  void *ws = nullptr;
+  {
+    DeviceGuard guard(L->device);
+    if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+    const burnext_status st = scratch_address(L->device, &ws);
+    if (st != BURNEXT_OK) return st;
+  }
+  struct Untimed {
+    bool prev = g_untimed;
+    Untimed() { g_untimed = true; }
+    ~Untimed() { g_untimed = prev; }
+  } untimed;
+  return burnext_moe_forward(L, x, x_dtype, y, n, flags, ws, kScratchBytes, stream);
 }
 
 burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, uint64_t n,

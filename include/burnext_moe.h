@@ -10,6 +10,7 @@
  *   burnext_moe_forward        MoeGatedSwiGLU::forward                src/moe/mod.rs:99-115
  *                              (forward_resident                      src/moe/mod.rs:122-412)
  *   burnext_moe_workspace_size (new: the reference allocates per call, src/moe/mod.rs:262,326)
+ *   burnext_moe_forward_noalloc (no counterpart: the forward for callers that cannot allocate)
  *   burnext_moe_route          gate Linear + topk_with_indices + softmax  src/moe/mod.rs:110,271-276
  *   burnext_moe_dispatch       per-expert routing masks               src/moe/mod.rs:279-288
  *   burnext_moe_route_dispatch top-k + softmax + routing masks, as the forward runs them
@@ -113,6 +114,17 @@ burnext_status burnext_moe_workspace_size(burnext_moe_layer_t layer, uint64_t n_
 burnext_status burnext_moe_forward(burnext_moe_layer_t layer, const void *x, burnext_dtype x_dtype, void *y,
                                    uint64_t n_tokens, uint32_t flags, void *workspace, uint64_t ws_bytes,
                                    void *stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): burnext_moe_forward
+ * with the library's own fixed scratch in place of a caller workspace.  The scratch is one 16 MiB
+ * device array per GPU, held from the first layer created on that GPU until the process ends;
+ * a batch whose burnext_moe_workspace_size exceeds 16 MiB (above about 120 tokens at the GPT-OSS
+ * shapes) returns BURNEXT_UNSUPPORTED.  The call allocates nothing (no hipMalloc, no events: the
+ * profiling hook does not time it).  Every call on one GPU shares that GPU's scratch, which keeps
+ * the last call's contents: calls that overlap on one GPU (other streams or threads) race. */
+burnext_status burnext_moe_forward_noalloc(burnext_moe_layer_t layer, const void *x, burnext_dtype x_dtype, void *y,
+                                           uint64_t n_tokens, uint32_t flags, void *stream);
 
 /* Routing only: topk_idx[n, k] (int32, descending logit, ties to the lower expert index),
  * topk_w[n, k] (softmax over the selected logits); logits[n, E] optional (nullable).
