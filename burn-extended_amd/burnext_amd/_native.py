@@ -1,4 +1,4 @@
-"""ctypes binding of libburnext_moe.so (include/burnext_moe.h).
+"""ctypes binding of libburnext_moe.so (include/burnext_moe.h, include/burnext_gptoss.h).
 
 The library is the product; this module only marshals arguments.  It fails loudly when the
 library has not been built -- there is no fallback path.
@@ -34,7 +34,10 @@ KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine", "swi
 EXPORTS = ["burnext_moe_layer_create", "burnext_moe_layer_destroy", "burnext_moe_workspace_size",
            "burnext_moe_forward", "burnext_moe_forward_noalloc", "burnext_moe_route", "burnext_moe_dispatch", "burnext_moe_route_dispatch",
            "burnext_mxfp4_dequant",
-           "burnext_moe_profile_enable", "burnext_moe_profile_read", "burnext_last_error"]
+           "burnext_moe_profile_enable", "burnext_moe_profile_read", "burnext_last_error",
+           # include/burnext_gptoss.h
+           "burnext_gptoss_create", "burnext_gptoss_destroy", "burnext_gptoss_workspace_size", "burnext_gptoss_reset",
+           "burnext_gptoss_cache_load", "burnext_gptoss_decode"]
 
 
 class MxFp4Desc(ctypes.Structure):
@@ -52,6 +55,21 @@ class MoeConfigC(ctypes.Structure):
     _fields_ = [("d_model", ctypes.c_uint32), ("ffn_hidden", ctypes.c_uint32), ("num_experts", ctypes.c_uint32),
                 ("experts_per_token", ctypes.c_uint32), ("swiglu_alpha", ctypes.c_float),
                 ("swiglu_limit", ctypes.c_float), ("rms_eps", ctypes.c_float), ("disabled", ctypes.c_int32)]
+
+
+class GptOssConfigC(ctypes.Structure):
+    """Mirror of burnext_gptoss_config."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("vocab_size", "d_model", "n_layers", "n_heads", "kv_heads", "head_dim",
+                                               "max_batch", "cache_len", "window_policy", "window", "full_on_even",
+                                               "rope_head_stride", "max_positions", "kv_bf16")] + \
+               [(n, ctypes.c_float) for n in ("rms_eps", "rope_theta", "rope_scaling_factor", "rope_initial_context",
+                                              "rope_ntk_alpha", "rope_ntk_beta", "scale_dk")]
+
+
+class GptOssWeightsC(ctypes.Structure):
+    """Mirror of burnext_gptoss_weights (host bf16 bit patterns)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("tok_emb", "norm_attn", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                                               "sinks", "norm_final", "lm_head")]
 
 
 class BurnextError(RuntimeError):
@@ -100,6 +118,20 @@ def lib() -> ctypes.CDLL:
         L.burnext_moe_profile_read.restype = ctypes.c_int
         L.burnext_moe_profile_read.argtypes = [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64),
                                                ctypes.c_int]
+        L.burnext_gptoss_create.restype = ctypes.c_int
+        L.burnext_gptoss_create.argtypes = [ctypes.POINTER(GptOssConfigC), ctypes.POINTER(GptOssWeightsC), _vp,
+                                            ctypes.c_int, ctypes.POINTER(_vp)]
+        L.burnext_gptoss_destroy.restype = None
+        L.burnext_gptoss_destroy.argtypes = [_vp]
+        L.burnext_gptoss_workspace_size.restype = ctypes.c_int
+        L.burnext_gptoss_workspace_size.argtypes = [_vp, ctypes.c_uint32, ctypes.POINTER(_u64)]
+        L.burnext_gptoss_reset.restype = ctypes.c_int
+        L.burnext_gptoss_reset.argtypes = [_vp]
+        L.burnext_gptoss_cache_load.restype = ctypes.c_int
+        L.burnext_gptoss_cache_load.argtypes = [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _vp]
+        L.burnext_gptoss_decode.restype = ctypes.c_int
+        L.burnext_gptoss_decode.argtypes = [_vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _vp,
+                                            _vp, _u64, _vp]
         _lib = L
     return _lib
 

@@ -1,0 +1,1042 @@
+// decoder.hip -- GPT-OSS decoder decode step on gfx950 around the MoE layer (include/burnext_gptoss.h).
+//
+// Per decode step (batch rows b < B, one token each, absolute position pos):
+//   embed_kernel        hidden[b] = tok_emb[token[b]]                       (f32 residual stream)
+//   per layer l:
+//     rmsnorm_kernel    xn = RmsNorm(hidden) with norm_attn[l]
+//     dense_gemv_kernel the fused q|k|v projection as K-part partial sums (bf16 weights on
+//                       v_mfma_f32_16x16x32_bf16, activations as two bf16 terms)
+//     qkv_post_kernel   sum of parts + bias, RoPE on q and k (YaRN table), k and v written into the
+//                       rolling cache at slot pos mod cache_len
+//     attn_chunk_kernel one query row per head against 256 cached keys per workgroup: chunk
+//                       maximum, exp, sums and the weighted value sum (flash-decoding split)
+//     attn_combine_kernel  chunks merged with the learned sink in the softmax denominator
+//     dense_gemv_kernel the output projection; o_post_kernel hidden += sum + bias
+//     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels
+//   rmsnorm_kernel (norm_final), dense_gemv_kernel (LM head), logits_kernel + argmax_kernel
+//
+// Replaces src/models/gpt_oss.rs:101-113,226-252 and src/attention/streaming_mqa.rs:239-419
+// (Burn tensor ops on WGPU).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/burnext_gptoss.h"
+#include "kernels.hpp"
+#include "mx_device.hpp"
+
+struct burnext_moe_layer;
+
+namespace burnext {
+burnext_status set_error(burnext_status st, const std::string &msg);
+void moe_layer_shape(const burnext_moe_layer *L, uint32_t *d_model, int *device);
+}  // namespace burnext
+
+using namespace burnext;
+
+namespace {
+
+constexpr uint32_t kDenseMaxH = 16;   // K-groups (32 inputs each) per GEMV work unit
+constexpr uint32_t kAttnChunk = 256;  // cached keys per attention workgroup
+constexpr uint32_t kMaxGroups = 16;   // query heads per kv head
+constexpr uint32_t kMaxHeadDim = 128;
+constexpr uint32_t kMaxBatch = 16;
+constexpr uint32_t kLogitsPerBlock = 1024;
+constexpr int32_t kNoIndex = 0x7fffffff;
+
+// ---------------------------------------------------------------------------------------------
+// Cache rows: f32 (the reference's element) or bf16.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void kv_store2(float *p, float a, float b) { *(float2 *)p = make_float2(a, b); }
+__device__ __forceinline__ void kv_store2(uint16_t *p, float a, float b) {
+  *(uint32_t *)p = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+__device__ __forceinline__ void kv_store1(float *p, float a) { *p = a; }
+__device__ __forceinline__ void kv_store1(uint16_t *p, float a) { *p = f32_to_bf16_bits(a); }
+__device__ __forceinline__ void kv_load4(const float *p, float (&v)[4]) {
+  const float4 x = *(const float4 *)p;
+  v[0] = x.x;
+  v[1] = x.y;
+  v[2] = x.z;
+  v[3] = x.w;
+}
+__device__ __forceinline__ void kv_load4(const uint16_t *p, float (&v)[4]) {
+  const uint2 r = *(const uint2 *)p;
+  v[0] = bf16_bits_to_f32((uint16_t)r.x);
+  v[1] = bf16_bits_to_f32((uint16_t)(r.x >> 16));
+  v[2] = bf16_bits_to_f32((uint16_t)r.y);
+  v[3] = bf16_bits_to_f32((uint16_t)(r.y >> 16));
+}
+template <typename KV>
+__device__ __forceinline__ void kv_load8(const KV *p, float (&v)[8]) {
+  float a[4], b[4];
+  kv_load4(p, a);
+  kv_load4(p + 4, b);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    v[u] = a[u];
+    v[4 + u] = b[u];
+  }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dense decode GEMV.  Weights W [N, K] bf16, repacked at create into tiles of 16 rows x 32
+// inputs (1 KiB): tile t, K-group kg at (t * nkg + kg) KiB, lane l = 16 q + i holding
+// W[16 t + i][32 kg + 8 q .. +8] -- the A operand of v_mfma_f32_16x16x32_bf16 for one K step.
+// Workgroup (x, h): 4 waves, row tiles 4 x .. 4 x + 3, K-groups [h H, (h + 1) H).  The K range of
+// the activations is staged once per workgroup in LDS as two bf16 terms (hi, lo = bf16 of the
+// residual; together f32-accurate to ~2^-17), token rows >= B zero.  Every wave issues all H
+// weight loads of its tile first (16 KiB in flight at H = 16), then 2 MFMAs per K-group.
+// Output: partial sums out[h][b][n] (no bias).
+// ---------------------------------------------------------------------------------------------
+struct DenseArgs {
+  const uint8_t *w;
+  const float *x;  // [B, K]
+  float *out;      // [parts][B][N]
+  uint32_t N, K, nkg, ntiles, B, H;
+  uint64_t part_stride;
+};
+
+__global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t H = a.H, ldk = H * 32u + 8u;  // +8: consecutive token rows start on other banks
+  uint16_t *bs = (uint16_t *)smem;             // [2 terms][16 tokens][ldk]
+  const uint32_t h = blockIdx.y, kg0 = h * H, kg1 = min(kg0 + H, a.nkg), nk = kg1 - kg0;
+  const uint32_t k0 = kg0 * 32u, kn = nk * 32u;
+  for (uint32_t i = threadIdx.x; i < 16u * kn; i += blockDim.x) {
+    const uint32_t j = i / kn, kk = i - j * kn, k = k0 + kk;
+    const float v = (j < a.B && k < a.K) ? a.x[(size_t)j * a.K + k] : 0.0f;
+    uint16_t t[2];
+    split_bf16<2>(v, t);
+    bs[(size_t)j * ldk + kk] = t[0];
+    bs[(size_t)(16u + j) * ldk + kk] = t[1];
+  }
+  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+  const uint32_t tile = blockIdx.x * 4u + wv;
+  const bool tv = tile < a.ntiles;  // wave-uniform
+  const uint32_t tl = tv ? tile : a.ntiles - 1u;
+  uint4 wbuf[kDenseMaxH];
+  const uint8_t *wt = a.w + ((size_t)tl * a.nkg + kg0) * 1024u + lane * 16u;
+#pragma unroll
+  for (uint32_t s = 0; s < kDenseMaxH; ++s)
+    if (s < nk) wbuf[s] = *(const uint4 *)(wt + (size_t)s * 1024u);
+  __syncthreads();
+  const uint32_t i16 = lane & 15u, q = lane >> 4;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (uint32_t s = 0; s < kDenseMaxH; ++s) {
+    if (s < nk) {
+      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, wbuf[s]);
+#pragma unroll
+      for (uint32_t term = 0; term < 2u; ++term) {
+        const u32x4_t raw = *(const u32x4_t *)(bs + (size_t)(term * 16u + i16) * ldk + 32u * s + 8u * q);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8_t, raw), acc, 0, 0, 0);
+      }
+    }
+  }
+  if (!tv || i16 >= a.B) return;
+  float *o = a.out + (size_t)h * a.part_stride + (size_t)i16 * a.N;
+  const uint32_t r0 = tile * 16u + 4u * q;
+#pragma unroll
+  for (uint32_t r = 0; r < 4u; ++r)
+    if (r0 + r < a.N) o[r0 + r] = acc[r];
+}
+
+// ---------------------------------------------------------------------------------------------
+// q|k|v post-processing: one thread per pair (2 i, 2 i + 1) of one head of one batch row.
+// Sum of the K-part partials plus bias; RoPE for q and k: pair i of head hh at position
+// pos + hh * head_stride rotated by table[p][i] = (cos, sin) x concentration:
+//   y0 = x0 c - x1 s, y1 = x1 c + x0 s   (Burn RotaryEncoding, interleaved pairs)
+// q goes to qbuf [B][nH dk] (f32); k and v to the cache [maxB][kvH][cap][dk] at slot.
+// ---------------------------------------------------------------------------------------------
+struct QkvPostArgs {
+  const float *part;  // [parts][B][qd + 2 kd]
+  uint64_t part_stride;
+  uint32_t parts;
+  const float *bias;  // [qd + 2 kd]
+  const float *rope;  // [npos][dk / 2][2]
+  float *qbuf;        // [B][nH * dk]
+  void *kc, *vc;      // this layer's cache
+  uint32_t B, nH, kvH, dk, cap, slot, pos, head_stride;
+};
+
+template <typename KV>
+__global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
+  const uint32_t b = blockIdx.y, qd = a.nH * a.dk, kd = a.kvH * a.dk, N = qd + 2u * kd;
+  const uint32_t pr = blockIdx.x * blockDim.x + threadIdx.x;
+  if (pr >= N / 2u) return;
+  const uint32_t o = 2u * pr;
+  float s0 = 0.0f, s1 = 0.0f;
+  for (uint32_t h = 0; h < a.parts; ++h) {
+    const float2 p = *(const float2 *)(a.part + (size_t)h * a.part_stride + (size_t)b * N + o);
+    s0 = s0 + p.x;
+    s1 = s1 + p.y;
+  }
+  const float x0 = s0 + a.bias[o], x1 = s1 + a.bias[o + 1u];
+  const uint32_t half = a.dk / 2u;
+  KV *kc = (KV *)a.kc, *vc = (KV *)a.vc;
+  if (o < qd + kd) {  // q or k: rotate
+    const uint32_t local = o < qd ? o : o - qd, hh = local / a.dk, i = (local - hh * a.dk) / 2u;
+    const uint32_t p = a.pos + hh * a.head_stride;
+    const float2 cs = *(const float2 *)(a.rope + ((size_t)p * half + i) * 2u);
+    const float y0 = x0 * cs.x - x1 * cs.y, y1 = x1 * cs.x + x0 * cs.y;
+    if (o < qd) {
+      *(float2 *)(a.qbuf + (size_t)b * qd + local) = make_float2(y0, y1);
+    } else {
+      kv_store2(kc + (((size_t)b * a.kvH + hh) * a.cap + a.slot) * a.dk + (local - hh * a.dk), y0, y1);
+    }
+  } else {
+    const uint32_t local = o - qd - kd, hh = local / a.dk;
+    kv_store2(vc + (((size_t)b * a.kvH + hh) * a.cap + a.slot) * a.dk + (local - hh * a.dk), x0, x1);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Attention, flash-decoding split.  Workgroup (chunk c, kv head g, batch b) covers positions
+// p = p_lo + 256 c + t (t < 256, p <= p_hi) of the active window [p_lo, p_hi], slot p mod cap,
+// for the `groups` query heads of kv head g.
+//   scores: thread t, s[j] = (q[j] . k[p]) / sqrt(scale_dk) (q broadcast from LDS)
+//   m[j] = chunk maximum, e = exp(s - m) (0 outside the window), l[j] = sum of e
+//   acc[j][d] = sum of e v: thread (key lane kq = t / 16, dim quad dq = t % 16) takes keys
+//     kq, kq + 16, ... in order, the 4 key lanes of a wave are summed by shuffles and the 4 waves
+//     in order through LDS
+// Output: part[b][g][c][j] = {m, l, acc[dk]}.
+// ---------------------------------------------------------------------------------------------
+struct AttnArgs {
+  const float *q;        // [B][nH * dk]
+  const void *kc, *vc;   // this layer's cache
+  float *part;           // [B][kvH][nchunk][groups][dk + 2]
+  uint32_t nH, kvH, dk, cap, p_lo, p_hi, nchunk;
+  float inv_scale;       // 1 / sqrt(scale_dk)
+};
+
+template <typename KV, uint32_t G>
+__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
+  __shared__ __align__(16) float q_l[kMaxGroups * kMaxHeadDim];   // 8 KiB
+  __shared__ float e_l[kAttnChunk * kMaxGroups];                  // 16 KiB: e[key][j]
+  __shared__ float m_l[4 * kMaxGroups];
+  __shared__ __align__(16) float acc_l[4 * kMaxGroups * 16 * 4];  // [wave][j][dq][4]: 16 KiB
+  const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  constexpr uint32_t groups = G;
+  const uint32_t dk = a.dk, t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  const KV *kc = (const KV *)a.kc, *vc = (const KV *)a.vc;
+  for (uint32_t i = t; i < groups * dk; i += blockDim.x)
+    q_l[i] = a.q[(size_t)b * a.nH * dk + (size_t)g * groups * dk + i];
+  __syncthreads();
+  const size_t head_base = ((size_t)b * a.kvH + g) * a.cap;
+  const uint32_t p0 = a.p_lo + c * kAttnChunk, p = p0 + t;
+  const bool valid = p <= a.p_hi;
+  float s[G];
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) s[j] = 0.0f;
+  if (valid) {
+    const KV *kr = kc + (head_base + p % a.cap) * dk;
+    for (uint32_t d0 = 0; d0 < dk; d0 += 8u) {
+      float kv[8];
+      kv_load8(kr + d0, kv);
+#pragma unroll
+      for (uint32_t j = 0; j < G; ++j) {
+        const float4 qa = *(const float4 *)(q_l + j * dk + d0), qb = *(const float4 *)(q_l + j * dk + d0 + 4u);
+        s[j] = fmaf(qa.x, kv[0], s[j]);
+        s[j] = fmaf(qa.y, kv[1], s[j]);
+        s[j] = fmaf(qa.z, kv[2], s[j]);
+        s[j] = fmaf(qa.w, kv[3], s[j]);
+        s[j] = fmaf(qb.x, kv[4], s[j]);
+        s[j] = fmaf(qb.y, kv[5], s[j]);
+        s[j] = fmaf(qb.z, kv[6], s[j]);
+        s[j] = fmaf(qb.w, kv[7], s[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+    s[j] = valid ? s[j] * a.inv_scale : -INFINITY;
+    const float mw = wave_max(s[j]);
+    if (lane == 0) m_l[w * kMaxGroups + j] = mw;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+    const float m = fmaxf(fmaxf(m_l[j], m_l[kMaxGroups + j]), fmaxf(m_l[2u * kMaxGroups + j], m_l[3u * kMaxGroups + j]));
+    e_l[t * groups + j] = valid ? expf(s[j] - m) : 0.0f;
+  }
+  __syncthreads();
+  const uint32_t kq = t >> 4, dq = t & 15u, nq = dk / 4u;
+  const uint32_t nkeys = min(kAttnChunk, a.p_hi + 1u - p0);
+  float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)groups * (dk + 2u);
+  for (uint32_t dbase = 0; dbase < nq; dbase += 16u) {
+    const uint32_t dqq = dbase + dq;
+    float acc[G][4];
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+    if (dqq < nq) {
+      for (uint32_t key = kq; key < nkeys; key += 16u) {
+        float v[4];
+        kv_load4(vc + (head_base + (p0 + key) % a.cap) * dk + 4u * dqq, v);
+#pragma unroll
+        for (uint32_t j = 0; j < G; ++j) {
+          const float e = e_l[key * groups + j];
+          acc[j][0] = fmaf(e, v[0], acc[j][0]);
+          acc[j][1] = fmaf(e, v[1], acc[j][1]);
+          acc[j][2] = fmaf(e, v[2], acc[j][2]);
+          acc[j][3] = fmaf(e, v[3], acc[j][3]);
+        }
+      }
+    }
+    // the 4 key lanes of a wave (lane bits 4 and 5)
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 16, 64);
+        acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 32, 64);
+      }
+    }
+    if (dbase != 0) __syncthreads();  // the previous pass has read acc_l
+    if (lane < 16u) {
+#pragma unroll
+      for (uint32_t j = 0; j < G; ++j) {
+        *(float4 *)(acc_l + ((w * kMaxGroups + j) * 16u + dq) * 4u) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+      }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < groups * 16u; i += blockDim.x) {
+      const uint32_t j = i >> 4, dd = i & 15u;
+      if (dbase + dd >= nq) continue;
+      float4 r = *(const float4 *)(acc_l + (j * 16u + dd) * 4u);
+#pragma unroll
+      for (uint32_t w2 = 1; w2 < 4u; ++w2) {
+        const float4 v = *(const float4 *)(acc_l + ((w2 * kMaxGroups + j) * 16u + dd) * 4u);
+        r = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+      }
+      float *dst = out + (size_t)j * (dk + 2u) + 2u + 4u * (dbase + dd);
+      dst[0] = r.x;
+      dst[1] = r.y;
+      dst[2] = r.z;
+      dst[3] = r.w;
+    }
+  }
+  if (t < groups) {
+    float l = 0.0f;
+    for (uint32_t key = 0; key < nkeys; ++key) l = l + e_l[key * groups + t];
+    out[(size_t)t * (dk + 2u)] =
+        fmaxf(fmaxf(m_l[t], m_l[kMaxGroups + t]), fmaxf(m_l[2u * kMaxGroups + t], m_l[3u * kMaxGroups + t]));
+    out[(size_t)t * (dk + 2u) + 1u] = l;
+  }
+}
+
+// Chunks merged per (head, dim) with the sink (src/attention/core.rs:34-55): M = max(sink, max_c
+// m_c), L = exp(sink - M) + sum_c l_c exp(m_c - M), ctx = sum_c acc_c exp(m_c - M) / L.
+struct CombineAttnArgs {
+  const float *part;   // [B][kvH][nchunk][groups][dk + 2]
+  const float *sinks;  // [nH] or null
+  float *ctx;          // [B][nH * dk]
+  uint32_t nH, kvH, dk, nchunk;
+};
+
+__global__ __launch_bounds__(256) void attn_combine_kernel(CombineAttnArgs a) {
+  const uint32_t g = blockIdx.x, b = blockIdx.y, groups = a.nH / a.kvH, dk = a.dk;
+  const float *base = a.part + ((size_t)b * a.kvH + g) * a.nchunk * (size_t)groups * (dk + 2u);
+  for (uint32_t i = threadIdx.x; i < groups * dk; i += blockDim.x) {
+    const uint32_t j = i / dk, d = i - j * dk, h = g * groups + j;
+    const float sink = a.sinks ? a.sinks[h] : -INFINITY;
+    float M = sink;
+    for (uint32_t c = 0; c < a.nchunk; ++c) M = fmaxf(M, base[((size_t)c * groups + j) * (dk + 2u)]);
+    float L = a.sinks ? expf(sink - M) : 0.0f, acc = 0.0f;
+    for (uint32_t c = 0; c < a.nchunk; ++c) {
+      const float *pc = base + ((size_t)c * groups + j) * (dk + 2u);
+      const float f = expf(pc[0] - M);
+      L = L + pc[1] * f;
+      acc = acc + pc[2u + d] * f;
+    }
+    a.ctx[(size_t)b * a.nH * dk + (size_t)h * dk + d] = acc / L;
+  }
+}
+
+// hidden[b][n] += sum of the K-part partials + bias (the attention residual).
+struct OPostArgs {
+  const float *part;
+  uint64_t part_stride;
+  uint32_t parts, N;
+  const float *bias;
+  float *hidden;
+};
+__global__ __launch_bounds__(256) void o_post_kernel(OPostArgs a) {
+  const uint32_t b = blockIdx.y, n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= a.N) return;
+  float s = 0.0f;
+  for (uint32_t h = 0; h < a.parts; ++h) s = s + a.part[(size_t)h * a.part_stride + (size_t)b * a.N + n];
+  a.hidden[(size_t)b * a.N + n] = a.hidden[(size_t)b * a.N + n] + (s + a.bias[n]);
+}
+
+// y[b] = x[b] / sqrt(mean(x[b]^2) + eps) * gamma (Burn RmsNorm); one workgroup per row.
+struct NormArgs {
+  const float *x;
+  const float *gamma;
+  float *y;
+  uint32_t D;
+  float eps;
+};
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
+  __shared__ float red[4];
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  const float *x = a.x + (size_t)b * a.D;
+  float ss = 0.0f;
+  for (uint32_t c = t; c < a.D; c += blockDim.x) ss = fmaf(x[c], x[c], ss);
+  ss = wave_sum_butterfly(ss);
+  if ((t & 63u) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float r = sqrtf(tot / (float)a.D + a.eps);
+  for (uint32_t c = t; c < a.D; c += blockDim.x) a.y[(size_t)b * a.D + c] = (x[c] / r) * a.gamma[c];
+}
+
+// hidden[b] = tok_emb[token[b]]; a token outside [0, V) reads row 0 (the caller keeps tokens in
+// range: the reference's embedding lookup fails on them, which device code cannot report here).
+struct EmbedArgs {
+  const int32_t *tokens;
+  const uint16_t *emb;
+  float *hidden;
+  uint32_t D, V;
+};
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  const uint32_t b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= a.D) return;
+  const int32_t tk = a.tokens[b];
+  const uint32_t row = (tk >= 0 && (uint32_t)tk < a.V) ? (uint32_t)tk : 0u;
+  a.hidden[(size_t)b * a.D + c] = bf16_bits_to_f32(a.emb[(size_t)row * a.D + c]);
+}
+
+// LM head: logits[b][v] = sum of the K-part partials (written when requested) and the best entry
+// of each block of kLogitsPerBlock vocabulary entries (`beats`: larger value, NaN lowest, lower
+// index on ties).
+struct LogitsArgs {
+  const float *part;
+  uint64_t part_stride;
+  uint32_t parts, V, nblk;
+  float *logits;  // [B][V] or null
+  float *bval;    // [B][nblk]
+  int32_t *bidx;  // [B][nblk]
+};
+
+__device__ __forceinline__ void block_best(float &bv, int32_t &bi, float *rv, int32_t *ri) {
+  const uint32_t t = threadIdx.x;
+  rv[t] = bv;
+  ri[t] = bi;
+  __syncthreads();
+  for (uint32_t st = 128; st >= 1; st >>= 1) {
+    if (t < st && ri[t + st] != kNoIndex && (ri[t] == kNoIndex || beats(rv[t + st], ri[t + st], rv[t], ri[t]))) {
+      rv[t] = rv[t + st];
+      ri[t] = ri[t + st];
+    }
+    __syncthreads();
+  }
+  bv = rv[0];
+  bi = ri[0];
+}
+
+__global__ __launch_bounds__(256) void logits_kernel(LogitsArgs a) {
+  __shared__ float rv[256];
+  __shared__ int32_t ri[256];
+  const uint32_t b = blockIdx.y, t = threadIdx.x;
+  float bv = -INFINITY;
+  int32_t bi = kNoIndex;
+  for (uint32_t u = 0; u < kLogitsPerBlock / 256u; ++u) {
+    const uint32_t v = blockIdx.x * kLogitsPerBlock + u * 256u + t;
+    if (v >= a.V) break;
+    float s = 0.0f;
+    for (uint32_t h = 0; h < a.parts; ++h) s = s + a.part[(size_t)h * a.part_stride + (size_t)b * a.V + v];
+    if (a.logits) a.logits[(size_t)b * a.V + v] = s;
+    if (bi == kNoIndex || beats(s, (int32_t)v, bv, bi)) {
+      bv = s;
+      bi = (int32_t)v;
+    }
+  }
+  block_best(bv, bi, rv, ri);
+  if (t == 0) {
+    a.bval[(size_t)b * a.nblk + blockIdx.x] = bv;
+    a.bidx[(size_t)b * a.nblk + blockIdx.x] = bi;
+  }
+}
+
+struct ArgmaxArgs {
+  const float *bval;
+  const int32_t *bidx;
+  uint32_t nblk;
+  int32_t *next;
+};
+__global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
+  __shared__ float rv[256];
+  __shared__ int32_t ri[256];
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  float bv = -INFINITY;
+  int32_t bi = kNoIndex;
+  for (uint32_t i = t; i < a.nblk; i += blockDim.x) {
+    const float v = a.bval[(size_t)b * a.nblk + i];
+    const int32_t ix = a.bidx[(size_t)b * a.nblk + i];
+    if (ix != kNoIndex && (bi == kNoIndex || beats(v, ix, bv, bi))) {
+      bv = v;
+      bi = ix;
+    }
+  }
+  block_best(bv, bi, rv, ri);
+  if (t == 0) a.next[b] = bi;
+}
+
+// f32 rows [B][len][kvH][dk] of one layer -> cache slots [maxB][kvH][cap][dk].
+struct CacheLoadArgs {
+  const float *src;
+  void *dst;
+  uint32_t B, len, kvH, dk, cap;
+};
+template <typename KV>
+__global__ __launch_bounds__(256) void cache_load_kernel(CacheLoadArgs a) {
+  const uint64_t n = (uint64_t)a.B * a.len * a.kvH * a.dk;
+  KV *dst = (KV *)a.dst;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t d = (uint32_t)(i % a.dk);
+    uint64_t r = i / a.dk;
+    const uint32_t hh = (uint32_t)(r % a.kvH);
+    r /= a.kvH;
+    const uint32_t p = (uint32_t)(r % a.len), b = (uint32_t)(r / a.len);
+    kv_store1(dst + (((size_t)b * a.kvH + hh) * a.cap + p) * a.dk + d, a.src[i]);
+  }
+}
+
+inline uint64_t cdiv(uint64_t x, uint64_t y) { return (x + y - 1) / y; }
+inline uint64_t align_up(uint64_t x, uint64_t y) { return cdiv(x, y) * y; }
+
+float bf16h(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// A dense [N, K] bf16 matrix in the GEMV's tiled layout (dense_gemv_kernel).
+struct DenseMat {
+  uint8_t *w = nullptr;
+  uint32_t N = 0, K = 0, nkg = 0, ntiles = 0, H = 0, parts = 0;
+};
+
+// K-groups per work unit: the largest H <= kDenseMaxH (halving, down to 4) that still gives at
+// least 8 waves per CU.
+void dense_plan(DenseMat &m, int num_cus) {
+  m.nkg = (uint32_t)cdiv(m.K, 32);
+  m.ntiles = (uint32_t)cdiv(m.N, 16);
+  uint32_t H = kDenseMaxH;
+  while (H > 4 && (uint64_t)m.ntiles * cdiv(m.nkg, H) < 8ull * (uint64_t)num_cus) H >>= 1;
+  m.H = std::min<uint32_t>(H, m.nkg);
+  m.parts = (uint32_t)cdiv(m.nkg, m.H);
+}
+
+// Host [N, K] bf16 -> tiled layout (rows beyond N and inputs beyond K are zeros).
+std::vector<uint16_t> dense_tile(const uint16_t *src, uint32_t N, uint32_t K, const DenseMat &m) {
+  std::vector<uint16_t> out((size_t)m.ntiles * m.nkg * 512, 0);
+  for (uint32_t t = 0; t < m.ntiles; ++t)
+    for (uint32_t kg = 0; kg < m.nkg; ++kg)
+      for (uint32_t l = 0; l < 64; ++l) {
+        const uint32_t row = 16 * t + (l & 15), k0 = 32 * kg + 8 * (l >> 4);
+        if (row >= N) continue;
+        uint16_t *d = out.data() + ((size_t)t * m.nkg + kg) * 512 + l * 8;
+        for (uint32_t e = 0; e < 8; ++e)
+          if (k0 + e < K) d[e] = src[(size_t)row * K + k0 + e];
+      }
+  return out;
+}
+
+}  // namespace
+
+struct burnext_gptoss {
+  int device = 0;
+  burnext_gptoss_config cfg{};
+  uint32_t qd = 0, kd = 0, groups = 0;
+  int num_cus = 256;
+  std::vector<burnext_moe_layer_t> moe;
+  uint16_t *emb = nullptr;
+  DenseMat lm;
+  std::vector<DenseMat> qkv, wo;
+  float *bqkv = nullptr, *bo = nullptr, *norm_attn = nullptr, *norm_final = nullptr, *sinks = nullptr, *rope = nullptr;
+  uint8_t *kc = nullptr, *vc = nullptr;  // [L][maxB][kvH][cap][dk] of the cache element
+  size_t kv_elem = 4;
+  uint64_t layer_cache = 0;  // elements per layer
+  uint32_t used = 0;         // cache rows held
+  uint64_t pos_next = 0;     // positions seen
+  std::vector<void *> allocs;
+};
+
+namespace {
+
+struct GWs {
+  uint64_t hid, hid2, xn, part, q, ctx, attn, bval, bidx, moe, total;
+  uint64_t moe_bytes;
+  uint32_t nblk;
+};
+
+GWs gptoss_ws(const burnext_gptoss &M, uint32_t B, uint64_t moe_bytes) {
+  GWs w{};
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) {
+    const uint64_t o = off;
+    off = align_up(off + std::max<uint64_t>(bytes, 1), 256);
+    return o;
+  };
+  const auto &c = M.cfg;
+  uint64_t part_elems = (uint64_t)M.lm.parts * B * M.lm.N;
+  for (const auto &m : M.qkv) part_elems = std::max<uint64_t>(part_elems, (uint64_t)m.parts * B * m.N);
+  for (const auto &m : M.wo) part_elems = std::max<uint64_t>(part_elems, (uint64_t)m.parts * B * m.N);
+  const uint64_t max_chunks = cdiv(c.cache_len, kAttnChunk);
+  w.nblk = (uint32_t)cdiv(c.vocab_size, kLogitsPerBlock);
+  w.hid = take((uint64_t)B * c.d_model * 4);
+  w.hid2 = take((uint64_t)B * c.d_model * 4);
+  w.xn = take((uint64_t)B * c.d_model * 4);
+  w.part = take(part_elems * 4);
+  w.q = take((uint64_t)B * M.qd * 4);
+  w.ctx = take((uint64_t)B * M.qd * 4);
+  w.attn = take((uint64_t)B * c.kv_heads * max_chunks * M.groups * (c.head_dim + 2ull) * 4);
+  w.bval = take((uint64_t)B * w.nblk * 4);
+  w.bidx = take((uint64_t)B * w.nblk * 4);
+  w.moe = take(moe_bytes);
+  w.moe_bytes = moe_bytes;
+  w.total = off;
+  return w;
+}
+
+burnext_status hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) return set_error(BURNEXT_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+  return BURNEXT_OK;
+}
+
+struct DevGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DevGuard(int d) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(d) == hipSuccess;
+  }
+  ~DevGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+void free_model(burnext_gptoss *M) {
+  if (!M) return;
+  DevGuard g(M->device);
+  for (void *p : M->allocs)
+    if (p) (void)hipFree(p);
+  delete M;
+}
+
+burnext_status dev_alloc(burnext_gptoss *M, void **dst, size_t bytes) {
+  if (hipMalloc(dst, std::max<size_t>(bytes, 1)) != hipSuccess) {
+    *dst = nullptr;
+    return set_error(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed in burnext_gptoss_create");
+  }
+  M->allocs.push_back(*dst);
+  return BURNEXT_OK;
+}
+
+template <typename T>
+burnext_status upload(burnext_gptoss *M, T **dst, const T *src, size_t n) {
+  const burnext_status st = dev_alloc(M, (void **)dst, n * sizeof(T));
+  if (st != BURNEXT_OK) return st;
+  if (n && hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    return set_error(BURNEXT_DEVICE_ERROR, "hipMemcpy failed in burnext_gptoss_create");
+  return BURNEXT_OK;
+}
+
+burnext_status dense_gemv(const DenseMat &m, const float *x, uint32_t B, float *out, hipStream_t s) {
+  DenseArgs a{};
+  a.w = m.w;
+  a.x = x;
+  a.out = out;
+  a.N = m.N;
+  a.K = m.K;
+  a.nkg = m.nkg;
+  a.ntiles = m.ntiles;
+  a.B = B;
+  a.H = m.H;
+  a.part_stride = (uint64_t)B * m.N;
+  const size_t lds = 2ull * 16 * (m.H * 32 + 8) * 2;
+  return hip_check(launch_kernel(dense_gemv_kernel, dim3((uint32_t)cdiv(m.ntiles, 4), m.parts), dim3(256), lds, s, a),
+                   "dense GEMV launch");
+}
+
+template <typename KV>
+hipError_t launch_attention_kv(uint32_t groups, dim3 grid, hipStream_t s, const AttnArgs &a) {
+  switch (groups) {
+    case 1: return launch_kernel(attn_chunk_kernel<KV, 1>, grid, dim3(256), 0, s, a);
+    case 2: return launch_kernel(attn_chunk_kernel<KV, 2>, grid, dim3(256), 0, s, a);
+    case 4: return launch_kernel(attn_chunk_kernel<KV, 4>, grid, dim3(256), 0, s, a);
+    case 8: return launch_kernel(attn_chunk_kernel<KV, 8>, grid, dim3(256), 0, s, a);
+    case 16: return launch_kernel(attn_chunk_kernel<KV, 16>, grid, dim3(256), 0, s, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_attention(bool kv_bf16, uint32_t groups, dim3 grid, hipStream_t s, const AttnArgs &a) {
+  return kv_bf16 ? launch_attention_kv<uint16_t>(groups, grid, s, a) : launch_attention_kv<float>(groups, grid, s, a);
+}
+
+// YaRN-scaled inverse frequencies and concentration (src/rope/mod.rs:11-52 over Burn's
+// RotaryEncoding frequency scaling): inv[i] = theta^(-2 i / d); with factor > 1 the ramp
+// r = clamp((2 i - low) / (high - low), 0, 1) blends inv / factor (r = 0) and inv (r = 1),
+// low = d ln(ctx / (beta 2 pi)) / ln theta, high = d ln(ctx / (alpha 2 pi)) / ln theta; the
+// cos/sin table is multiplied by 0.1 ln(factor) + 1.
+bool yarn_frequencies(const burnext_gptoss_config &c, std::vector<double> &inv, double &conc) {
+  const uint32_t dk = c.head_dim, half = dk / 2;
+  inv.assign(half, 0.0);
+  for (uint32_t i = 0; i < half; ++i) inv[i] = (double)(float)(1.0 / std::pow((double)c.rope_theta, (2.0 * i) / dk));
+  conc = 1.0;
+  if (!(c.rope_scaling_factor > 1.0f)) return true;
+  const double dd = dk, lb = std::log((double)c.rope_theta), two_pi = 6.283185307179586476925;
+  const double low = dd * std::log(c.rope_initial_context / (c.rope_ntk_beta * two_pi)) / lb;
+  const double high = dd * std::log(c.rope_initial_context / (c.rope_ntk_alpha * two_pi)) / lb;
+  if (!(low > 0.0 && high > 0.0 && low < high && high < dd - 1.0)) return false;
+  for (uint32_t i = 0; i < half; ++i) {
+    const double f = inv[i], ir = -std::log(f) * dd / lb;
+    const double r = std::min(1.0, std::max(0.0, (ir - low) / (high - low)));
+    inv[i] = (double)(float)(f / c.rope_scaling_factor * (1.0 - r) + f * r);
+  }
+  conc = (double)(float)(0.1 * std::log((double)c.rope_scaling_factor) + 1.0);
+  return true;
+}
+
+// The layer's attention window, 0 = Full: WindowPolicy::window_for(l) combined with the caller's
+// window by combine_windows (src/cache/mod.rs:15-44): Full yields the other, two windows the smaller.
+uint32_t layer_window(const burnext_gptoss_config &c, uint32_t l, uint32_t caller) {
+  uint32_t pw = 0;
+  if (c.window_policy == 1) pw = c.window;
+  if (c.window_policy == 2) pw = ((l % 2 == 0) == (c.full_on_even != 0)) ? 0 : c.window;
+  if (pw == 0) return caller;
+  return caller == 0 ? pw : std::min(pw, caller);
+}
+
+burnext_status moe_ws_bytes(const burnext_gptoss *M, uint32_t batch, uint64_t *bytes) {
+  uint64_t moe = 0;
+  for (auto *m : M->moe) {
+    uint64_t b = 0;
+    const burnext_status s = burnext_moe_workspace_size(m, batch, &b);
+    if (s != BURNEXT_OK) return s;
+    moe = std::max(moe, b);
+  }
+  *bytes = moe;
+  return BURNEXT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const burnext_gptoss_weights *w,
+                                     const burnext_moe_layer_t *moe_layers, int device, burnext_gptoss_t *out) {
+  if (!out) return set_error(BURNEXT_INVALID_ARG, "out is null");
+  *out = nullptr;
+  if (!cfg || !w || !moe_layers) return set_error(BURNEXT_INVALID_ARG, "null config, weights or MoE layers");
+  const auto &c = *cfg;
+  if (!w->tok_emb || !w->norm_attn || !w->wq || !w->bq || !w->wk || !w->bk || !w->wv || !w->bv || !w->wo || !w->bo ||
+      !w->norm_final || !w->lm_head)
+    return set_error(BURNEXT_INVALID_ARG, "null weight pointer");
+  if (!c.vocab_size || !c.d_model || !c.n_layers || !c.n_heads || !c.kv_heads || !c.head_dim || !c.max_batch ||
+      !c.cache_len || !c.max_positions)
+    return set_error(BURNEXT_INVALID_ARG, "zero dimension in burnext_gptoss_config");
+  if (c.n_heads % c.kv_heads || c.n_heads / c.kv_heads > kMaxGroups || ((c.n_heads / c.kv_heads) & (c.n_heads / c.kv_heads - 1)))
+    return set_error(BURNEXT_UNSUPPORTED, "n_heads / kv_heads must be a power of two <= 16");
+  if (c.head_dim % 8 || c.head_dim > kMaxHeadDim)
+    return set_error(BURNEXT_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 128");
+  if (c.max_batch > kMaxBatch) return set_error(BURNEXT_UNSUPPORTED, "max_batch above 16 is not supported");
+  if (c.d_model % 2) return set_error(BURNEXT_UNSUPPORTED, "d_model must be even");
+  if (c.rope_head_stride > 1 || c.kv_bf16 > 1 || c.full_on_even > 1)
+    return set_error(BURNEXT_INVALID_ARG, "rope_head_stride, kv_bf16 and full_on_even must be 0 or 1");
+  if (c.window_policy > 2) return set_error(BURNEXT_INVALID_ARG, "window_policy must be 0 (Full), 1 (Fixed) or 2 (EveryOther)");
+  if (c.window_policy != 0 && c.window == 0) return set_error(BURNEXT_INVALID_ARG, "window must be positive");
+  if (c.cache_len > (1u << 30) || c.max_positions > (1u << 30))
+    return set_error(BURNEXT_UNSUPPORTED, "cache_len and max_positions above 2^30 are not supported");
+  if (!(c.scale_dk > 0.0f) || !(c.rms_eps >= 0.0f) || !(c.rope_theta > 1.0f))
+    return set_error(BURNEXT_INVALID_ARG, "scale_dk > 0, rope_theta > 1 and rms_eps >= 0 are required");
+  std::vector<double> inv;
+  double conc = 1.0;
+  if (!yarn_frequencies(c, inv, conc))
+    return set_error(BURNEXT_INVALID_ARG, "YaRN thresholds out of range (the reference asserts 0 < low < high < d - 1)");
+  for (uint32_t l = 0; l < c.n_layers; ++l)
+    if (!moe_layers[l]) return set_error(BURNEXT_INVALID_ARG, "null MoE layer handle");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return set_error(BURNEXT_INVALID_ARG, "device index out of range (or no HIP device)");
+  for (uint32_t l = 0; l < c.n_layers; ++l) {
+    uint32_t dm = 0;
+    int dev = -1;
+    moe_layer_shape(moe_layers[l], &dm, &dev);
+    if (dm != c.d_model || dev != device)
+      return set_error(BURNEXT_INVALID_ARG, "MoE layer d_model or device differs from the decoder's");
+  }
+  DevGuard guard(device);
+  if (!guard.ok) return set_error(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  burnext_gptoss *M = new (std::nothrow) burnext_gptoss();
+  if (!M) return set_error(BURNEXT_OUT_OF_MEMORY, "host allocation failed");
+  M->device = device;
+  M->cfg = c;
+  const uint32_t dk = c.head_dim, half = dk / 2;
+  M->qd = c.n_heads * dk;
+  M->kd = c.kv_heads * dk;
+  M->groups = c.n_heads / c.kv_heads;
+  M->kv_elem = c.kv_bf16 ? 2 : 4;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) M->num_cus = cus;
+  M->moe.assign(moe_layers, moe_layers + c.n_layers);
+  const uint32_t D = c.d_model, L = c.n_layers, V = c.vocab_size, N3 = M->qd + 2 * M->kd;
+  burnext_status st = upload(M, &M->emb, w->tok_emb, (size_t)V * D);
+  auto up_dense = [&](DenseMat &m, const uint16_t *src) -> burnext_status {
+    dense_plan(m, M->num_cus);
+    const std::vector<uint16_t> t = dense_tile(src, m.N, m.K, m);
+    uint16_t *p = nullptr;
+    const burnext_status s2 = upload(M, &p, t.data(), t.size());
+    m.w = (uint8_t *)p;
+    return s2;
+  };
+  M->lm.N = V;
+  M->lm.K = D;
+  if (st == BURNEXT_OK) st = up_dense(M->lm, w->lm_head);
+  M->qkv.resize(L);
+  M->wo.resize(L);
+  std::vector<uint16_t> fused((size_t)N3 * D);
+  for (uint32_t l = 0; l < L && st == BURNEXT_OK; ++l) {
+    memcpy(fused.data(), w->wq + (size_t)l * M->qd * D, (size_t)M->qd * D * 2);
+    memcpy(fused.data() + (size_t)M->qd * D, w->wk + (size_t)l * M->kd * D, (size_t)M->kd * D * 2);
+    memcpy(fused.data() + (size_t)(M->qd + M->kd) * D, w->wv + (size_t)l * M->kd * D, (size_t)M->kd * D * 2);
+    M->qkv[l].N = N3;
+    M->qkv[l].K = D;
+    st = up_dense(M->qkv[l], fused.data());
+    if (st != BURNEXT_OK) break;
+    M->wo[l].N = D;
+    M->wo[l].K = M->qd;
+    st = up_dense(M->wo[l], w->wo + (size_t)l * D * M->qd);
+  }
+  if (st == BURNEXT_OK) {
+    std::vector<float> bq((size_t)L * N3), bo((size_t)L * D), na((size_t)L * D), nf(D), sk;
+    for (uint32_t l = 0; l < L; ++l) {
+      for (uint32_t i = 0; i < M->qd; ++i) bq[(size_t)l * N3 + i] = bf16h(w->bq[(size_t)l * M->qd + i]);
+      for (uint32_t i = 0; i < M->kd; ++i) {
+        bq[(size_t)l * N3 + M->qd + i] = bf16h(w->bk[(size_t)l * M->kd + i]);
+        bq[(size_t)l * N3 + M->qd + M->kd + i] = bf16h(w->bv[(size_t)l * M->kd + i]);
+      }
+      for (uint32_t i = 0; i < D; ++i) {
+        bo[(size_t)l * D + i] = bf16h(w->bo[(size_t)l * D + i]);
+        na[(size_t)l * D + i] = bf16h(w->norm_attn[(size_t)l * D + i]);
+      }
+    }
+    for (uint32_t i = 0; i < D; ++i) nf[i] = bf16h(w->norm_final[i]);
+    st = upload(M, &M->bqkv, bq.data(), bq.size());
+    if (st == BURNEXT_OK) st = upload(M, &M->bo, bo.data(), bo.size());
+    if (st == BURNEXT_OK) st = upload(M, &M->norm_attn, na.data(), na.size());
+    if (st == BURNEXT_OK) st = upload(M, &M->norm_final, nf.data(), nf.size());
+    if (st == BURNEXT_OK && w->sinks) {
+      sk.resize((size_t)L * c.n_heads);
+      for (size_t i = 0; i < sk.size(); ++i) sk[i] = bf16h(w->sinks[i]);
+      st = upload(M, &M->sinks, sk.data(), sk.size());
+    }
+  }
+  if (st == BURNEXT_OK) {  // RoPE table [max_positions + nH][dk/2][2] = (cos, sin) x concentration
+    const uint64_t npos = (uint64_t)c.max_positions + c.n_heads;
+    std::vector<float> tab(npos * half * 2);
+    for (uint64_t p = 0; p < npos; ++p)
+      for (uint32_t i = 0; i < half; ++i) {
+        const float ang = (float)p * (float)inv[i];  // one f32 product, as the reference's f32 table
+        tab[(p * half + i) * 2] = (float)(std::cos((double)ang) * conc);
+        tab[(p * half + i) * 2 + 1] = (float)(std::sin((double)ang) * conc);
+      }
+    st = upload(M, &M->rope, tab.data(), tab.size());
+  }
+  if (st == BURNEXT_OK) {  // KV cache
+    M->layer_cache = (uint64_t)c.max_batch * c.kv_heads * c.cache_len * dk;
+    const size_t bytes = (size_t)L * M->layer_cache * M->kv_elem;
+    st = dev_alloc(M, (void **)&M->kc, bytes);
+    if (st == BURNEXT_OK) st = dev_alloc(M, (void **)&M->vc, bytes);
+    if (st == BURNEXT_OK && (hipMemset(M->kc, 0, bytes) != hipSuccess || hipMemset(M->vc, 0, bytes) != hipSuccess))
+      st = set_error(BURNEXT_DEVICE_ERROR, "hipMemset of the KV cache failed");
+  }
+  if (st != BURNEXT_OK) {
+    free_model(M);
+    return st;
+  }
+  *out = M;
+  return set_error(BURNEXT_OK, "");
+}
+
+void burnext_gptoss_destroy(burnext_gptoss_t M) { free_model(M); }
+
+burnext_status burnext_gptoss_workspace_size(burnext_gptoss_t M, uint32_t batch, uint64_t *bytes) {
+  if (!M || !bytes) return set_error(BURNEXT_INVALID_ARG, "null model or output pointer");
+  if (batch == 0 || batch > M->cfg.max_batch) return set_error(BURNEXT_INVALID_ARG, "batch must be in [1, max_batch]");
+  uint64_t moe = 0;
+  const burnext_status s = moe_ws_bytes(M, batch, &moe);
+  if (s != BURNEXT_OK) return s;
+  *bytes = gptoss_ws(*M, batch, moe).total;
+  return set_error(BURNEXT_OK, "");
+}
+
+burnext_status burnext_gptoss_reset(burnext_gptoss_t M) {
+  if (!M) return set_error(BURNEXT_INVALID_ARG, "null model");
+  M->used = 0;
+  M->pos_next = 0;
+  return set_error(BURNEXT_OK, "");
+}
+
+burnext_status burnext_gptoss_cache_load(burnext_gptoss_t M, const float *k, const float *v, uint32_t batch,
+                                         uint32_t len, void *stream) {
+  if (!M) return set_error(BURNEXT_INVALID_ARG, "null model");
+  if (batch == 0 || batch > M->cfg.max_batch) return set_error(BURNEXT_INVALID_ARG, "batch must be in [1, max_batch]");
+  if (len > M->cfg.cache_len) return set_error(BURNEXT_INVALID_ARG, "len exceeds cache_len");
+  if (len > 0 && (!k || !v)) return set_error(BURNEXT_INVALID_ARG, "null cache rows");
+  DevGuard guard(M->device);
+  if (!guard.ok) return set_error(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  hipStream_t s = (hipStream_t)stream;
+  const uint64_t per_layer = (uint64_t)batch * len * M->cfg.kv_heads * M->cfg.head_dim;
+  for (uint32_t l = 0; l < M->cfg.n_layers && len > 0; ++l)
+    for (int which = 0; which < 2; ++which) {
+      CacheLoadArgs a{};
+      a.src = (which ? v : k) + l * per_layer;
+      a.dst = (which ? M->vc : M->kc) + l * M->layer_cache * M->kv_elem;
+      a.B = batch;
+      a.len = len;
+      a.kvH = M->cfg.kv_heads;
+      a.dk = M->cfg.head_dim;
+      a.cap = M->cfg.cache_len;
+      const dim3 grid((uint32_t)std::min<uint64_t>(cdiv(per_layer, 256), 8192));
+      const hipError_t e = M->cfg.kv_bf16 ? launch_kernel(cache_load_kernel<uint16_t>, grid, dim3(256), 0, s, a)
+                                          : launch_kernel(cache_load_kernel<float>, grid, dim3(256), 0, s, a);
+      const burnext_status st = hip_check(e, "cache load launch");
+      if (st != BURNEXT_OK) return st;
+    }
+  M->used = len;
+  M->pos_next = len;
+  return set_error(BURNEXT_OK, "");
+}
+
+burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, uint32_t B, uint32_t pos,
+                                     uint32_t window, int32_t *next_tokens, float *logits, float *hidden,
+                                     void *workspace, uint64_t ws_bytes, void *stream) {
+  if (!M || !tokens || !next_tokens) return set_error(BURNEXT_INVALID_ARG, "null model, tokens or next_tokens");
+  const auto &c = M->cfg;
+  if (B == 0 || B > c.max_batch) return set_error(BURNEXT_INVALID_ARG, "batch must be in [1, max_batch]");
+  if (pos != M->pos_next) {
+    char buf[160];
+    snprintf(buf, sizeof(buf), "pos %u is not the next position (%llu positions seen)", pos,
+             (unsigned long long)M->pos_next);
+    return set_error(BURNEXT_INVALID_ARG, buf);
+  }
+  if (pos >= c.max_positions) return set_error(BURNEXT_UNSUPPORTED, "pos >= max_positions (beyond the RoPE table)");
+  if (!workspace || ((uintptr_t)workspace & 255u))
+    return set_error(BURNEXT_INVALID_ARG, "workspace null or not 256-byte aligned");
+  uint64_t moe_bytes = 0;
+  burnext_status st = moe_ws_bytes(M, B, &moe_bytes);
+  if (st != BURNEXT_OK) return st;
+  const GWs w = gptoss_ws(*M, B, moe_bytes);
+  if (ws_bytes < w.total)
+    return set_error(BURNEXT_WORKSPACE_TOO_SMALL, "workspace smaller than burnext_gptoss_workspace_size");
+  DevGuard guard(M->device);
+  if (!guard.ok) return set_error(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t *base = (uint8_t *)workspace;
+  float *hid = (float *)(base + w.hid), *hid2 = (float *)(base + w.hid2), *xn = (float *)(base + w.xn);
+  float *part = (float *)(base + w.part), *qb = (float *)(base + w.q), *ctx = (float *)(base + w.ctx);
+  float *attn = (float *)(base + w.attn), *bval = (float *)(base + w.bval);
+  int32_t *bidx = (int32_t *)(base + w.bidx);
+  void *moe_ws = base + w.moe;
+  const uint32_t D = c.d_model, dk = c.head_dim, cap = c.cache_len, N3 = M->qd + 2 * M->kd;
+  const uint32_t used = (uint32_t)std::min<uint64_t>((uint64_t)M->used + 1, cap), slot = pos % cap;
+  {
+    EmbedArgs a{tokens, M->emb, hid, D, c.vocab_size};
+    st = hip_check(launch_kernel(embed_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, a), "embedding launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  for (uint32_t l = 0; l < c.n_layers; ++l) {
+    NormArgs na{hid, M->norm_attn + (size_t)l * D, xn, D, c.rms_eps};
+    st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, na), "RmsNorm launch");
+    if (st == BURNEXT_OK) st = dense_gemv(M->qkv[l], xn, B, part, s);
+    if (st != BURNEXT_OK) return st;
+    QkvPostArgs qa{};
+    qa.part = part;
+    qa.part_stride = (uint64_t)B * N3;
+    qa.parts = M->qkv[l].parts;
+    qa.bias = M->bqkv + (size_t)l * N3;
+    qa.rope = M->rope;
+    qa.qbuf = qb;
+    qa.kc = M->kc + l * M->layer_cache * M->kv_elem;
+    qa.vc = M->vc + l * M->layer_cache * M->kv_elem;
+    qa.B = B;
+    qa.nH = c.n_heads;
+    qa.kvH = c.kv_heads;
+    qa.dk = dk;
+    qa.cap = cap;
+    qa.slot = slot;
+    qa.pos = pos;
+    qa.head_stride = c.rope_head_stride;
+    const dim3 qgrid((uint32_t)cdiv(N3 / 2, 256), B);
+    st = hip_check(c.kv_bf16 ? launch_kernel(qkv_post_kernel<uint16_t>, qgrid, dim3(256), 0, s, qa)
+                             : launch_kernel(qkv_post_kernel<float>, qgrid, dim3(256), 0, s, qa),
+                   "q/k/v post launch");
+    if (st != BURNEXT_OK) return st;
+    const uint32_t lw = layer_window(c, l, window);  // 0 = Full
+    const uint32_t active = lw ? std::min(lw, used) : used;
+    AttnArgs aa{};
+    aa.q = qb;
+    aa.kc = qa.kc;
+    aa.vc = qa.vc;
+    aa.part = attn;
+    aa.nH = c.n_heads;
+    aa.kvH = c.kv_heads;
+    aa.dk = dk;
+    aa.cap = cap;
+    aa.p_hi = pos;
+    aa.p_lo = pos + 1 - active;
+    aa.nchunk = (uint32_t)cdiv(active, kAttnChunk);
+    aa.inv_scale = 1.0f / std::sqrt(c.scale_dk);
+    const dim3 agrid(aa.nchunk, c.kv_heads, B);
+    st = hip_check(launch_attention(c.kv_bf16 != 0, M->groups, agrid, s, aa), "attention launch");
+    if (st != BURNEXT_OK) return st;
+    CombineAttnArgs ca{attn, M->sinks ? M->sinks + (size_t)l * c.n_heads : nullptr, ctx, c.n_heads, c.kv_heads, dk,
+                       aa.nchunk};
+    st = hip_check(launch_kernel(attn_combine_kernel, dim3(c.kv_heads, B), dim3(256), 0, s, ca),
+                   "attention combine launch");
+    if (st == BURNEXT_OK) st = dense_gemv(M->wo[l], ctx, B, part, s);
+    if (st != BURNEXT_OK) return st;
+    OPostArgs oa{part, (uint64_t)B * D, M->wo[l].parts, D, M->bo + (size_t)l * D, hid};
+    st = hip_check(launch_kernel(o_post_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, oa), "o post launch");
+    if (st != BURNEXT_OK) return st;
+    st = burnext_moe_forward(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes, stream);
+    if (st != BURNEXT_OK) return st;
+    std::swap(hid, hid2);
+  }
+  if (hidden) {
+    st = hip_check(hipMemcpyAsync(hidden, hid, (size_t)B * D * 4, hipMemcpyDeviceToDevice, s), "hidden copy");
+    if (st != BURNEXT_OK) return st;
+  }
+  NormArgs nf{hid, M->norm_final, xn, D, c.rms_eps};
+  st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, nf), "final RmsNorm launch");
+  if (st == BURNEXT_OK) st = dense_gemv(M->lm, xn, B, part, s);
+  if (st != BURNEXT_OK) return st;
+  LogitsArgs la{part, (uint64_t)B * c.vocab_size, M->lm.parts, c.vocab_size, w.nblk, logits, bval, bidx};
+  st = hip_check(launch_kernel(logits_kernel, dim3(w.nblk, B), dim3(256), 0, s, la), "logits launch");
+  if (st != BURNEXT_OK) return st;
+  ArgmaxArgs ga{bval, bidx, w.nblk, next_tokens};
+  st = hip_check(launch_kernel(argmax_kernel, dim3(B), dim3(256), 0, s, ga), "argmax launch");
+  if (st != BURNEXT_OK) return st;
+  M->used = used;
+  M->pos_next = (uint64_t)pos + 1;
+  return set_error(BURNEXT_OK, "");
+}
+
+}  // extern "C"

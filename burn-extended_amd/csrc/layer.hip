@@ -69,6 +69,11 @@ struct ProfPair {
 
 }  // namespace
 
+namespace burnext {
+// The thread's burnext_last_error() message, shared with the decoder entry points.
+burnext_status set_error(burnext_status st, const std::string &msg) { return fail(st, msg); }
+}  // namespace burnext
+
 // Tiled MXFP4 layout of one projection (see the expert_gemv comment in kernels.hip).
 struct TiledMx {
   uint32_t rows = 0, rows_p = 0, cols = 0, nb = 0, nrt = 0;
@@ -96,6 +101,14 @@ struct burnext_moe_layer {
   bool profiling = false;
   std::vector<ProfPair> prof;
 };
+
+namespace burnext {
+// d_model and device of a MoE layer (the decoder checks them against its own at create).
+void moe_layer_shape(const burnext_moe_layer *L, uint32_t *d_model, int *device) {
+  *d_model = L->D;
+  *device = L->device;
+}
+}  // namespace burnext
 
 namespace {
 

@@ -18,10 +18,11 @@ sys.path.insert(0, str(ROOT / "burn-extended_amd"))
 from burnext_amd import _native as N  # noqa: E402
 
 HEADER = ROOT / "include" / "burnext_moe.h"
+HEADERS = [HEADER, ROOT / "include" / "burnext_gptoss.h"]
 
 
 def header_functions() -> list[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = "".join(re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S) for h in HEADERS)
     return sorted(set(re.findall(r"\b(burnext_\w+)\s*\(", text)))
 
 
@@ -193,3 +194,103 @@ def test_last_error_is_thread_local(L):
     t.join()
     assert seen == [""]
     assert "256" in N.last_error()
+
+
+# ---- include/burnext_gptoss.h -------------------------------------------------------------------
+
+def test_gptoss_struct_layouts_match_header():
+    src = r'''
+#include <stddef.h>
+#include <stdio.h>
+#include "burnext_gptoss.h"
+int main(void) {
+  printf("%zu %zu %zu %zu %zu\n", sizeof(burnext_gptoss_config), offsetof(burnext_gptoss_config, kv_bf16),
+         offsetof(burnext_gptoss_config, rms_eps), offsetof(burnext_gptoss_config, scale_dk),
+         sizeof(burnext_gptoss_weights));
+  printf("%zu %zu\n", offsetof(burnext_gptoss_weights, sinks), offsetof(burnext_gptoss_weights, lm_head));
+  return 0;
+}
+'''
+    exe = ROOT / "oracle" / "_build" / "abi_layout_gptoss"
+    exe.parent.mkdir(parents=True, exist_ok=True)
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", str(HEADER.parent), "-x", "c", "-", "-o",
+                        str(exe)], input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals == [ctypes.sizeof(N.GptOssConfigC), N.GptOssConfigC.kv_bf16.offset, N.GptOssConfigC.rms_eps.offset,
+                    N.GptOssConfigC.scale_dk.offset, ctypes.sizeof(N.GptOssWeightsC), N.GptOssWeightsC.sinks.offset,
+                    N.GptOssWeightsC.lm_head.offset]
+
+
+def _gcfg(**kw):
+    base = dict(vocab_size=64, d_model=64, n_layers=2, n_heads=4, kv_heads=2, head_dim=16, max_batch=4, cache_len=32,
+                window_policy=2, window=8, full_on_even=1, rope_head_stride=1, max_positions=64, kv_bf16=0, rms_eps=1e-5,
+                rope_theta=150000.0, rope_scaling_factor=32.0, rope_initial_context=4096.0, rope_ntk_alpha=1.0,
+                rope_ntk_beta=32.0, scale_dk=1.0)
+    base.update(kw)
+    return N.GptOssConfigC(**base)
+
+
+def _gweights():
+    buf = np.zeros(1 << 16, np.uint16)
+    p = buf.ctypes.data_as(ctypes.c_void_p)
+    return N.GptOssWeightsC(*([p] * 13)), buf
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(head_dim=12), N.BURNEXT_UNSUPPORTED, "head_dim"),
+    (dict(head_dim=136), N.BURNEXT_UNSUPPORTED, "head_dim"),
+    (dict(n_heads=6, kv_heads=2), N.BURNEXT_UNSUPPORTED, "power of two"),
+    (dict(n_heads=5, kv_heads=2), N.BURNEXT_UNSUPPORTED, "power of two"),
+    (dict(n_heads=64, kv_heads=2), N.BURNEXT_UNSUPPORTED, "power of two"),
+    (dict(max_batch=17), N.BURNEXT_UNSUPPORTED, "max_batch"),
+    (dict(d_model=63), N.BURNEXT_UNSUPPORTED, "d_model"),
+    (dict(vocab_size=0), N.BURNEXT_INVALID_ARG, "zero dimension"),
+    (dict(cache_len=0), N.BURNEXT_INVALID_ARG, "zero dimension"),
+    (dict(kv_bf16=2), N.BURNEXT_INVALID_ARG, "kv_bf16"),
+    (dict(rope_head_stride=3), N.BURNEXT_INVALID_ARG, "rope_head_stride"),
+    (dict(window=0), N.BURNEXT_INVALID_ARG, "window"),
+    (dict(window_policy=3), N.BURNEXT_INVALID_ARG, "window_policy"),
+    (dict(scale_dk=0.0), N.BURNEXT_INVALID_ARG, "scale_dk"),
+    (dict(rope_theta=1.0), N.BURNEXT_INVALID_ARG, "rope_theta"),
+    # YaRN thresholds: beta <= alpha makes low >= high (the reference asserts)
+    (dict(rope_ntk_alpha=32.0, rope_ntk_beta=1.0), N.BURNEXT_INVALID_ARG, "YaRN"),
+])
+def test_gptoss_create_rejects_bad_config(L, kw, status, msg):
+    cfg = _gcfg(**kw)
+    w, _buf = _gweights()
+    handles = (ctypes.c_void_p * 2)(1, 1)
+    out = ctypes.c_void_p(123)
+    st = L.burnext_gptoss_create(ctypes.byref(cfg), ctypes.byref(w), handles, 0, ctypes.byref(out))
+    assert st == status, N.last_error()
+    assert msg in N.last_error()
+    assert not out.value
+
+
+def test_gptoss_create_rejects_null_arguments(L):
+    cfg = _gcfg()
+    w, _buf = _gweights()
+    handles = (ctypes.c_void_p * 2)(1, 1)
+    out = ctypes.c_void_p()
+    assert L.burnext_gptoss_create(ctypes.byref(cfg), ctypes.byref(w), handles, 0, None) == N.BURNEXT_INVALID_ARG
+    assert L.burnext_gptoss_create(None, ctypes.byref(w), handles, 0, ctypes.byref(out)) == N.BURNEXT_INVALID_ARG
+    assert L.burnext_gptoss_create(ctypes.byref(cfg), ctypes.byref(w), None, 0, ctypes.byref(out)) == \
+        N.BURNEXT_INVALID_ARG
+    w.wq = None
+    assert L.burnext_gptoss_create(ctypes.byref(cfg), ctypes.byref(w), handles, 0, ctypes.byref(out)) == \
+        N.BURNEXT_INVALID_ARG
+    assert "weight" in N.last_error()
+    w, _buf = _gweights()
+    nulls = (ctypes.c_void_p * 2)(1, None)
+    assert L.burnext_gptoss_create(ctypes.byref(cfg), ctypes.byref(w), nulls, 0, ctypes.byref(out)) == \
+        N.BURNEXT_INVALID_ARG
+    assert "MoE layer" in N.last_error()
+
+
+def test_gptoss_calls_on_null_model(L):
+    b = ctypes.c_uint64()
+    assert L.burnext_gptoss_workspace_size(None, 1, ctypes.byref(b)) == N.BURNEXT_INVALID_ARG
+    assert L.burnext_gptoss_reset(None) == N.BURNEXT_INVALID_ARG
+    assert L.burnext_gptoss_cache_load(None, None, None, 1, 0, None) == N.BURNEXT_INVALID_ARG
+    assert L.burnext_gptoss_decode(None, None, 1, 0, 0, None, None, None, None, 0, None) == N.BURNEXT_INVALID_ARG
+    L.burnext_gptoss_destroy(None)  # no-op

@@ -1,0 +1,176 @@
+"""GPU parity of the decoder decode step (include/burnext_gptoss.h) against the CPU decoder oracle.
+
+Bars: with f32 cache rows (the reference's element) logits and the final hidden state within
+max|y - y_ref| / max|y_ref| <= 5e-4 of the oracle at every step, greedy tokens equal wherever the
+oracle's top-2 margin exceeds that tolerance; with bf16 cache rows within the bf16 bar 2e-2.  The
+cases cover cache eviction (positions past cache_len), every window policy and the caller's
+window, sinks, head-indexed and per-token RoPE positions, YaRN on and off, partial row tiles
+(vocabulary not a multiple of 16), group sizes 1..16 and the GPT-OSS-20B shapes with an 8192-row
+cache.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 5e-4
+TOL_BF16 = 2e-2
+
+
+@pytest.fixture(scope="module")
+def D():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from burnext_amd import decoder
+    return decoder
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _cfg(D, **kw):
+    base = dict(vocab_size=509, d_model=256, n_layers=4, n_heads=8, head_dim=32, kv_heads=2, ffn_hidden=256,
+                num_experts=4, experts_per_token=2, cache_len=40, window_policy="every_other", window=8,
+                full_on_even=True, max_seq_len=128)
+    base.update(kw)
+    return D.GptOssConfig(**base)
+
+
+def _check_step(oracle, tol, nxt, lg, hid, o_nxt, o_lg, o_hid, where):
+    assert oracle.max_abs_rel(_np(hid), o_hid) <= tol, (where, oracle.max_abs_rel(_np(hid), o_hid))
+    assert oracle.max_abs_rel(_np(lg), o_lg) <= tol, (where, oracle.max_abs_rel(_np(lg), o_lg))
+    top2 = np.sort(o_lg, axis=1)[:, -2:]
+    scale = np.abs(o_lg).max()
+    n = _np(nxt).astype(np.int64)
+    for b in range(o_lg.shape[0]):
+        if top2[b, 1] - top2[b, 0] > 2 * tol * scale:
+            assert n[b] == o_nxt[b], (where, b)
+
+
+CASES = {
+    "every_other": dict(),
+    "every_other_odd_full": dict(full_on_even=False),
+    "fixed": dict(window_policy="fixed", window=5),
+    "full_stride0": dict(window_policy="full", rope_head_stride=0),
+    "no_yarn_no_sinks": dict(use_ntk_yarn=False, learned_sinks=False),
+    "groups1": dict(n_heads=4, kv_heads=4, head_dim=64),
+    "groups16": dict(n_heads=16, kv_heads=1, head_dim=16),
+    "dk128": dict(n_heads=4, kv_heads=2, head_dim=128, cache_len=300, window=200, max_seq_len=512),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_decode_steps_match_oracle(D, oracle, case):
+    """Teacher-forced decode past cache eviction; tokens fed to both sides are the oracle's greedy
+    choices, so a near-tie cannot fork the two sequences."""
+    cfg = _cfg(D, **CASES[case])
+    data = D.make_decoder(cfg, seed=11, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B = 3
+    print(f"[decoder] case={case} cfg={cfg}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    orc = oracle.DecoderOracle(data, B)
+    rng = np.random.default_rng(7)
+    tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
+    caller = 6 if case == "full_stride0" else 0
+    steps = cfg.cache_len + 12
+    for pos in range(steps):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True, window=caller)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos, caller)
+        torch.cuda.synchronize()
+        _check_step(oracle, TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, (case, pos))
+        tok = o_nxt
+    dev.close()
+
+
+def test_decode_bf16_cache(D, oracle):
+    cfg = _cfg(D, kv_bf16=True)
+    data = D.make_decoder(cfg, seed=12, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B = 2
+    dev = D.GptOssDecoder(data, max_batch=B)
+    orc = oracle.DecoderOracle(data, B)
+    tok = np.array([3, 100], np.int32)
+    for pos in range(cfg.cache_len + 5):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        _check_step(oracle, TOL_BF16, nxt, lg, hid, o_nxt, o_lg, o_hid, pos)
+        tok = o_nxt
+
+
+def test_greedy_generation_and_null_outputs(D, oracle):
+    """Free-running greedy generation equals the oracle's token for token; the step without
+    logits / hidden outputs returns the same tokens; batch rows are independent."""
+    cfg = _cfg(D, cache_len=24)
+    data = D.make_decoder(cfg, seed=13, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B = 4
+    first = np.array([1, 2, 3, 1], np.int32)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    gen = _np(dev.generate(torch.from_numpy(first).cuda(), 0, 30)).astype(np.int32)
+    orc = oracle.DecoderOracle(data, B)
+    tok, seq = first, []
+    for pos in range(30):
+        tok, _, _ = orc.step(tok, pos)
+        seq.append(tok)
+    assert np.array_equal(gen, np.stack(seq, 1))
+    assert np.array_equal(gen[0], gen[3])  # identical prompts, identical rows
+    dev.reset()
+    out = dev.decode(torch.from_numpy(first).cuda(), 0)
+    assert np.array_equal(_np(out).astype(np.int32), gen[:, 0])
+    # a smaller batch on the same decoder
+    dev.reset()
+    out2 = dev.decode(torch.from_numpy(first[:1]).cuda(), 0)
+    assert int(_np(out2)[0]) == gen[0, 0]
+
+
+def test_decode_argument_errors(D):
+    from burnext_amd import _native as N
+    cfg = _cfg(D, n_layers=2, max_seq_len=8)
+    data = D.make_decoder(cfg, seed=1, moe_dtype="f32")
+    dev = D.GptOssDecoder(data, max_batch=2)
+    tok = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(N.BurnextError, match="not the next position"):
+        dev.decode(tok, 3)
+    with pytest.raises(N.BurnextError, match="batch"):
+        dev.decode(torch.zeros(3, dtype=torch.int32, device="cuda"), 0)
+    ws = dev.workspace(2)
+    with pytest.raises(N.BurnextError, match="WORKSPACE_TOO_SMALL"):
+        dev.decode(tok, 0, workspace=ws[:ws.numel() // 2])
+    for p in range(8):
+        dev.decode(tok, p)
+    with pytest.raises(N.BurnextError, match="max_positions"):
+        dev.decode(tok, 8)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_decode_20b_shapes_full_cache(D, oracle, kv_bf16):
+    """GPT-OSS-20B layer shapes (d_model 2880, 64 q / 8 kv heads of 64, 32 experts top-4, 128-row
+    window on the odd layer) with an 8192-row cache loaded to 8190 rows: three steps fill it and
+    evict the oldest row."""
+    cfg = D.GptOssConfig(vocab_size=50001, n_layers=2, kv_bf16=kv_bf16, max_seq_len=16384)
+    data = D.make_decoder(cfg, seed=21, sinks_std=0.8, norm_std=0.1)
+    B, pre = 8, cfg.cache_len - 2
+    rng = np.random.default_rng(5)
+    shape = (cfg.n_layers, B, pre, cfg.kv_heads, cfg.head_dim)
+    k = (rng.standard_normal(shape, dtype=np.float32) * 0.6).astype(np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32).astype(np.float32)
+    print(f"[decoder] 20b shapes kv_bf16={kv_bf16}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    dev.cache_load(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    orc = oracle.DecoderOracle(data, B)
+    if kv_bf16:
+        from burnext_amd.synth import round_bf16
+        orc.load(round_bf16(k).reshape(shape), round_bf16(v).reshape(shape))
+    else:
+        orc.load(k, v)
+    del k, v
+    tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
+    tol = TOL_BF16 if kv_bf16 else TOL_F32
+    for pos in range(pre, pre + 3):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        _check_step(oracle, tol, nxt, lg, hid, o_nxt, o_lg, o_hid, pos)
+        tok = o_nxt
+    dev.close()
