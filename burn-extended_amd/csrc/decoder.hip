@@ -91,15 +91,30 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Cache layouts of one layer (cap_p = cache_len rounded up to 64 rows).
+// K: [maxB][kvH][cap_p / 64][dk / 4][64 rows][4]: the 4-wide dimension quads of 64 consecutive
+//    slots are contiguous, so the score phase (one lane per key) reads 16 bytes per lane with
+//    consecutive lanes on consecutive addresses.
+// V: [maxB][kvH][cap_p][dk] row-major (the value phase reads rows with lanes along dk).
+__host__ __device__ __forceinline__ size_t k_index(uint32_t b, uint32_t g, uint32_t slot, uint32_t d, uint32_t kvH,
+                                                   uint32_t cap_p, uint32_t dk) {
+  return ((((size_t)b * kvH + g) * (cap_p / 64u) + slot / 64u) * (dk / 4u) + d / 4u) * 256u + (slot % 64u) * 4u +
+         (d % 4u);
+}
+__host__ __device__ __forceinline__ size_t v_index(uint32_t b, uint32_t g, uint32_t slot, uint32_t d, uint32_t kvH,
+                                                   uint32_t cap_p, uint32_t dk) {
+  return (((size_t)b * kvH + g) * cap_p + slot) * dk + d;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Dense decode GEMV.  Weights W [N, K] bf16, repacked at create into tiles of 16 rows x 32
 // inputs (1 KiB): tile t, K-group kg at (t * nkg + kg) KiB, lane l = 16 q + i holding
 // W[16 t + i][32 kg + 8 q .. +8] -- the A operand of v_mfma_f32_16x16x32_bf16 for one K step.
-// Workgroup (x, h): 4 waves, row tiles 4 x .. 4 x + 3, K-groups [h H, (h + 1) H).  The K range of
-// the activations is staged once per workgroup in LDS as two bf16 terms (hi, lo = bf16 of the
-// residual; together f32-accurate to ~2^-17), token rows >= B zero.  Every wave issues all H
-// weight loads of its tile first (16 KiB in flight at H = 16), then 2 MFMAs per K-group.
-// Output: partial sums out[h][b][n] (no bias).
+// Workgroup (x, h): 4 waves, row tiles 4 x .. 4 x + 3, K-groups [h H, (h + 1) H).  Every wave
+// first issues all its H weight loads (16 KiB in flight at H = 16); while they are in flight the
+// workgroup stages the B token rows of its K range in LDS as two bf16 terms (hi, lo = bf16 of the
+// residual; together f32-accurate to ~2^-17).  Lanes of token columns >= B feed zeros to the
+// MFMA.  2 MFMAs per K-group.  Output: partial sums out[h][b][n] (no bias).  K % 4 == 0.
 // ---------------------------------------------------------------------------------------------
 struct DenseArgs {
   const uint8_t *w;
@@ -114,26 +129,47 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
   const uint32_t H = a.H, ldk = H * 32u + 8u;  // +8: consecutive token rows start on other banks
   uint16_t *bs = (uint16_t *)smem;             // [2 terms][16 tokens][ldk]
   const uint32_t h = blockIdx.y, kg0 = h * H, kg1 = min(kg0 + H, a.nkg), nk = kg1 - kg0;
-  const uint32_t k0 = kg0 * 32u, kn = nk * 32u;
-  for (uint32_t i = threadIdx.x; i < 16u * kn; i += blockDim.x) {
-    const uint32_t j = i / kn, kk = i - j * kn, k = k0 + kk;
-    const float v = (j < a.B && k < a.K) ? a.x[(size_t)j * a.K + k] : 0.0f;
-    uint16_t t[2];
-    split_bf16<2>(v, t);
-    bs[(size_t)j * ldk + kk] = t[0];
-    bs[(size_t)(16u + j) * ldk + kk] = t[1];
-  }
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t tile = blockIdx.x * 4u + wv;
   const bool tv = tile < a.ntiles;  // wave-uniform
   const uint32_t tl = tv ? tile : a.ntiles - 1u;
+  // activation quads of rows j < B in this K range (at most 16 x 16 x 8 / 256 = 8 per thread),
+  // requested before the weights: the in-order load counter then lets the staging wait for
+  // them alone
+  const uint32_t k0 = kg0 * 32u, kq = nk * 8u;  // quads per row
+  constexpr uint32_t kXq = 16u * kDenseMaxH * 8u / 256u;
+  float4 xv[kXq];
+#pragma unroll
+  for (uint32_t u = 0; u < kXq; ++u) {
+    const uint32_t i = threadIdx.x + u * 256u, j = i / kq, qq = i - j * kq, k = k0 + 4u * qq;
+    xv[u] = (i < a.B * kq && k < a.K) ? *(const float4 *)(a.x + (size_t)j * a.K + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
   uint4 wbuf[kDenseMaxH];
   const uint8_t *wt = a.w + ((size_t)tl * a.nkg + kg0) * 1024u + lane * 16u;
 #pragma unroll
-  for (uint32_t s = 0; s < kDenseMaxH; ++s)
-    if (s < nk) wbuf[s] = *(const uint4 *)(wt + (size_t)s * 1024u);
+  for (uint32_t s = 0; s < kDenseMaxH; ++s)  // unconditional (clamped): a static count of loads in flight
+    wbuf[s] = *(const uint4 *)(wt + (size_t)min(s, nk - 1u) * 1024u);
+#pragma unroll
+  for (uint32_t u = 0; u < kXq; ++u) {
+    const uint32_t i = threadIdx.x + u * 256u, j = i / kq, qq = i - j * kq;
+    if (i >= a.B * kq) continue;
+    const float vv[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+    uint32_t hi[2], lo[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      uint16_t t0[2], t1[2];
+      split_bf16<2>(vv[2 * u], t0);
+      split_bf16<2>(vv[2 * u + 1], t1);
+      hi[u] = (uint32_t)t0[0] | ((uint32_t)t1[0] << 16);
+      lo[u] = (uint32_t)t0[1] | ((uint32_t)t1[1] << 16);
+    }
+    *(uint2 *)(bs + (size_t)j * ldk + 4u * qq) = make_uint2(hi[0], hi[1]);
+    *(uint2 *)(bs + (size_t)(16u + j) * ldk + 4u * qq) = make_uint2(lo[0], lo[1]);
+  }
   __syncthreads();
   const uint32_t i16 = lane & 15u, q = lane >> 4;
+  const bool bok = i16 < a.B;
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (uint32_t s = 0; s < kDenseMaxH; ++s) {
@@ -141,12 +177,12 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
       const bf16x8_t A = __builtin_bit_cast(bf16x8_t, wbuf[s]);
 #pragma unroll
       for (uint32_t term = 0; term < 2u; ++term) {
-        const u32x4_t raw = *(const u32x4_t *)(bs + (size_t)(term * 16u + i16) * ldk + 32u * s + 8u * q);
+        const u32x4_t raw = bok ? *(const u32x4_t *)(bs + (size_t)(term * 16u + i16) * ldk + 32u * s + 8u * q) : zero;
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8_t, raw), acc, 0, 0, 0);
       }
     }
   }
-  if (!tv || i16 >= a.B) return;
+  if (!tv || !bok) return;
   float *o = a.out + (size_t)h * a.part_stride + (size_t)i16 * a.N;
   const uint32_t r0 = tile * 16u + 4u * q;
 #pragma unroll
@@ -159,7 +195,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
 // Sum of the K-part partials plus bias; RoPE for q and k: pair i of head hh at position
 // pos + hh * head_stride rotated by table[p][i] = (cos, sin) x concentration:
 //   y0 = x0 c - x1 s, y1 = x1 c + x0 s   (Burn RotaryEncoding, interleaved pairs)
-// q goes to qbuf [B][nH dk] (f32); k and v to the cache [maxB][kvH][cap][dk] at slot.
+// q goes to qbuf [B][nH dk] (f32); k and v to the cache at slot (k_index / v_index layouts).
 // ---------------------------------------------------------------------------------------------
 struct QkvPostArgs {
   const float *part;  // [parts][B][qd + 2 kd]
@@ -169,7 +205,7 @@ struct QkvPostArgs {
   const float *rope;  // [npos][dk / 2][2]
   float *qbuf;        // [B][nH * dk]
   void *kc, *vc;      // this layer's cache
-  uint32_t B, nH, kvH, dk, cap, slot, pos, head_stride;
+  uint32_t B, nH, kvH, dk, cap_p, slot, pos, head_stride;
 };
 
 template <typename KV>
@@ -195,20 +231,22 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
     if (o < qd) {
       *(float2 *)(a.qbuf + (size_t)b * qd + local) = make_float2(y0, y1);
     } else {
-      kv_store2(kc + (((size_t)b * a.kvH + hh) * a.cap + a.slot) * a.dk + (local - hh * a.dk), y0, y1);
+      kv_store2(kc + k_index(b, hh, a.slot, local - hh * a.dk, a.kvH, a.cap_p, a.dk), y0, y1);
     }
   } else {
     const uint32_t local = o - qd - kd, hh = local / a.dk;
-    kv_store2(vc + (((size_t)b * a.kvH + hh) * a.cap + a.slot) * a.dk + (local - hh * a.dk), x0, x1);
+    kv_store2(vc + v_index(b, hh, a.slot, local - hh * a.dk, a.kvH, a.cap_p, a.dk), x0, x1);
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Attention, flash-decoding split.  Workgroup (chunk c, kv head g, batch b) covers positions
 // p = p_lo + 256 c + t (t < 256, p <= p_hi) of the active window [p_lo, p_hi], slot p mod cap,
-// for the `groups` query heads of kv head g.
-//   scores: thread t, s[j] = (q[j] . k[p]) / sqrt(scale_dk) (q broadcast from LDS)
-//   m[j] = chunk maximum, e = exp(s - m) (0 outside the window), l[j] = sum of e
+// for the G query heads of kv head g.
+//   scores: thread t, s[j] = (q[j] . k[p]) / sqrt(scale_dk) (q broadcast from LDS, k in
+//     dimension quads from the tiled K layout)
+//   m[j] = chunk maximum (wave maxima, then the 4 waves), e = exp(s - m) (0 outside the window),
+//   l[j] = sum of e (wave butterflies, then the 4 waves in order)
 //   acc[j][d] = sum of e v: thread (key lane kq = t / 16, dim quad dq = t % 16) takes keys
 //     kq, kq + 16, ... in order, the 4 key lanes of a wave are summed by shuffles and the 4 waves
 //     in order through LDS
@@ -218,7 +256,7 @@ struct AttnArgs {
   const float *q;        // [B][nH * dk]
   const void *kc, *vc;   // this layer's cache
   float *part;           // [B][kvH][nchunk][groups][dk + 2]
-  uint32_t nH, kvH, dk, cap, p_lo, p_hi, nchunk;
+  uint32_t nH, kvH, dk, cap, cap_p, p_lo, p_hi, nchunk;
   float inv_scale;       // 1 / sqrt(scale_dk)
 };
 
@@ -226,37 +264,38 @@ template <typename KV, uint32_t G>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
   __shared__ __align__(16) float q_l[kMaxGroups * kMaxHeadDim];   // 8 KiB
   __shared__ float e_l[kAttnChunk * kMaxGroups];                  // 16 KiB: e[key][j]
-  __shared__ float m_l[4 * kMaxGroups];
+  __shared__ float m_l[4 * kMaxGroups], l_l[4 * kMaxGroups];
   __shared__ __align__(16) float acc_l[4 * kMaxGroups * 16 * 4];  // [wave][j][dq][4]: 16 KiB
   const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  constexpr uint32_t groups = G;
-  const uint32_t dk = a.dk, t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  const uint32_t dk = a.dk, nq = dk / 4u, t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const KV *kc = (const KV *)a.kc, *vc = (const KV *)a.vc;
-  for (uint32_t i = t; i < groups * dk; i += blockDim.x)
-    q_l[i] = a.q[(size_t)b * a.nH * dk + (size_t)g * groups * dk + i];
+  for (uint32_t i = t; i < G * dk; i += blockDim.x) q_l[i] = a.q[(size_t)b * a.nH * dk + (size_t)g * G * dk + i];
   __syncthreads();
-  const size_t head_base = ((size_t)b * a.kvH + g) * a.cap;
   const uint32_t p0 = a.p_lo + c * kAttnChunk, p = p0 + t;
   const bool valid = p <= a.p_hi;
   float s[G];
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) s[j] = 0.0f;
-  if (valid) {
-    const KV *kr = kc + (head_base + p % a.cap) * dk;
-    for (uint32_t d0 = 0; d0 < dk; d0 += 8u) {
-      float kv[8];
-      kv_load8(kr + d0, kv);
+  {
+    // dimension quads in batches of 8 loads in flight (quads past dk and keys outside the window
+    // read a valid slot and are not used)
+    const KV *kr = kc + k_index(b, g, valid ? p % a.cap : 0u, 0u, a.kvH, a.cap_p, dk);
+    for (uint32_t q0 = 0; q0 < nq; q0 += 8u) {
+      float kv[8][4];
 #pragma unroll
-      for (uint32_t j = 0; j < G; ++j) {
-        const float4 qa = *(const float4 *)(q_l + j * dk + d0), qb = *(const float4 *)(q_l + j * dk + d0 + 4u);
-        s[j] = fmaf(qa.x, kv[0], s[j]);
-        s[j] = fmaf(qa.y, kv[1], s[j]);
-        s[j] = fmaf(qa.z, kv[2], s[j]);
-        s[j] = fmaf(qa.w, kv[3], s[j]);
-        s[j] = fmaf(qb.x, kv[4], s[j]);
-        s[j] = fmaf(qb.y, kv[5], s[j]);
-        s[j] = fmaf(qb.z, kv[6], s[j]);
-        s[j] = fmaf(qb.w, kv[7], s[j]);
+      for (uint32_t u = 0; u < 8u; ++u) kv_load4(kr + (size_t)min(q0 + u, nq - 1u) * 256u, kv[u]);
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        if (q0 + u < nq) {
+#pragma unroll
+          for (uint32_t j = 0; j < G; ++j) {
+            const float4 qa = *(const float4 *)(q_l + j * dk + 4u * (q0 + u));
+            s[j] = fmaf(qa.x, kv[u][0], s[j]);
+            s[j] = fmaf(qa.y, kv[u][1], s[j]);
+            s[j] = fmaf(qa.z, kv[u][2], s[j]);
+            s[j] = fmaf(qa.w, kv[u][3], s[j]);
+          }
+        }
       }
     }
   }
@@ -270,28 +309,42 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) {
     const float m = fmaxf(fmaxf(m_l[j], m_l[kMaxGroups + j]), fmaxf(m_l[2u * kMaxGroups + j], m_l[3u * kMaxGroups + j]));
-    e_l[t * groups + j] = valid ? expf(s[j] - m) : 0.0f;
+    const float e = valid ? expf(s[j] - m) : 0.0f;
+    e_l[t * G + j] = e;
+    const float lw = wave_sum_butterfly(e);
+    if (lane == 0) l_l[w * kMaxGroups + j] = lw;
   }
   __syncthreads();
-  const uint32_t kq = t >> 4, dq = t & 15u, nq = dk / 4u;
+  const uint32_t kq = t >> 4, dq = t & 15u;
   const uint32_t nkeys = min(kAttnChunk, a.p_hi + 1u - p0);
-  float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)groups * (dk + 2u);
+  float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)G * (dk + 2u);
   for (uint32_t dbase = 0; dbase < nq; dbase += 16u) {
     const uint32_t dqq = dbase + dq;
     float acc[G][4];
 #pragma unroll
     for (uint32_t j = 0; j < G; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
     if (dqq < nq) {
-      for (uint32_t key = kq; key < nkeys; key += 16u) {
-        float v[4];
-        kv_load4(vc + (head_base + (p0 + key) % a.cap) * dk + 4u * dqq, v);
+      // keys kq + 16 i in batches of 4 loads in flight (past the chunk: a valid row, weight 0)
+      for (uint32_t k0 = kq; k0 < nkeys; k0 += 64u) {
+        float v[4][4];
 #pragma unroll
-        for (uint32_t j = 0; j < G; ++j) {
-          const float e = e_l[key * groups + j];
-          acc[j][0] = fmaf(e, v[0], acc[j][0]);
-          acc[j][1] = fmaf(e, v[1], acc[j][1]);
-          acc[j][2] = fmaf(e, v[2], acc[j][2]);
-          acc[j][3] = fmaf(e, v[3], acc[j][3]);
+        for (uint32_t u = 0; u < 4u; ++u) {
+          const uint32_t key = min(k0 + 16u * u, nkeys - 1u);
+          kv_load4(vc + v_index(b, g, (p0 + key) % a.cap, 4u * dqq, a.kvH, a.cap_p, dk), v[u]);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) {
+          const uint32_t key = k0 + 16u * u;
+          if (key < nkeys) {
+#pragma unroll
+            for (uint32_t j = 0; j < G; ++j) {
+              const float e = e_l[key * G + j];
+              acc[j][0] = fmaf(e, v[u][0], acc[j][0]);
+              acc[j][1] = fmaf(e, v[u][1], acc[j][1]);
+              acc[j][2] = fmaf(e, v[u][2], acc[j][2]);
+              acc[j][3] = fmaf(e, v[u][3], acc[j][3]);
+            }
+          }
         }
       }
     }
@@ -307,12 +360,11 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
     if (dbase != 0) __syncthreads();  // the previous pass has read acc_l
     if (lane < 16u) {
 #pragma unroll
-      for (uint32_t j = 0; j < G; ++j) {
+      for (uint32_t j = 0; j < G; ++j)
         *(float4 *)(acc_l + ((w * kMaxGroups + j) * 16u + dq) * 4u) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
-      }
     }
     __syncthreads();
-    for (uint32_t i = t; i < groups * 16u; i += blockDim.x) {
+    for (uint32_t i = t; i < G * 16u; i += blockDim.x) {
       const uint32_t j = i >> 4, dd = i & 15u;
       if (dbase + dd >= nq) continue;
       float4 r = *(const float4 *)(acc_l + (j * 16u + dd) * 4u);
@@ -328,17 +380,18 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
       dst[3] = r.w;
     }
   }
-  if (t < groups) {
-    float l = 0.0f;
-    for (uint32_t key = 0; key < nkeys; ++key) l = l + e_l[key * groups + t];
+  if (t < G) {
     out[(size_t)t * (dk + 2u)] =
         fmaxf(fmaxf(m_l[t], m_l[kMaxGroups + t]), fmaxf(m_l[2u * kMaxGroups + t], m_l[3u * kMaxGroups + t]));
-    out[(size_t)t * (dk + 2u) + 1u] = l;
+    out[(size_t)t * (dk + 2u) + 1u] = (l_l[t] + l_l[kMaxGroups + t]) + (l_l[2u * kMaxGroups + t] + l_l[3u * kMaxGroups + t]);
   }
 }
 
-// Chunks merged per (head, dim) with the sink (src/attention/core.rs:34-55): M = max(sink, max_c
-// m_c), L = exp(sink - M) + sum_c l_c exp(m_c - M), ctx = sum_c acc_c exp(m_c - M) / L.
+// Chunks merged with the sink (src/attention/core.rs:34-55): per head j, M = max(sink, max_c m_c),
+// f_c = exp(m_c - M), L = exp(sink - M) + sum_c l_c f_c; ctx[d] = sum_c acc_c[d] f_c / L.
+// Workgroup (kv head g, batch b): wave w takes heads w, w + 4, ... with lanes over chunks (wave
+// max / butterfly sums, chunks lane-strided in order), f in LDS; then threads over (head, dim
+// pair) sum the chunks in order.  Dynamic LDS: (nchunk * groups + groups) floats.
 struct CombineAttnArgs {
   const float *part;   // [B][kvH][nchunk][groups][dk + 2]
   const float *sinks;  // [nH] or null
@@ -347,21 +400,40 @@ struct CombineAttnArgs {
 };
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(CombineAttnArgs a) {
-  const uint32_t g = blockIdx.x, b = blockIdx.y, groups = a.nH / a.kvH, dk = a.dk;
-  const float *base = a.part + ((size_t)b * a.kvH + g) * a.nchunk * (size_t)groups * (dk + 2u);
-  for (uint32_t i = threadIdx.x; i < groups * dk; i += blockDim.x) {
-    const uint32_t j = i / dk, d = i - j * dk, h = g * groups + j;
-    const float sink = a.sinks ? a.sinks[h] : -INFINITY;
+  extern __shared__ float cl[];  // f[nchunk][groups], then 1/L[groups]
+  const uint32_t g = blockIdx.x, b = blockIdx.y, groups = a.nH / a.kvH, dk = a.dk, rec = dk + 2u;
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6, nc = a.nchunk;
+  const float *base = a.part + ((size_t)b * a.kvH + g) * nc * (size_t)groups * rec;
+  float *rinv = cl + (size_t)nc * groups;
+  for (uint32_t j = w; j < groups; j += 4u) {
+    const float sink = a.sinks ? a.sinks[g * groups + j] : -INFINITY;
     float M = sink;
-    for (uint32_t c = 0; c < a.nchunk; ++c) M = fmaxf(M, base[((size_t)c * groups + j) * (dk + 2u)]);
-    float L = a.sinks ? expf(sink - M) : 0.0f, acc = 0.0f;
-    for (uint32_t c = 0; c < a.nchunk; ++c) {
-      const float *pc = base + ((size_t)c * groups + j) * (dk + 2u);
+    for (uint32_t c = lane; c < nc; c += 64u) M = fmaxf(M, base[((size_t)c * groups + j) * rec]);
+    M = wave_max(M);
+    float L = 0.0f;
+    for (uint32_t c = lane; c < nc; c += 64u) {
+      const float *pc = base + ((size_t)c * groups + j) * rec;
       const float f = expf(pc[0] - M);
+      cl[c * groups + j] = f;
       L = L + pc[1] * f;
-      acc = acc + pc[2u + d] * f;
     }
-    a.ctx[(size_t)b * a.nH * dk + (size_t)h * dk + d] = acc / L;
+    L = wave_sum_butterfly(L);
+    if (lane == 0) rinv[j] = 1.0f / (L + (a.sinks ? expf(sink - M) : 0.0f));
+  }
+  __syncthreads();
+  const uint32_t half = dk / 2u;
+  for (uint32_t i = t; i < groups * half; i += blockDim.x) {
+    const uint32_t j = i / half, d = 2u * (i - j * half);
+    float ax = 0.0f, ay = 0.0f;
+#pragma unroll 8
+    for (uint32_t c = 0; c < nc; ++c) {
+      const float f = cl[c * groups + j];
+      const float2 v = *(const float2 *)(base + ((size_t)c * groups + j) * rec + 2u + d);
+      ax = fmaf(v.x, f, ax);
+      ay = fmaf(v.y, f, ay);
+    }
+    const float r = rinv[j];
+    *(float2 *)(a.ctx + (size_t)b * a.nH * dk + (size_t)(g * groups + j) * dk + d) = make_float2(ax * r, ay * r);
   }
 }
 
@@ -381,7 +453,8 @@ __global__ __launch_bounds__(256) void o_post_kernel(OPostArgs a) {
   a.hidden[(size_t)b * a.N + n] = a.hidden[(size_t)b * a.N + n] + (s + a.bias[n]);
 }
 
-// y[b] = x[b] / sqrt(mean(x[b]^2) + eps) * gamma (Burn RmsNorm); one workgroup per row.
+// y[b] = x[b] / sqrt(mean(x[b]^2) + eps) * gamma (Burn RmsNorm); one workgroup per row, D % 4 == 0.
+// Rows of up to 4096 values stay in registers between the two passes.
 struct NormArgs {
   const float *x;
   const float *gamma;
@@ -391,16 +464,49 @@ struct NormArgs {
 };
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   __shared__ float red[4];
-  const uint32_t b = blockIdx.x, t = threadIdx.x;
-  const float *x = a.x + (size_t)b * a.D;
+  constexpr uint32_t kR = 4;
+  const uint32_t b = blockIdx.x, t = threadIdx.x, nq = a.D / 4u;
+  const float4 *x4 = (const float4 *)(a.x + (size_t)b * a.D);
+  float4 v[kR];
   float ss = 0.0f;
-  for (uint32_t c = t; c < a.D; c += blockDim.x) ss = fmaf(x[c], x[c], ss);
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    const uint32_t i = t + r * 256u;
+    v[r] = i < nq ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    ss = fmaf(v[r].x, v[r].x, ss);
+    ss = fmaf(v[r].y, v[r].y, ss);
+    ss = fmaf(v[r].z, v[r].z, ss);
+    ss = fmaf(v[r].w, v[r].w, ss);
+  }
+  for (uint32_t i = t + kR * 256u; i < nq; i += 256u) {
+    const float4 u = x4[i];
+    ss = fmaf(u.x, u.x, ss);
+    ss = fmaf(u.y, u.y, ss);
+    ss = fmaf(u.z, u.z, ss);
+    ss = fmaf(u.w, u.w, ss);
+  }
   ss = wave_sum_butterfly(ss);
   if ((t & 63u) == 0) red[t >> 6] = ss;
   __syncthreads();
   const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  const float r = sqrtf(tot / (float)a.D + a.eps);
-  for (uint32_t c = t; c < a.D; c += blockDim.x) a.y[(size_t)b * a.D + c] = (x[c] / r) * a.gamma[c];
+  const float rr = sqrtf(tot / (float)a.D + a.eps);
+  const float4 *g4 = (const float4 *)a.gamma;
+  float4 *y4 = (float4 *)(a.y + (size_t)b * a.D);
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    const uint32_t i = t + r * 256u;
+    if (i < nq) {
+      const float4 gg = g4[i];
+      y4[i] = make_float4((v[r].x / rr) * gg.x, (v[r].y / rr) * gg.y, (v[r].z / rr) * gg.z, (v[r].w / rr) * gg.w);
+    }
+  }
+  for (uint32_t i = t + kR * 256u; i < nq; i += 256u) {
+    const float4 u = x4[i], gg = g4[i];
+    y4[i] = make_float4((u.x / rr) * gg.x, (u.y / rr) * gg.y, (u.z / rr) * gg.z, (u.w / rr) * gg.w);
+  }
 }
 
 // hidden[b] = tok_emb[token[b]]; a token outside [0, V) reads row 0 (the caller keeps tokens in
@@ -495,11 +601,11 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
   if (t == 0) a.next[b] = bi;
 }
 
-// f32 rows [B][len][kvH][dk] of one layer -> cache slots [maxB][kvH][cap][dk].
+// f32 rows [B][len][kvH][dk] of one layer -> cache slots 0 .. len-1 (k_index or v_index layout).
 struct CacheLoadArgs {
   const float *src;
   void *dst;
-  uint32_t B, len, kvH, dk, cap;
+  uint32_t B, len, kvH, dk, cap_p, is_k;
 };
 template <typename KV>
 __global__ __launch_bounds__(256) void cache_load_kernel(CacheLoadArgs a) {
@@ -511,7 +617,8 @@ __global__ __launch_bounds__(256) void cache_load_kernel(CacheLoadArgs a) {
     const uint32_t hh = (uint32_t)(r % a.kvH);
     r /= a.kvH;
     const uint32_t p = (uint32_t)(r % a.len), b = (uint32_t)(r / a.len);
-    kv_store1(dst + (((size_t)b * a.kvH + hh) * a.cap + p) * a.dk + d, a.src[i]);
+    const size_t o = a.is_k ? k_index(b, hh, p, d, a.kvH, a.cap_p, a.dk) : v_index(b, hh, p, d, a.kvH, a.cap_p, a.dk);
+    kv_store1(dst + o, a.src[i]);
   }
 }
 
@@ -569,8 +676,9 @@ struct burnext_gptoss {
   DenseMat lm;
   std::vector<DenseMat> qkv, wo;
   float *bqkv = nullptr, *bo = nullptr, *norm_attn = nullptr, *norm_final = nullptr, *sinks = nullptr, *rope = nullptr;
-  uint8_t *kc = nullptr, *vc = nullptr;  // [L][maxB][kvH][cap][dk] of the cache element
+  uint8_t *kc = nullptr, *vc = nullptr;  // per layer: k_index / v_index layouts of the cache element
   size_t kv_elem = 4;
+  uint32_t cap_p = 0;        // cache_len rounded up to 64 rows
   uint64_t layer_cache = 0;  // elements per layer
   uint32_t used = 0;         // cache rows held
   uint64_t pos_next = 0;     // positions seen
@@ -757,13 +865,15 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
   if (c.head_dim % 8 || c.head_dim > kMaxHeadDim)
     return set_error(BURNEXT_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 128");
   if (c.max_batch > kMaxBatch) return set_error(BURNEXT_UNSUPPORTED, "max_batch above 16 is not supported");
-  if (c.d_model % 2) return set_error(BURNEXT_UNSUPPORTED, "d_model must be even");
+  if (c.d_model % 4) return set_error(BURNEXT_UNSUPPORTED, "d_model must be a multiple of 4");
   if (c.rope_head_stride > 1 || c.kv_bf16 > 1 || c.full_on_even > 1)
     return set_error(BURNEXT_INVALID_ARG, "rope_head_stride, kv_bf16 and full_on_even must be 0 or 1");
   if (c.window_policy > 2) return set_error(BURNEXT_INVALID_ARG, "window_policy must be 0 (Full), 1 (Fixed) or 2 (EveryOther)");
   if (c.window_policy != 0 && c.window == 0) return set_error(BURNEXT_INVALID_ARG, "window must be positive");
   if (c.cache_len > (1u << 30) || c.max_positions > (1u << 30))
     return set_error(BURNEXT_UNSUPPORTED, "cache_len and max_positions above 2^30 are not supported");
+  if ((c.n_heads % c.kv_heads) == 0 && (cdiv(c.cache_len, kAttnChunk) + 1) * (c.n_heads / c.kv_heads) > 16384)
+    return set_error(BURNEXT_UNSUPPORTED, "cache_len * n_heads / kv_heads above 4M rows (attention combine LDS)");
   if (!(c.scale_dk > 0.0f) || !(c.rms_eps >= 0.0f) || !(c.rope_theta > 1.0f))
     return set_error(BURNEXT_INVALID_ARG, "scale_dk > 0, rope_theta > 1 and rms_eps >= 0 are required");
   std::vector<double> inv;
@@ -793,6 +903,7 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
   M->kd = c.kv_heads * dk;
   M->groups = c.n_heads / c.kv_heads;
   M->kv_elem = c.kv_bf16 ? 2 : 4;
+  M->cap_p = (uint32_t)align_up(c.cache_len, 64);
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) M->num_cus = cus;
   M->moe.assign(moe_layers, moe_layers + c.n_layers);
@@ -860,7 +971,7 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
     st = upload(M, &M->rope, tab.data(), tab.size());
   }
   if (st == BURNEXT_OK) {  // KV cache
-    M->layer_cache = (uint64_t)c.max_batch * c.kv_heads * c.cache_len * dk;
+    M->layer_cache = (uint64_t)c.max_batch * c.kv_heads * M->cap_p * dk;
     const size_t bytes = (size_t)L * M->layer_cache * M->kv_elem;
     st = dev_alloc(M, (void **)&M->kc, bytes);
     if (st == BURNEXT_OK) st = dev_alloc(M, (void **)&M->vc, bytes);
@@ -913,7 +1024,8 @@ burnext_status burnext_gptoss_cache_load(burnext_gptoss_t M, const float *k, con
       a.len = len;
       a.kvH = M->cfg.kv_heads;
       a.dk = M->cfg.head_dim;
-      a.cap = M->cfg.cache_len;
+      a.cap_p = M->cap_p;
+      a.is_k = which == 0 ? 1u : 0u;
       const dim3 grid((uint32_t)std::min<uint64_t>(cdiv(per_layer, 256), 8192));
       const hipError_t e = M->cfg.kv_bf16 ? launch_kernel(cache_load_kernel<uint16_t>, grid, dim3(256), 0, s, a)
                                           : launch_kernel(cache_load_kernel<float>, grid, dim3(256), 0, s, a);
@@ -980,7 +1092,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     qa.nH = c.n_heads;
     qa.kvH = c.kv_heads;
     qa.dk = dk;
-    qa.cap = cap;
+    qa.cap_p = M->cap_p;
     qa.slot = slot;
     qa.pos = pos;
     qa.head_stride = c.rope_head_stride;
@@ -1000,6 +1112,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     aa.kvH = c.kv_heads;
     aa.dk = dk;
     aa.cap = cap;
+    aa.cap_p = M->cap_p;
     aa.p_hi = pos;
     aa.p_lo = pos + 1 - active;
     aa.nchunk = (uint32_t)cdiv(active, kAttnChunk);
@@ -1009,7 +1122,8 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     if (st != BURNEXT_OK) return st;
     CombineAttnArgs ca{attn, M->sinks ? M->sinks + (size_t)l * c.n_heads : nullptr, ctx, c.n_heads, c.kv_heads, dk,
                        aa.nchunk};
-    st = hip_check(launch_kernel(attn_combine_kernel, dim3(c.kv_heads, B), dim3(256), 0, s, ca),
+    st = hip_check(launch_kernel(attn_combine_kernel, dim3(c.kv_heads, B), dim3(256),
+                                 (size_t)(aa.nchunk + 1) * M->groups * 4, s, ca),
                    "attention combine launch");
     if (st == BURNEXT_OK) st = dense_gemv(M->wo[l], ctx, B, part, s);
     if (st != BURNEXT_OK) return st;

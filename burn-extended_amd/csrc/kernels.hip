@@ -1654,13 +1654,13 @@ hipError_t configure_kernels() {
   BX_ATTR((expert_gemv_kernel<1, false, float, 1>));
   BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit>));
   BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplitFew>));
-  BX_ATTR((expert_gemv_kernel<3, true, uint16_t, 1>));
-  BX_ATTR((expert_gemv_kernel<3, true, float, 1>));
-  BX_ATTR((expert_gemv_kernel<3, true, uint16_t, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<3, true, float, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<3, false, float, 1>));
-  BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplit>));
-  BX_ATTR((expert_gemv_kernel<3, false, float, kDownSplitFew>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, 1>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, 1>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, kGateUpSplit>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, kGateUpSplit>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, 1>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplit>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplitFew>));
 #undef BX_ATTR
   return err;
 }
@@ -1793,21 +1793,21 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
       (void)launch_kernel(expert_gemv_kernel<1, true, uint16_t, 1>, g, block, lds, s, a);
     else
       (void)launch_kernel(expert_gemv_kernel<1, true, float, 1>, g, block, lds, s, a);
-  } else if (nt == 3) {
+  } else if (nt == 2) {
     if (split && a.ksplit == kDownSplitFew)
-      (void)launch_kernel(expert_gemv_kernel<3, false, float, kDownSplitFew>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, false, float, kDownSplitFew>, g, block, lds, s, a);
     else if (split)
-      (void)launch_kernel(expert_gemv_kernel<3, false, float, kDownSplit>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, false, float, kDownSplit>, g, block, lds, s, a);
     else if (!gate_up)
-      (void)launch_kernel(expert_gemv_kernel<3, false, float, 1>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, false, float, 1>, g, block, lds, s, a);
     else if (usplit && x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<3, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
     else if (usplit)
-      (void)launch_kernel(expert_gemv_kernel<3, true, float, kGateUpSplit>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, true, float, kGateUpSplit>, g, block, lds, s, a);
     else if (x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<3, true, uint16_t, 1>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, true, uint16_t, 1>, g, block, lds, s, a);
     else
-      (void)launch_kernel(expert_gemv_kernel<3, true, float, 1>, g, block, lds, s, a);
+      (void)launch_kernel(expert_gemv_kernel<2, true, float, 1>, g, block, lds, s, a);
   } else {
     return hipErrorInvalidValue;
   }

@@ -251,7 +251,9 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   const uint64_t max_active = std::min<uint64_t>(L.E, n * L.K);
   c.nrec = (uint32_t)max_active;
   const bool small_segments = n <= 16 || n * L.K <= 4ull * L.E;
-  uint32_t mt = 8;
+  // two-term (f32) activations at decode sizes: 4 rows per pass keep 3 workgroups per CU (8 rows
+  // would leave one; segments beyond 4 tokens are rare there and take a second pass)
+  uint32_t mt = (nt >= 2 && n <= 16) ? 4 : 8;
   if (!small_segments)
     for (mt = 16; mt > 8 && gemv_total_lds_bytes(nt, mt, t.nb, c.nrec) > 80 * 1024; --mt) {
     }
@@ -844,7 +846,8 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext
     if (st != BURNEXT_OK) return st;
     return combine(L, x, y, xb, n, flags, p, s, 1, true);  // bf16 slot rows from the down GEMM
   }
-  const int nt = xb ? 1 : 3;
+  // f32 activations: two bf16 terms (hi + bf16 of the residual, ~2^-17 relative per value)
+  const int nt = xb ? 1 : 2;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread

@@ -34,7 +34,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
 // Split an f32 into NT bf16 terms t0 + t1 + ... (each the rounded residual of the previous).
-// NT = 3 reproduces any normal float to within 2^-24 relative; NT = 1 is plain rounding.
+// NT = 2 keeps ~2^-17 relative, NT = 3 any normal float to within 2^-24; NT = 1 is plain rounding.
 template <int NT>
 __device__ __forceinline__ void split_bf16(float v, uint16_t (&t)[NT]) {
   float r = v;

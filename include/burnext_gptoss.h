@@ -29,13 +29,13 @@ extern "C" {
 /* Mirrors GptOssConfig (src/models/gpt_oss.rs:18-47) for the decode path. */
 typedef struct burnext_gptoss_config {
   uint32_t vocab_size;
-  uint32_t d_model;
+  uint32_t d_model;        /* multiple of 4 */
   uint32_t n_layers;
   uint32_t n_heads;
   uint32_t kv_heads;        /* n_heads / kv_heads a power of two <= 16 */
   uint32_t head_dim;       /* multiple of 8, <= 128 */
   uint32_t max_batch;      /* <= 16 */
-  uint32_t cache_len;      /* rolling KV cache rows per (layer, batch row) */
+  uint32_t cache_len;      /* rolling KV cache rows per (layer, batch row); cache_len * n_heads / kv_heads <= 4M */
   uint32_t window_policy;  /* WindowPolicy (src/cache/mod.rs:7-33): 0 Full, 1 Fixed(window),
                               2 EveryOther { window, full_on_even } */
   uint32_t window;
