@@ -7,8 +7,10 @@ with inputs already resident in HBM.  Several device copies of the layer are rot
 256 MB Infinity Cache cannot serve a step's expert weights from the previous step.
 
 The same run also measures the metric's prefill half (C3: T=4096 with the calibrated Zipf router
-bias) as the `prefill` object, and the GPT-OSS-120B-shaped layer (C4: E=128) at T = 1, 64 and 8192
-as `sweep_120b`.  `--workload NAME` measures one workload alone (profiling runs).
+bias) as the `prefill` object, the GPT-OSS-120B-shaped layer (C4: E=128) at T = 1, 64 and 8192
+as `sweep_120b`, and the full GPT-OSS-20B-shaped decoder decode (C5: 24 layers, batch 8, an
+8192-row KV cache held full, greedy) as `decoder`.  `--workload NAME` measures one workload alone
+(profiling runs).
 
 Prints ONE JSON line: metric/value/unit plus, per workload, a `roofline` object for the dominant
 kernel (algorithmic bytes or FLOPs from the realised routing, divided by that kernel's average
@@ -54,6 +56,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of each CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-120b", action="store_true", help="skip the 120B sweep of the default run")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder leg of the default run")
+    ap.add_argument("--decoder-steps", type=int, default=50, help="timed decode steps of the decoder leg")
+    ap.add_argument("--decoder-only", action="store_true", help="measure the full-decoder leg alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     return ap.parse_args()
@@ -203,6 +208,102 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     return out
 
 
+def measure_decoder(steps, warmup, with_cpu):
+    """C5: the GPT-OSS-20B-shaped decoder (24 layers, d_model 2880, 64 q / 8 kv heads of 64,
+    alternating 128-row window and full layers with learned sinks, YaRN factor 32 base 150000,
+    vocabulary 201088, 32 experts top-4 per MoE layer) decoding batch 8 greedily with its
+    8192-row f32 KV cache held full (loaded with 8191 rows, so every timed step attends over 8192
+    rows in the full layers and evicts the oldest).  One step = one token per batch row through
+    all 24 layers, final norm, LM head and argmax."""
+    import numpy as np
+    import torch
+
+    from burnext_amd import decoder as DEC
+
+    B, pre = 8, 8191
+    cfg = DEC.GptOssConfig(max_seq_len=pre + warmup + steps + 64)
+    t0 = time.perf_counter()
+    data = DEC.make_decoder(cfg, seed=0, sinks_std=0.5)
+    log(f"decoder: weights generated in {time.perf_counter() - t0:.1f} s")
+    dev = DEC.GptOssDecoder(data, max_batch=B)
+    shape = (cfg.n_layers, B, pre, cfg.kv_heads, cfg.head_dim)
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    k = torch.randn(shape, generator=g, device="cuda:0") * 0.6
+    v = torch.randn(shape, generator=g, device="cuda:0")
+    dev.cache_load(k, v)
+    torch.cuda.synchronize()
+    del k, v
+    tok = torch.from_numpy(np.arange(B, dtype=np.int32) * 1009 % cfg.vocab_size).cuda()
+    ws = dev.workspace(B)
+    pos = pre
+    for _ in range(warmup):
+        tok = dev.decode(tok, pos, workspace=ws)
+        pos += 1
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        tok = dev.decode(tok, pos, workspace=ws)
+        pos += 1
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    # algorithmic HBM bytes of one step: dense weights (bf16) and their f32 biases / norms, the
+    # touched experts of every MoE layer (expected count under uniform routing), the cache rows
+    # each layer attends over (k and v, f32) and the new rows, the LM head
+    D, L, V = cfg.d_model, cfg.n_layers, cfg.vocab_size
+    qd, kd = cfg.n_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    touched = cfg.num_experts * (1 - (1 - cfg.experts_per_token / cfg.num_experts) ** B)
+    m = data.moe[0]
+    moe_b = touched * m.expert_bytes() + cfg.num_experts * D * 2 + cfg.num_experts * 2 + 2 * B * D * 4
+    dense_b = ((qd + 2 * kd) * D + D * qd) * 2 + (qd + 2 * kd + D + D) * 4 + cfg.n_heads * 4
+    rows = sum(min(cfg.layer_window(l) or cfg.cache_len, cfg.cache_len) for l in range(L))
+    kv_b = rows * B * kd * 4 * 2 + L * B * kd * 4 * 2
+    step_b = L * (dense_b + moe_b) + kv_b + V * D * 2 + D * 4 + B * D * 2
+    out = {"value": round(B / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+           "config": {"workload": "gpt-oss-20b decoder decode (C5)", "layers": L, "batch": B, "d_model": D,
+                      "heads": cfg.n_heads, "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
+                      "window": f"every other layer {cfg.window} rows (full on even)", "sinks": "learned",
+                      "rope": f"yarn factor {cfg.rope_scaling_factor} base {cfg.rope_theta}",
+                      "kv_cache": f"{cfg.cache_len} rows f32, held full (rolling)", "vocab": V,
+                      "experts": cfg.num_experts, "top_k": cfg.experts_per_token, "sampling": "greedy",
+                      "data": "random-init weights (seed 0), random cache rows, greedy-fed tokens"},
+           "step_algorithmic_bytes": int(step_b),
+           "step_hbm_gbs": round(step_b / (ms * 1e-3) / 1e9, 1),
+           "step_hbm_frac": round(step_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "step_bytes_note": f"expected touched experts {touched:.1f} of {cfg.num_experts} per layer under "
+                              f"uniform routing; cache rows attended per step summed over layers: {rows}"}
+    log(f"decoder: {ms:.3f} ms/step, {out['value']} tokens/s, step {out['step_hbm_gbs']} GB/s")
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline_decoder(data, B, pre)
+    dev.close()
+    return out
+
+
+def cpu_baseline_decoder(data, B, pre):
+    """One decode step of the same decoder on the host cores: the CPU restatement of the
+    reference's decode (oracle/decoder_oracle.c: dense Linear, RoPE, cache roll, sink attention,
+    the MoE layer by oracle/moe_oracle.c), f32, with the same 8191 cached rows per layer."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    O.lib()
+    orc = O.DecoderOracle(data, B)
+    rng = np.random.default_rng(0)
+    for l in range(data.cfg.n_layers):  # cache contents do not change the work
+        orc.k[l, :, :pre] = rng.standard_normal((B, pre, data.cfg.kv_heads, data.cfg.head_dim), np.float32) * 0.6
+        orc.v[l, :, :pre] = rng.standard_normal((B, pre, data.cfg.kv_heads, data.cfg.head_dim), np.float32)
+    orc.used = pre
+    tok = (np.arange(B, dtype=np.int32) * 1009) % data.cfg.vocab_size
+    t0 = time.perf_counter()
+    orc.step(tok, pre)
+    el = time.perf_counter() - t0
+    return {"value": round(B / el, 3), "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"1 decode step (batch {B}, 24 layers, 8192-row cache) in {el:.1f} s "
+                      "(reference decode restated in C, f32)", "cpu": _cpu_model()}
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (profiles/hbm_traffic_<workload>.txt: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a plain
@@ -265,6 +366,10 @@ def main():
     import torch
 
     torch.cuda.set_device(0)
+    if args.decoder_only:
+        res = measure_decoder(args.decoder_steps, 5, not args.no_cpu)
+        print(json.dumps({"decoder": res}), flush=True)
+        return
     head = args.workload or "20b_decode"
     data = make_data(head)
     layers = make_layers(data, args.copies or WORKLOADS[head]["copies"])
@@ -302,6 +407,8 @@ def main():
             for L in layers:
                 L.close()
             del layers
+        if not args.no_decoder:
+            out["decoder"] = measure_decoder(args.decoder_steps, 5, not args.no_cpu)
     print(json.dumps(out), flush=True)
 
 
