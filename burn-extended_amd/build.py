@@ -39,6 +39,38 @@ def build(verbose: bool = False) -> pathlib.Path:
     return LIB
 
 
+# Host-side sanitizers for build_asan: every -fsanitize option is given to the host half of the
+# compile only (device code is built as for the library).
+ASAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-Xarch_host",
+             "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+ASAN_DIR = LIB_DIR / "asan"
+ASAN_EXE = ASAN_DIR / "asan_host"
+ASAN_DRIVER = PKG.parent / "tests" / "native" / "asan_host.cpp"
+
+
+def build_asan(verbose: bool = False, force: bool = False) -> pathlib.Path:
+    """The library sources with AddressSanitizer + UndefinedBehaviorSanitizer on the host code, linked
+    into the driver tests/native/asan_host.cpp (lib/asan/asan_host).  Skipped when the executable is
+    newer than every source unless `force`."""
+    srcs = [CSRC / f for f in SOURCES] + [ASAN_DRIVER]
+    deps = srcs + list(CSRC.glob("*.hpp")) + list((PKG.parent / "include").glob("*.h"))
+    if not force and ASAN_EXE.exists() and ASAN_EXE.stat().st_mtime > max(d.stat().st_mtime for d in deps):
+        return ASAN_EXE
+    ASAN_DIR.mkdir(parents=True, exist_ok=True)
+    objs = [str(ASAN_DIR / (pathlib.Path(f).stem + ".o")) for f in srcs]
+    inc = ["-I", str(PKG.parent / "include")]
+    cmds = [[HIPCC, *FLAGS, *ASAN_HOST, *inc, "-c", str(src), "-o", obj] for src, obj in zip(srcs, objs)]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = ASAN_EXE.with_suffix(".tmp")
+    _run([HIPCC, "--offload-arch=gfx950", *ASAN_HOST, "-o", str(tmp), *objs, "-lpthread"], verbose)
+    shutil.move(str(tmp), str(ASAN_EXE))
+    for o in objs:
+        os.remove(o)
+    return ASAN_EXE
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -638,11 +638,16 @@ struct DenseMat {
   uint32_t N = 0, K = 0, nkg = 0, ntiles = 0, H = 0, parts = 0;
 };
 
+// Tiles and K-groups of an [N, K] matrix.
+void dense_geometry(DenseMat &m) {
+  m.nkg = (uint32_t)cdiv(m.K, 32);
+  m.ntiles = (uint32_t)cdiv(m.N, 16);
+}
+
 // K-groups per work unit: the largest H <= kDenseMaxH (halving, down to 4) that still gives at
 // least 8 waves per CU.
 void dense_plan(DenseMat &m, int num_cus) {
-  m.nkg = (uint32_t)cdiv(m.K, 32);
-  m.ntiles = (uint32_t)cdiv(m.N, 16);
+  dense_geometry(m);
   uint32_t H = kDenseMaxH;
   while (H > 4 && (uint64_t)m.ntiles * cdiv(m.nkg, H) < 8ull * (uint64_t)num_cus) H >>= 1;
   m.H = std::min<uint32_t>(H, m.nkg);
@@ -882,6 +887,63 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
     return set_error(BURNEXT_INVALID_ARG, "YaRN thresholds out of range (the reference asserts 0 < low < high < d - 1)");
   for (uint32_t l = 0; l < c.n_layers; ++l)
     if (!moe_layers[l]) return set_error(BURNEXT_INVALID_ARG, "null MoE layer handle");
+
+  // host preparation (no device call): tiled projections, f32 biases / norms / sinks, RoPE table
+  const uint32_t dk = c.head_dim, half = dk / 2, qd = c.n_heads * dk, kd = c.kv_heads * dk;
+  const uint32_t D = c.d_model, L = c.n_layers, V = c.vocab_size, N3 = qd + 2 * kd;
+  DenseMat lm;
+  std::vector<DenseMat> qkv(L), wo(L);
+  std::vector<std::vector<uint16_t>> qkv_t(L), wo_t(L);
+  std::vector<uint16_t> lm_t;
+  std::vector<float> bq((size_t)L * N3), bo((size_t)L * D), na((size_t)L * D), nf(D), sk, tab;
+  try {
+    lm.N = V;
+    lm.K = D;
+    dense_geometry(lm);
+    lm_t = dense_tile(w->lm_head, V, D, lm);
+    std::vector<uint16_t> fused((size_t)N3 * D);
+    for (uint32_t l = 0; l < L; ++l) {
+      memcpy(fused.data(), w->wq + (size_t)l * qd * D, (size_t)qd * D * 2);
+      memcpy(fused.data() + (size_t)qd * D, w->wk + (size_t)l * kd * D, (size_t)kd * D * 2);
+      memcpy(fused.data() + (size_t)(qd + kd) * D, w->wv + (size_t)l * kd * D, (size_t)kd * D * 2);
+      qkv[l].N = N3;
+      qkv[l].K = D;
+      dense_geometry(qkv[l]);
+      qkv_t[l] = dense_tile(fused.data(), N3, D, qkv[l]);
+      wo[l].N = D;
+      wo[l].K = qd;
+      dense_geometry(wo[l]);
+      wo_t[l] = dense_tile(w->wo + (size_t)l * D * qd, D, qd, wo[l]);
+    }
+    for (uint32_t l = 0; l < L; ++l) {
+      for (uint32_t i = 0; i < qd; ++i) bq[(size_t)l * N3 + i] = bf16h(w->bq[(size_t)l * qd + i]);
+      for (uint32_t i = 0; i < kd; ++i) {
+        bq[(size_t)l * N3 + qd + i] = bf16h(w->bk[(size_t)l * kd + i]);
+        bq[(size_t)l * N3 + qd + kd + i] = bf16h(w->bv[(size_t)l * kd + i]);
+      }
+      for (uint32_t i = 0; i < D; ++i) {
+        bo[(size_t)l * D + i] = bf16h(w->bo[(size_t)l * D + i]);
+        na[(size_t)l * D + i] = bf16h(w->norm_attn[(size_t)l * D + i]);
+      }
+    }
+    for (uint32_t i = 0; i < D; ++i) nf[i] = bf16h(w->norm_final[i]);
+    if (w->sinks) {
+      sk.resize((size_t)L * c.n_heads);
+      for (size_t i = 0; i < sk.size(); ++i) sk[i] = bf16h(w->sinks[i]);
+    }
+    // RoPE table [max_positions + nH][dk/2][2] = (cos, sin) x concentration
+    const uint64_t npos = (uint64_t)c.max_positions + c.n_heads;
+    tab.resize(npos * half * 2);
+    for (uint64_t p = 0; p < npos; ++p)
+      for (uint32_t i = 0; i < half; ++i) {
+        const float ang = (float)p * (float)inv[i];  // one f32 product, as the reference's f32 table
+        tab[(p * half + i) * 2] = (float)(std::cos((double)ang) * conc);
+        tab[(p * half + i) * 2 + 1] = (float)(std::sin((double)ang) * conc);
+      }
+  } catch (const std::bad_alloc &) {
+    return set_error(BURNEXT_OUT_OF_MEMORY, "host allocation failed while preparing the decoder weights");
+  }
+
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
     return set_error(BURNEXT_INVALID_ARG, "device index out of range (or no HIP device)");
@@ -898,78 +960,36 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
   if (!M) return set_error(BURNEXT_OUT_OF_MEMORY, "host allocation failed");
   M->device = device;
   M->cfg = c;
-  const uint32_t dk = c.head_dim, half = dk / 2;
-  M->qd = c.n_heads * dk;
-  M->kd = c.kv_heads * dk;
+  M->qd = qd;
+  M->kd = kd;
   M->groups = c.n_heads / c.kv_heads;
   M->kv_elem = c.kv_bf16 ? 2 : 4;
   M->cap_p = (uint32_t)align_up(c.cache_len, 64);
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) M->num_cus = cus;
   M->moe.assign(moe_layers, moe_layers + c.n_layers);
-  const uint32_t D = c.d_model, L = c.n_layers, V = c.vocab_size, N3 = M->qd + 2 * M->kd;
   burnext_status st = upload(M, &M->emb, w->tok_emb, (size_t)V * D);
-  auto up_dense = [&](DenseMat &m, const uint16_t *src) -> burnext_status {
+  auto up_dense = [&](DenseMat &m, const DenseMat &geom, const std::vector<uint16_t> &t) -> burnext_status {
+    m = geom;
     dense_plan(m, M->num_cus);
-    const std::vector<uint16_t> t = dense_tile(src, m.N, m.K, m);
     uint16_t *p = nullptr;
     const burnext_status s2 = upload(M, &p, t.data(), t.size());
     m.w = (uint8_t *)p;
     return s2;
   };
-  M->lm.N = V;
-  M->lm.K = D;
-  if (st == BURNEXT_OK) st = up_dense(M->lm, w->lm_head);
+  if (st == BURNEXT_OK) st = up_dense(M->lm, lm, lm_t);
   M->qkv.resize(L);
   M->wo.resize(L);
-  std::vector<uint16_t> fused((size_t)N3 * D);
   for (uint32_t l = 0; l < L && st == BURNEXT_OK; ++l) {
-    memcpy(fused.data(), w->wq + (size_t)l * M->qd * D, (size_t)M->qd * D * 2);
-    memcpy(fused.data() + (size_t)M->qd * D, w->wk + (size_t)l * M->kd * D, (size_t)M->kd * D * 2);
-    memcpy(fused.data() + (size_t)(M->qd + M->kd) * D, w->wv + (size_t)l * M->kd * D, (size_t)M->kd * D * 2);
-    M->qkv[l].N = N3;
-    M->qkv[l].K = D;
-    st = up_dense(M->qkv[l], fused.data());
-    if (st != BURNEXT_OK) break;
-    M->wo[l].N = D;
-    M->wo[l].K = M->qd;
-    st = up_dense(M->wo[l], w->wo + (size_t)l * D * M->qd);
+    st = up_dense(M->qkv[l], qkv[l], qkv_t[l]);
+    if (st == BURNEXT_OK) st = up_dense(M->wo[l], wo[l], wo_t[l]);
   }
-  if (st == BURNEXT_OK) {
-    std::vector<float> bq((size_t)L * N3), bo((size_t)L * D), na((size_t)L * D), nf(D), sk;
-    for (uint32_t l = 0; l < L; ++l) {
-      for (uint32_t i = 0; i < M->qd; ++i) bq[(size_t)l * N3 + i] = bf16h(w->bq[(size_t)l * M->qd + i]);
-      for (uint32_t i = 0; i < M->kd; ++i) {
-        bq[(size_t)l * N3 + M->qd + i] = bf16h(w->bk[(size_t)l * M->kd + i]);
-        bq[(size_t)l * N3 + M->qd + M->kd + i] = bf16h(w->bv[(size_t)l * M->kd + i]);
-      }
-      for (uint32_t i = 0; i < D; ++i) {
-        bo[(size_t)l * D + i] = bf16h(w->bo[(size_t)l * D + i]);
-        na[(size_t)l * D + i] = bf16h(w->norm_attn[(size_t)l * D + i]);
-      }
-    }
-    for (uint32_t i = 0; i < D; ++i) nf[i] = bf16h(w->norm_final[i]);
-    st = upload(M, &M->bqkv, bq.data(), bq.size());
-    if (st == BURNEXT_OK) st = upload(M, &M->bo, bo.data(), bo.size());
-    if (st == BURNEXT_OK) st = upload(M, &M->norm_attn, na.data(), na.size());
-    if (st == BURNEXT_OK) st = upload(M, &M->norm_final, nf.data(), nf.size());
-    if (st == BURNEXT_OK && w->sinks) {
-      sk.resize((size_t)L * c.n_heads);
-      for (size_t i = 0; i < sk.size(); ++i) sk[i] = bf16h(w->sinks[i]);
-      st = upload(M, &M->sinks, sk.data(), sk.size());
-    }
-  }
-  if (st == BURNEXT_OK) {  // RoPE table [max_positions + nH][dk/2][2] = (cos, sin) x concentration
-    const uint64_t npos = (uint64_t)c.max_positions + c.n_heads;
-    std::vector<float> tab(npos * half * 2);
-    for (uint64_t p = 0; p < npos; ++p)
-      for (uint32_t i = 0; i < half; ++i) {
-        const float ang = (float)p * (float)inv[i];  // one f32 product, as the reference's f32 table
-        tab[(p * half + i) * 2] = (float)(std::cos((double)ang) * conc);
-        tab[(p * half + i) * 2 + 1] = (float)(std::sin((double)ang) * conc);
-      }
-    st = upload(M, &M->rope, tab.data(), tab.size());
-  }
+  if (st == BURNEXT_OK) st = upload(M, &M->bqkv, bq.data(), bq.size());
+  if (st == BURNEXT_OK) st = upload(M, &M->bo, bo.data(), bo.size());
+  if (st == BURNEXT_OK) st = upload(M, &M->norm_attn, na.data(), na.size());
+  if (st == BURNEXT_OK) st = upload(M, &M->norm_final, nf.data(), nf.size());
+  if (st == BURNEXT_OK && w->sinks) st = upload(M, &M->sinks, sk.data(), sk.size());
+  if (st == BURNEXT_OK) st = upload(M, &M->rope, tab.data(), tab.size());
   if (st == BURNEXT_OK) {  // KV cache
     M->layer_cache = (uint64_t)c.max_batch * c.kv_heads * M->cap_p * dk;
     const size_t bytes = (size_t)L * M->layer_cache * M->kv_elem;

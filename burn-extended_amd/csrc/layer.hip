@@ -153,9 +153,11 @@ void repack_expert(const uint8_t *src_b, const uint8_t *src_s, uint64_t bpr, uin
   }
 }
 
-burnext_status upload_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols, const uint8_t *blocks,
+// Host half of the upload: geometry of t and the repacked bytes of all E experts (no device call,
+// so create can prepare everything before it touches the GPU).
+burnext_status repack_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols, const uint8_t *blocks,
                             const uint8_t *scales, const burnext_mxfp4_desc &d, bool is_w1, uint32_t F,
-                            burnext_gate_up_layout layout) {
+                            burnext_gate_up_layout layout, std::vector<uint8_t> &hb, std::vector<uint8_t> &hs) {
   t.rows = rows;
   t.rows_p = (uint32_t)align_up(rows, 16);
   t.cols = cols;
@@ -163,7 +165,6 @@ burnext_status upload_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols
   t.nrt = t.rows_p / 16;
   t.blocks_per_expert = (uint64_t)t.rows_p * t.nb * 16;
   t.scales_per_expert = (uint64_t)t.rows_p * t.nb;
-  std::vector<uint8_t> hb, hs;
   try {
     hb.resize(t.blocks_per_expert * E);
     hs.resize(t.scales_per_expert * E);
@@ -182,6 +183,10 @@ burnext_status upload_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols
     });
   }
   for (auto &th : pool) th.join();
+  return BURNEXT_OK;
+}
+
+burnext_status upload_tiled(TiledMx &t, const std::vector<uint8_t> &hb, const std::vector<uint8_t> &hs) {
   if (hipMalloc(&t.blocks, hb.size()) != hipSuccess || hipMalloc(&t.scales, hs.size()) != hipSuccess)
     return fail(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed for MXFP4 weights");
   if (hipMemcpy(t.blocks, hb.data(), hb.size(), hipMemcpyHostToDevice) != hipSuccess ||
@@ -714,6 +719,34 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   std::string msg;
   if (!check_desc(w1_desc, E, 2ull * F, D, "w1", msg) || !check_desc(w2_desc, E, D, F, "w2", msg))
     return fail(BURNEXT_INVALID_ARG, msg);
+
+  // host preparation (no device call): tiled experts, biases in the internal row order, gamma and
+  // the gamma-folded router rows
+  TiledMx t1, t2;
+  std::vector<uint8_t> hb1t, hs1t, hb2t, hs2t;
+  burnext_status st = repack_tiled(t1, E, 2 * F, D, w1_blocks, w1_scales, *w1_desc, true, F, gate_up_layout, hb1t, hs1t);
+  if (st == BURNEXT_OK) st = repack_tiled(t2, E, D, F, w2_blocks, w2_scales, *w2_desc, false, F, gate_up_layout, hb2t, hs2t);
+  if (st != BURNEXT_OK) return st;
+  std::vector<float> hb1((size_t)E * t1.rows_p, 0.0f), hb2((size_t)E * t2.rows_p, 0.0f), hrb(E, 0.0f), hg(D, 1.0f);
+  for (uint32_t e = 0; e < E; ++e) {
+    for (uint32_t r = 0; r < 2 * F; ++r)
+      hb1[(size_t)e * t1.rows_p + r] = read_scalar(b1, bias_dtype, (size_t)e * 2 * F + w1_src_row(r, F, gate_up_layout));
+    for (uint32_t d = 0; d < D; ++d) hb2[(size_t)e * t2.rows_p + d] = read_scalar(b2, bias_dtype, (size_t)e * D + d);
+    if (router_b) hrb[e] = read_scalar(router_b, router_dtype, e);
+  }
+  if (norm_gamma)
+    for (uint32_t d = 0; d < D; ++d) hg[d] = read_scalar(norm_gamma, norm_dtype, d);
+  // RmsNorm routing uses gamma-folded rows gw[e, c] = gamma[c] * w[e, c] (f32); with gamma all ones
+  // they equal the given rows, which are then shared.
+  bool ones = true;
+  for (uint32_t d = 0; d < D; ++d) ones = ones && hg[d] == 1.0f;
+  std::vector<float> gw;
+  if (!ones) {
+    gw.resize((size_t)E * D);
+    for (uint32_t e = 0; e < E; ++e)
+      for (uint32_t d = 0; d < D; ++d) gw[(size_t)e * D + d] = hg[d] * read_scalar(router_w, router_dtype, (size_t)e * D + d);
+  }
+
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
     return fail(BURNEXT_INVALID_ARG, "device index out of range (or no HIP device)");
@@ -743,25 +776,13 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   L->disabled = cfg->disabled != 0;
   L->Dp = (uint32_t)align_up(D, 32);
   L->Fp = (uint32_t)align_up(F, 32);
+  L->w1 = t1;
+  L->w2 = t2;
 
-  burnext_status st = upload_tiled(L->w1, E, 2 * F, D, w1_blocks, w1_scales, *w1_desc, true, F, gate_up_layout);
-  if (st == BURNEXT_OK) st = upload_tiled(L->w2, E, D, F, w2_blocks, w2_scales, *w2_desc, false, F, gate_up_layout);
-  if (st != BURNEXT_OK) {
-    free_layer(L);
-    return st;
-  }
+  st = upload_tiled(L->w1, hb1t, hs1t);
+  if (st == BURNEXT_OK) st = upload_tiled(L->w2, hb2t, hs2t);
   // biases (f32 on device), b1 permuted to the interleaved internal row order
-  std::vector<float> hb1((size_t)E * L->w1.rows_p, 0.0f), hb2((size_t)E * L->w2.rows_p, 0.0f), hrb(E, 0.0f),
-      hg(D, 1.0f);
-  for (uint32_t e = 0; e < E; ++e) {
-    for (uint32_t r = 0; r < 2 * F; ++r)
-      hb1[(size_t)e * L->w1.rows_p + r] = read_scalar(b1, bias_dtype, (size_t)e * 2 * F + w1_src_row(r, F, gate_up_layout));
-    for (uint32_t d = 0; d < D; ++d) hb2[(size_t)e * L->w2.rows_p + d] = read_scalar(b2, bias_dtype, (size_t)e * D + d);
-    if (router_b) hrb[e] = read_scalar(router_b, router_dtype, e);
-  }
-  if (norm_gamma)
-    for (uint32_t d = 0; d < D; ++d) hg[d] = read_scalar(norm_gamma, norm_dtype, d);
-  st = upload_vec(&L->b1, hb1);
+  if (st == BURNEXT_OK) st = upload_vec(&L->b1, hb1);
   if (st == BURNEXT_OK) st = upload_vec(&L->b2, hb2);
   if (st == BURNEXT_OK) st = upload_vec(&L->router_b, hrb);
   if (st == BURNEXT_OK) st = upload_vec(&L->gamma, hg);
@@ -774,18 +795,10 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
       st = fail(BURNEXT_DEVICE_ERROR, "hipMemcpy failed for router weight");
   }
   if (st == BURNEXT_OK) {
-    // RmsNorm routing uses gamma-folded rows gw[e, c] = gamma[c] * w[e, c] (f32); with gamma all
-    // ones they equal the given rows, which are then shared.
-    bool ones = true;
-    for (uint32_t d = 0; d < D; ++d) ones = ones && hg[d] == 1.0f;
     if (ones) {
       L->router_wg = L->router_w;
       L->router_wg_bf16 = L->router_bf16;
     } else {
-      std::vector<float> gw((size_t)E * D);
-      for (uint32_t e = 0; e < E; ++e)
-        for (uint32_t d = 0; d < D; ++d)
-          gw[(size_t)e * D + d] = hg[d] * read_scalar(router_w, router_dtype, (size_t)e * D + d);
       float *dgw = nullptr;
       st = upload_vec(&dgw, gw);
       L->router_wg = dgw;
