@@ -169,6 +169,9 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     dominant = max((k for k in stage_us if k in kbytes), key=stage_us.get)
     label = gate_label if dominant == "gate_up" else dominant
     traffic = measured_traffic(name, dominant)
+    if traffic is not None and label == "gate_up+swiglu":
+        sw = measured_traffic(name, "swiglu")
+        traffic = traffic + sw if sw is not None else None
     prefill = T >= 1024
     if prefill:
         fl = kflops[dominant]
