@@ -21,6 +21,7 @@ reference algorithm, timed on a bounded sample of the same workload on the host 
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import pathlib
@@ -211,7 +212,7 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     return out
 
 
-def measure_decoder(steps, warmup, with_cpu):
+def measure_decoder(steps, warmup, with_cpu, kv_bf16_leg=True):
     """C5: the GPT-OSS-20B-shaped decoder (24 layers, d_model 2880, 64 q / 8 kv heads of 64,
     alternating 128-row window and full layers with learned sinks, YaRN factor 32 base 150000,
     vocabulary 201088, 32 experts top-4 per MoE layer) decoding batch 8 greedily with its
@@ -277,6 +278,36 @@ def measure_decoder(steps, warmup, with_cpu):
            "step_bytes_note": f"expected touched experts {touched:.1f} of {cfg.num_experts} per layer under "
                               f"uniform routing; cache rows attended per step summed over layers: {rows}"}
     log(f"decoder: {ms:.3f} ms/step, {out['value']} tokens/s, step {out['step_hbm_gbs']} GB/s")
+    if kv_bf16_leg:
+        # the same decoder with bf16 cache rows (half the attention bytes; parity bar 2e-2 instead of
+        # the f32 cache's 5e-4): a second model object on the same MoE layers
+        cfg16 = dataclasses.replace(cfg, kv_bf16=True)
+        data16 = dataclasses.replace(data, cfg=cfg16)
+        dev.close()
+        dev = DEC.GptOssDecoder(data16, max_batch=B, moe_layers=dev.moe_layers)
+        k = torch.randn(shape, generator=g, device="cuda:0") * 0.6
+        v = torch.randn(shape, generator=g, device="cuda:0")
+        dev.cache_load(k, v)
+        torch.cuda.synchronize()
+        del k, v
+        ws = dev.workspace(B)
+        pos = pre
+        for _ in range(warmup):
+            tok = dev.decode(tok, pos, workspace=ws)
+            pos += 1
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            tok = dev.decode(tok, pos, workspace=ws)
+            pos += 1
+        end.record()
+        torch.cuda.synchronize()
+        ms16 = start.elapsed_time(end) / steps
+        step16 = step_b - (rows * B * kd * 4 * 2 + L * B * kd * 4 * 2) / 2
+        out["kv_bf16"] = {"value": round(B / (ms16 * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms16, 4),
+                          "step_hbm_frac": round(step16 / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "note": "same decoder with bf16 cache rows (the reference keeps f32)"}
+        log(f"decoder (bf16 cache): {ms16:.3f} ms/step, {out['kv_bf16']['value']} tokens/s")
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_decoder(data, B, pre)
     dev.close()

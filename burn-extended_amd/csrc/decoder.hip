@@ -387,6 +387,149 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
   }
 }
 
+// Raw cache quads (4 values), loaded now and converted at use so that the loads stay in flight.
+template <typename KV> struct RawQ;
+template <> struct RawQ<float> { float4 v; };
+template <> struct RawQ<uint16_t> { uint2 v; };
+__device__ __forceinline__ void raw_load(const float *p, RawQ<float> &r) { r.v = *(const float4 *)p; }
+__device__ __forceinline__ void raw_load(const uint16_t *p, RawQ<uint16_t> &r) { r.v = *(const uint2 *)p; }
+__device__ __forceinline__ void raw_vals(const RawQ<float> &r, float (&v)[4]) {
+  v[0] = r.v.x;
+  v[1] = r.v.y;
+  v[2] = r.v.z;
+  v[3] = r.v.w;
+}
+__device__ __forceinline__ void raw_vals(const RawQ<uint16_t> &r, float (&v)[4]) {
+  v[0] = bf16_bits_to_f32((uint16_t)r.v.x);
+  v[1] = bf16_bits_to_f32((uint16_t)(r.v.x >> 16));
+  v[2] = bf16_bits_to_f32((uint16_t)r.v.y);
+  v[3] = bf16_bits_to_f32((uint16_t)(r.v.y >> 16));
+}
+
+// The same chunk as attn_chunk_kernel for head_dim <= 64 and G <= 8, in one memory round trip:
+// every thread requests its q quad, then its key's (up to) 16 K quads and the 16 value quads its
+// (key lane kq, dim quad dq) slot of the value phase needs, before waiting for any of them.  Keys
+// past the window and quads past head_dim read a valid slot and are not used.  Same arithmetic
+// order as attn_chunk_kernel.
+template <typename KV, uint32_t G>
+__global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
+  __shared__ __align__(16) float q_l[G * 64];
+  __shared__ float e_l[kAttnChunk * G];
+  __shared__ float m_l[4 * G], l_l[4 * G];
+  __shared__ __align__(16) float acc_l[4 * G * 16 * 4];  // [wave][j][dq][4]
+  const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const uint32_t dk = a.dk, nq = dk / 4u, t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  const KV *kc = (const KV *)a.kc, *vc = (const KV *)a.vc;
+  const uint32_t p0 = a.p_lo + c * kAttnChunk, p = p0 + t;
+  const bool valid = p <= a.p_hi;
+  const uint32_t nkeys = min(kAttnChunk, a.p_hi + 1u - p0);
+  // requests: q quad, K quads, value quads
+  const uint32_t nqq = G * nq;  // q quads of this kv head's G query heads (<= 128)
+  const float *qsrc = a.q + (size_t)b * a.nH * dk + (size_t)g * G * dk;
+  const float4 qv = *(const float4 *)(qsrc + 4u * min(t, nqq - 1u));
+  __builtin_amdgcn_sched_barrier(0);  // q first: its wait then leaves the K and V loads in flight
+  RawQ<KV> kr[16];
+  const KV *kb = kc + k_index(b, g, (valid ? p : p0) % a.cap, 0u, a.kvH, a.cap_p, dk);
+#pragma unroll
+  for (uint32_t u = 0; u < 16u; ++u) raw_load(kb + (size_t)min(u, nq - 1u) * 256u, kr[u]);
+  const uint32_t kq = t >> 4, dq = t & 15u, dqc = min(dq, nq - 1u);
+  RawQ<KV> vr[16];
+#pragma unroll
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const uint32_t key = min(kq + 16u * i, nkeys - 1u);
+    raw_load(vc + v_index(b, g, (p0 + key) % a.cap, 4u * dqc, a.kvH, a.cap_p, dk), vr[i]);
+  }
+  if (t < nqq) *(float4 *)(q_l + 4u * t) = qv;
+  __syncthreads();
+  float s[G];
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) s[j] = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < 16u; ++u) {
+    if (u < nq) {
+      float k4[4];
+      raw_vals(kr[u], k4);
+#pragma unroll
+      for (uint32_t j = 0; j < G; ++j) {
+        const float4 qa = *(const float4 *)(q_l + j * dk + 4u * u);
+        s[j] = fmaf(qa.x, k4[0], s[j]);
+        s[j] = fmaf(qa.y, k4[1], s[j]);
+        s[j] = fmaf(qa.z, k4[2], s[j]);
+        s[j] = fmaf(qa.w, k4[3], s[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+    s[j] = valid ? s[j] * a.inv_scale : -INFINITY;
+    const float mw = wave_max(s[j]);
+    if (lane == 0) m_l[w * G + j] = mw;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+    const float m = fmaxf(fmaxf(m_l[j], m_l[G + j]), fmaxf(m_l[2u * G + j], m_l[3u * G + j]));
+    const float e = valid ? expf(s[j] - m) : 0.0f;
+    e_l[t * G + j] = e;
+    const float lw = wave_sum_butterfly(e);
+    if (lane == 0) l_l[w * G + j] = lw;
+  }
+  __syncthreads();
+  float acc[G][4];
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const uint32_t key = kq + 16u * i;
+    if (dq < nq && key < nkeys) {
+      float v4[4];
+      raw_vals(vr[i], v4);
+#pragma unroll
+      for (uint32_t j = 0; j < G; ++j) {
+        const float e = e_l[key * G + j];
+        acc[j][0] = fmaf(e, v4[0], acc[j][0]);
+        acc[j][1] = fmaf(e, v4[1], acc[j][1]);
+        acc[j][2] = fmaf(e, v4[2], acc[j][2]);
+        acc[j][3] = fmaf(e, v4[3], acc[j][3]);
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 16, 64);
+      acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 32, 64);
+    }
+  }
+  if (lane < 16u) {
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j)
+      *(float4 *)(acc_l + ((w * G + j) * 16u + dq) * 4u) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+  }
+  __syncthreads();
+  float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)G * (dk + 2u);
+  for (uint32_t i = t; i < G * 16u; i += blockDim.x) {
+    const uint32_t j = i >> 4, dd = i & 15u;
+    if (dd >= nq) continue;
+    float4 r = *(const float4 *)(acc_l + (j * 16u + dd) * 4u);
+#pragma unroll
+    for (uint32_t w2 = 1; w2 < 4u; ++w2) {
+      const float4 v = *(const float4 *)(acc_l + ((w2 * G + j) * 16u + dd) * 4u);
+      r = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+    }
+    float *dst = out + (size_t)j * (dk + 2u) + 2u + 4u * dd;
+    dst[0] = r.x;
+    dst[1] = r.y;
+    dst[2] = r.z;
+    dst[3] = r.w;
+  }
+  if (t < G) {
+    out[(size_t)t * (dk + 2u)] = fmaxf(fmaxf(m_l[t], m_l[G + t]), fmaxf(m_l[2u * G + t], m_l[3u * G + t]));
+    out[(size_t)t * (dk + 2u) + 1u] = (l_l[t] + l_l[G + t]) + (l_l[2u * G + t] + l_l[3u * G + t]);
+  }
+}
+
 // Chunks merged with the sink (src/attention/core.rs:34-55): per head j, M = max(sink, max_c m_c),
 // f_c = exp(m_c - M), L = exp(sink - M) + sum_c l_c f_c; ctx[d] = sum_c acc_c[d] f_c / L.
 // Workgroup (kv head g, batch b): wave w takes heads w, w + 4, ... with lanes over chunks (wave
@@ -789,6 +932,15 @@ burnext_status dense_gemv(const DenseMat &m, const float *x, uint32_t B, float *
 
 template <typename KV>
 hipError_t launch_attention_kv(uint32_t groups, dim3 grid, hipStream_t s, const AttnArgs &a) {
+  if (a.dk <= 64u) {  // one memory round trip per chunk
+    switch (groups) {
+      case 1: return launch_kernel(attn_chunk64_kernel<KV, 1>, grid, dim3(256), 0, s, a);
+      case 2: return launch_kernel(attn_chunk64_kernel<KV, 2>, grid, dim3(256), 0, s, a);
+      case 4: return launch_kernel(attn_chunk64_kernel<KV, 4>, grid, dim3(256), 0, s, a);
+      case 8: return launch_kernel(attn_chunk64_kernel<KV, 8>, grid, dim3(256), 0, s, a);
+      default: break;
+    }
+  }
   switch (groups) {
     case 1: return launch_kernel(attn_chunk_kernel<KV, 1>, grid, dim3(256), 0, s, a);
     case 2: return launch_kernel(attn_chunk_kernel<KV, 2>, grid, dim3(256), 0, s, a);
