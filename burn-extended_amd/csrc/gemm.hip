@@ -4,15 +4,17 @@
 // batches whose expert segments hold many tokens (the reference runs them per 256-token tile
 // and per used expert, src/moe/mod.rs:262-404).
 //
-// v_mfma_scale_f32_16x16x128_f8f6f4 with A = MXFP4 weights (cbsz 4) and B = MXFP8 activations
-// (blgp 0), e8m0 block scales applied by the matrix core:
+// v_mfma_scale_f32_16x16x128_f8f6f4 with A = MXFP4 weights (cbsz 4) and B = activations as an
+// MXFP8 hi term (blgp 0) and an MXFP4 lo term (blgp 4), e8m0 block scales applied by the matrix
+// core:
 //   A: lane l = 16 g + i holds row i, K [32 g, 32 g + 32) as 16 bytes (low nibble first) -- one
 //      K-group of the tiled weight layout, read straight from HBM -- and that block's scale.
-//   B: lane l = 16 g + j holds column (token) j, K [16 g, 16 g + 16) in bytes 0-15 and
-//      K [64 + 16 g, 64 + 16 g + 16) in bytes 16-31; its scale operand is the scale of
+//   B hi (fp8): lane l = 16 g + j holds column (token) j, K [16 g, 16 g + 16) in bytes 0-15 and
+//      K [64 + 16 g, 64 + 16 g + 16) in bytes 16-31; B lo (fp4): lane l holds K [32 g, 32 g + 32)
+//      of column j as 16 bytes, as A does; each term's scale operand is its scale of
 //      K [32 g, 32 g + 32) of column j.
 //   C: lane l = 16 q + j holds rows 4 q .. 4 q + 3 of column j.
-// Activations are two MXFP8 terms (hi + lo), so each product is two MFMAs into one accumulator.
+// Activations are two terms (hi + lo), so each product is two MFMAs into one accumulator.
 #include "kernels.hpp"
 #include "mx_device.hpp"
 
@@ -23,14 +25,18 @@ typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 // One pipeline stage (one 128-wide K-group) in LDS:
-//   B codes [term 2][token 128][slot 8] x 16 bytes, chunk c of token t in slot c ^ ((t >> 1) & 7):
+//   B hi codes [token 128][slot 8] x 16 bytes, chunk c of token t in slot c ^ ((t >> 1) & 7):
 //     a fill instruction reads 8 whole 128-byte rows (coalesced) and the 16 lanes reading one
 //     chunk of 16 consecutive tokens hit 16 distinct 16-byte bank groups;
+//   B lo codes [token 128][slot 4] x 16 bytes (64-byte fp4 rows), chunk c of token t in slot
+//     c ^ ((t >> 2) & 3): a fill instruction reads 16 whole rows, one chunk of 16 consecutive
+//     tokens again hits 16 distinct bank groups;
 //   B scale dwords [term 2][token 128] (byte g = scale of K [32 g, 32 g + 32));
 //   A codes [row tile 16][lane 64] x 16 bytes (the tiled weight layout's K-group, unchanged);
 //   A scales [row tile 16][lane 64] bytes.
 constexpr uint32_t kRowTiles = kGemmRows / 16u;
-constexpr uint32_t kBData = 2u * 8u * kGemmTok * 16u;
+constexpr uint32_t kBHi = 8u * kGemmTok * 16u;
+constexpr uint32_t kBData = kBHi + 4u * kGemmTok * 16u;
 constexpr uint32_t kBScale = 2u * kGemmTok * 4u;
 constexpr uint32_t kAData = kRowTiles * 64u * 16u;
 constexpr uint32_t kAScale = kRowTiles * 64u;
@@ -50,7 +56,7 @@ constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
 // direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
 // accesses across.
 // Clamped SwiGLU with the hardware exp2 and reciprocal (about 1 ulp each): the epilogue feeds it
-// straight into the two-term MXFP8 quantisation (2^-8-level), so the precise expf and division
+// straight into the two-term quantisation (2^-6-level), so the precise expf and division
 // of swiglu_clamp_f would only cost VALU time there.
 __device__ __forceinline__ float swiglu_clamp_fast(float g, float l, float alpha, float limit) {
   const float xg = fminf(g, limit);
@@ -86,8 +92,8 @@ size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 6
 // run together on one XCD.  A workgroup (8 waves, one
 // per CU) computes kGemmRows weight rows (16 row tiles) x kGemmTok tokens; wave w computes rows
 // 64 (w / 2) .. and tokens 64 (w % 2) .. (4 x 4 MFMA tiles, two terms each).  K-groups stream
-// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (56 wave
-// instructions per stage, 7 per wave), one barrier per K-group.
+// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (48 wave
+// instructions per stage, 6 per wave), one barrier per K-group.
 template <bool GATE_UP>
 __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -140,12 +146,17 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   // ---- stage fill by direct-to-LDS loads.  Token columns beyond the tile read the tile's first
   // row and row tiles beyond the expert its last one; their results are never stored.  Lanes
   // outside a K-group's blocks read the row tile's first 16 bytes; they are neutralised at use.
-  // B codes: instruction k = wv + 8 m (m < 4) of 32 fills term k / 16, tokens 8 (k % 16) + lane / 8;
-  // this lane's two tokens (m even / odd) and its swizzled chunk
+  // B hi codes: instruction m (< 2) of wave wv fills tokens 8 (wv + 8 m) + lane / 8; this lane's
+  // two tokens and its swizzled chunk.  B lo codes: wave wv's one instruction fills tokens
+  // 16 wv + lane / 4, chunk lane & 3 into slot (lane & 3) ^ ((token >> 2) & 3).
   const uint32_t tk0 = 8u * wv + (lane >> 3), tk1 = tk0 + 64u;
   const int32_t rk0 = rows_l[tk0], rk1 = rows_l[tk1];
   const size_t browk0 = (size_t)(rk0 >= 0 ? rk0 : rows_l[0]) * kq, browk1 = (size_t)(rk1 >= 0 ? rk1 : rows_l[0]) * kq;
   const uint32_t bchunk = ((lane & 7u) ^ ((tk0 >> 1) & 7u)) * 16u;  // tk1 has the same swizzle
+  const uint32_t tkl = 16u * wv + (lane >> 2);
+  const int32_t rkl = rows_l[tkl];
+  const size_t browl = (size_t)(rkl >= 0 ? rkl : rows_l[0]) * (kq / 2u);
+  const uint32_t lchunk = ((lane & 3u) ^ ((tkl >> 2) & 3u)) * 16u;
   // B scales (waves 4-7): term (wv - 4) / 2, tokens 64 (wv % 2) + lane
   const int32_t r0l = rows_l[lane], r1l = rows_l[64u + lane];
   const size_t row0 = (size_t)(r0l >= 0 ? r0l : rows_l[0]), row1 = (size_t)(r1l >= 0 ? r1l : rows_l[0]);
@@ -155,10 +166,14 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   auto stage = [&](uint32_t kg, uint32_t p) {
     uint8_t *st = smem + p * kStage;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {  // B codes: term m / 2, token group wv + 8 (m % 2)
-      const uint32_t term = (uint32_t)m >> 1, tg = wv + 8u * ((uint32_t)m & 1u);
-      const uint8_t *src = (term ? a.b.lo : a.b.hi) + ((m & 1) ? browk1 : browk0) + kg * 128u + bchunk;
-      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + (term * kGemmTok * 8u + tg * 64u) * 16u), 16, 0, 0);
+    for (int m = 0; m < 2; ++m) {  // B hi codes: token group wv + 8 m
+      const uint32_t tg = wv + 8u * (uint32_t)m;
+      const uint8_t *src = a.b.hi + (m ? browk1 : browk0) + kg * 128u + bchunk;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + tg * 64u * 16u), 16, 0, 0);
+    }
+    {  // B lo codes: tokens 16 wv .. 16 wv + 15
+      const uint8_t *src = a.b.lo + browl + kg * 64u + lchunk;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBHi + wv * 1024u), 16, 0, 0);
     }
     {  // A codes of row tiles wv and wv + 8
       const uint32_t off = lane_ok(kg) ? kg * 1024u + lane * 16u : 0u;
@@ -208,14 +223,15 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   };
   auto read_b = [&](const uint8_t *st, int tt, BFrag &f) {
     const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
-    // lane group q: chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)) of both terms
+    // lane group q: hi chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)); lo chunk q
+    // (K [32 q, +32))
     const uint32_t sw = (tok >> 1) & 7u;
     const uint8_t *r = st + tok * 128u;
     const uint32_t s1 = (q ^ sw) * 16u, s2 = ((4u + q) ^ sw) * 16u;
     const i32x4_t h0 = *(const i32x4_t *)(r + s1), h1 = *(const i32x4_t *)(r + s2);
-    const i32x4_t l0 = *(const i32x4_t *)(r + kGemmTok * 128u + s1), l1 = *(const i32x4_t *)(r + kGemmTok * 128u + s2);
+    const i32x4_t l0 = *(const i32x4_t *)(st + kBHi + tok * 64u + (q ^ ((tok >> 2) & 3u)) * 16u);
     f.Bh = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-    f.Bl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+    f.Bl = __builtin_shufflevector(l0, z4, 0, 1, 2, 3, 4, 5, 6, 7);
     f.sbh = st[kBData + tok * 4u + q];
     f.sbl = st[kBData + (kGemmTok + tok) * 4u + q];
   };
@@ -228,7 +244,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const i32x8_t A8 = __builtin_shufflevector(fa.A[rt], z4, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bl, acc[rt][tt], 4, 0, 0, fa.sa[rt], 0, fb.sbl);
+      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bl, acc[rt][tt], 4, 4, 0, fa.sa[rt], 0, fb.sbl);
     }
   };
 
@@ -243,7 +259,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   }
   stage(0, 0);
   stage(min(1u, nkg - 1u), 1);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(7));  // stage 0 landed (this wave issued 7 after it)
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(6));  // stage 0 landed (this wave issued 6 after it)
   ring_barrier();
   for (uint32_t kg = 0; kg < nkg; ++kg) {
     stage(min(kg + 2u, nkg - 1u), (kg + 2u) % kStages);  // the stage every wave left at the last barrier
@@ -260,9 +276,9 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     read_b(st, 3, b1);
     mma(fa, b0, 2);
     mma(fa, b1, 3);
-    // this wave issued 7 instructions for stage kg + 2 after stage kg + 1's: stage kg + 1 landed
-    // once at most 7 are outstanding
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(7));
+    // this wave issued 6 instructions for stage kg + 2 after stage kg + 1's: stage kg + 1 landed
+    // once at most 6 are outstanding
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(6));
     ring_barrier();
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the trailing reloads have landed
@@ -303,16 +319,17 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         rmax = fmaxf(rmax, fmaxf(fabsf(res[2 * k]), fabsf(res[2 * k + 1])));
       }
       rmax = max_lanes_16_32(rmax);
-      const uint32_t sbl = mx8_scale_byte(rmax);
+      const uint32_t sbl = mx4_scale_byte(rmax);
       const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
         uint8_t *dh = a.act.hi + row * a.act.kq + fb + 2u * q;
-        uint8_t *dl = a.act.lo + row * a.act.kq + fb + 2u * q;
+        // lo: features 8 k + 2 q and 8 k + 2 q + 1 of the block are one byte of e2m1 codes
+        uint8_t *dl = a.act.lo + row * (a.act.kq / 2u) + fb / 2u + q;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           *(uint16_t *)(dh + 8u * k) = (uint16_t)ch[k];
-          *(uint16_t *)(dl + 8u * k) = (uint16_t)f32x2_to_fp8x2(res[2 * k] * il, res[2 * k + 1] * il);
+          dl[4u * k] = (uint8_t)(f32_to_e2m1(res[2 * k] * il) | (f32_to_e2m1(res[2 * k + 1] * il) << 4));
         }
         if (q == 0) {
           a.act.shi[row * (a.act.kq >> 5) + (fb >> 5)] = (uint8_t)sbh;
@@ -327,7 +344,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
         const uint32_t tk = i / padb, c = i - tk * padb;
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tk));
         a.act.hi[row * a.act.kq + f_end + c] = 0;
-        a.act.lo[row * a.act.kq + f_end + c] = 0;
+        if ((c & 1u) == 0u) a.act.lo[row * (a.act.kq / 2u) + (f_end + c) / 2u] = 0;
         if ((c & 31u) == 0u) {
           a.act.shi[row * (a.act.kq >> 5) + ((f_end + c) >> 5)] = 0;
           a.act.slo[row * (a.act.kq >> 5) + ((f_end + c) >> 5)] = 0;

@@ -3,7 +3,7 @@
 // router_kernel     RmsNorm + router logits, parallel over token blocks x expert groups
 //                   replaces src/moe/mod.rs:109-110 (Burn RmsNorm / Linear)
 // router_rows       the same for prefill batches: one wave per few tokens, rows in registers,
-//                   also writes the two-term MXFP8 rows of the grouped GEMM
+//                   also writes the two-term (MXFP8 hi + MXFP4 lo) rows of the grouped GEMM
 // topk_kernel       top-k + softmax over the selected logits, one wave per token
 //                   replaces src/moe/mod.rs:271-276 (topk_with_indices, max/exp/sum/div)
 // dispatch_kernel   histogram / exclusive scan / stable scatter into expert segments
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 
   __syncthreads();  // rr visible
   // normalised rows xn = x * (1/r) * gamma (x without RmsNorm) for the expert GEMV in the x dtype,
-  // zero padded to Dp, and (grouped GEMM) their two-term MXFP8 form zero padded to the K-group
+  // zero padded to Dp, and (grouped GEMM) their two-term form zero padded to the K-group
   // length.  Every expert group shares the writing (chunk or block i of the token block by group
   // i mod gridDim.y), before the dot products so the stores drain meanwhile.
   auto gamma8 = [&](uint32_t c0, float g[8]) {  // gamma[c0 .. c0 + 8), ones beyond D
@@ -277,8 +277,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
         }
       }
       const size_t row = t0 + tt;
-      mx8_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * a.xq.kq + bk * 32u,
-                     a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
+      mx84_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * (a.xq.kq / 2u) + bk * 16u,
+                      a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
     }
   }
 
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prefill router (D % 8 == 0, D, Dp and the MXFP8 row length <= 512 * kFrontChunks, 16-byte
+// Prefill router (D % 8 == 0, D, Dp and the two-term row length <= 512 * kFrontChunks, 16-byte
 // aligned rows).  Workgroup of kRowsThreads: wave w holds tokens T (8 b + w) .. +T in registers
 // (f32, T = 2 or 4); the router rows pass through LDS as f32 in stages of kRowsExperts experts (double
 // buffered, filled by all threads, one barrier per stage), so each row is converted once per
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 // 512 i + 256 (j / 4) + 4 l + j % 4, so lane l's two float4 of its chunk are conflict-free.
 // Same fixed reduction order and formulas as router_kernel (lane l owns chunks c = 512 i + 8 l + j,
 // fmaf over i then j, xor butterfly; logit = dot / r + b): the logits, r and the written rows
-// equal router_kernel's bit for bit.  The two-term MXFP8 rows come from the registers: a 32-value
+// equal router_kernel's bit for bit.  The two-term rows come from the registers: a 32-value
 // block is the 8-value chunks of lanes 4 b .. 4 b + 3, its maxima taken over those four lanes.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRowsExperts = 4;    // experts per LDS stage
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
   }
 
   // normalised rows xn = x * (1/r) * gamma (x without RmsNorm), zero padded to Dp, and their
-  // two-term MXFP8 form zero padded to the K-group length; written before the dot products so
+  // two-term form zero padded to the K-group length; written before the dot products so
   // the stores drain meanwhile
   if (active && (a.xn || a.xq.hi)) {
     const uint32_t nbk = a.xq.kq >> 5;
@@ -497,14 +497,14 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
           }
           rmax = fmaxf(rmax, dpp_mov<0xB1>(rmax));
           rmax = fmaxf(rmax, dpp_mov<0x4E>(rmax));
-          const uint32_t sbl = mx8_scale_byte(rmax);
+          const uint32_t sbl = mx4_scale_byte(rmax);
           const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
           if (tv && c0 < a.xq.kq) {
-            uint32_t cl[4];
+            uint32_t cl = 0u;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) cl[k] = f32x2_to_fp8x2(res[2 * k] * il, res[2 * k + 1] * il);
+            for (int k = 0; k < 8; ++k) cl |= f32_to_e2m1(res[k] * il) << (4 * k);
             *(uint2 *)(a.xq.hi + row * a.xq.kq + c0) = make_uint2(ch[0] | (ch[1] << 16), ch[2] | (ch[3] << 16));
-            *(uint2 *)(a.xq.lo + row * a.xq.kq + c0) = make_uint2(cl[0] | (cl[1] << 16), cl[2] | (cl[3] << 16));
+            *(uint32_t *)(a.xq.lo + row * (a.xq.kq / 2u) + c0 / 2u) = cl;
             if ((lane & 3u) == 0u) {
               a.xq.shi[row * nbk + (c0 >> 5)] = (uint8_t)sbh;
               a.xq.slo[row * nbk + (c0 >> 5)] = (uint8_t)sbl;

@@ -27,11 +27,12 @@ inline hipError_t launch_kernel(void (*k)(A), dim3 grid, dim3 block, size_t lds,
   return hipLaunchKernel((const void *)k, grid, block, args, lds, s);
 }
 
-// Two-term MXFP8 rows (see mx_device.hpp): kq code bytes per row and term, K padded to whole
-// 128-wide K-groups with zero codes and zero scale bytes, natural K order; kq / 32 scale bytes
-// per row and term.
+// The grouped GEMM's activation rows (see mx_device.hpp): kq codes per row, K padded to whole
+// 128-wide K-groups with zero codes and zero scale bytes, natural K order -- the hi term as MXFP8
+// (kq bytes per row), the lo term as MXFP4 (kq / 2 bytes per row, two codes per byte); kq / 32
+// scale bytes per row and term.
 struct QRows {
-  uint8_t *hi, *lo;    // [rows, kq]
+  uint8_t *hi, *lo;    // [rows, kq], [rows, kq / 2]
   uint8_t *shi, *slo;  // [rows, kq / 32]
   uint32_t kq;
 };
@@ -46,7 +47,7 @@ struct RouterArgs {
   float *logits;      // [n, E]
   float *rms;         // [n] (written when apply_norm), nullable
   void *xn;           // [n, Dp] normalised rows in the x dtype (expert group 0 writes), nullable
-  QRows xq;           // the same rows as two-term MXFP8 (expert group 0 writes when xq.hi)
+  QRows xq;           // the same rows in the GEMM's two-term form (expert group 0 writes when xq.hi)
   const float *gamma; // [D]
   uint32_t n, D, Dpad, Dp, E, tb, epw;
   float eps;
@@ -137,7 +138,7 @@ constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 
 // Grouped expert GEMM for prefill-sized batches (expert_gemm_kernel): every active expert's
 // segment is cut into tiles of kGemmTok routed tokens; a workgroup computes kGemmRows weight
-// rows x one token tile with the block-scaled MFMA (MXFP4 weights x two-term MXFP8 activations).
+// rows x one token tile with the block-scaled MFMA (MXFP4 weights x MXFP8 hi + MXFP4 lo activations).
 constexpr uint32_t kGemmTok = 128;
 constexpr uint32_t kGemmRows = 256;
 struct GemmArgs {

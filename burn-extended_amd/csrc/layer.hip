@@ -288,7 +288,7 @@ struct WsLayout {
 
 // bf16 batches of at least kGemmMinTokens tokens with at least kGemmMinPerExpert routed tokens per
 // expert on average run the grouped GEMM (its 128-token tiles are then mostly full); the others,
-// and every f32 batch (the GEMM's two MXFP8 terms carry bf16-level precision), run the expert
+// and every f32 batch (the GEMM's two activation terms carry about 2^-6 relative precision), run the expert
 // GEMVs.  Measured crossover (per step): 20B (E = 32) GEMV 192 / 243 / 335 us against GEMM 242 /
 // 243 / 246 us at 64 / 128 / 200 tokens; 120B (E = 128) GEMV 489 / 435 us against GEMM 755 / 761
 // us at 128 / 200 tokens.
@@ -298,7 +298,8 @@ inline bool use_gemm_path(const burnext_moe_layer &L, uint64_t n) {
   return n >= kGemmMinTokens && n * L.K >= kGemmMinPerExpert * L.E;
 }
 
-// Row bytes of two-term MXFP8 rows over K = cols of a tiled projection (whole 128-wide K-groups).
+// Codes per row of the GEMM's activation rows over K = cols of a tiled projection (whole 128-wide
+// K-groups): the hi term's bytes; the lo term takes half as many.
 inline uint32_t qrow_bytes(const TiledMx &t) { return ((t.nb + 3u) / 4u) * 128u; }
 
 // Largest batch m <= min(n, kSmallRouteMaxTokens) that still splits gate_up in K-parts (0: none).
@@ -341,11 +342,11 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.tile_off = take((L.E + 1ull) * 4);
     const uint64_t kx = qrow_bytes(L.w1), ka = qrow_bytes(L.w2);
     w.xq[0] = take(n * kx);
-    w.xq[1] = take(n * kx);
+    w.xq[1] = take(n * kx / 2);  // e2m1 lo codes, two per byte
     w.xq[2] = take(n * kx / 32);
     w.xq[3] = take(n * kx / 32);
     w.aq[0] = take(nk * ka);
-    w.aq[1] = take(nk * ka);
+    w.aq[1] = take(nk * ka / 2);
     w.aq[2] = take(nk * ka / 32);
     w.aq[3] = take(nk * ka / 32);
   }
@@ -593,7 +594,7 @@ burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, ui
   return st == BURNEXT_OK ? ok() : st;
 }
 
-// Grouped-GEMM path (use_gemm_path): router (+ two-term MXFP8 rows of xn), top-k,
+// Grouped-GEMM path (use_gemm_path): router (+ the two-term rows of xn), top-k,
 // dispatch (+ token-tile prefix), gate_up GEMM (SwiGLU, quantised act rows), down GEMM (slot rows).
 burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64_t n, bool norm, const WsPtrs &p,
                             hipStream_t s) {

@@ -102,8 +102,9 @@ __device__ __forceinline__ bf16x8_t fp4x8_to_bf16x8(uint32_t w, float scale) {
 // A value v of a block with scale byte sb is stored as e4m3(v * 2^(127 - sb)).  The scale of a
 // block is the smallest power of two that brings the block's largest magnitude to <= 448 (the
 // largest finite e4m3fn value), so every code is finite; an all-zero block gets scale byte 0.
-// Activations are carried as two such terms, hi + lo (lo = the block-scaled residual of hi),
-// which keeps about 2^-8 relative accuracy: bf16-like, where one term alone (2^-4) is not.
+// The grouped GEMM carries activations as two terms: hi in this format and lo = the residual
+// x - hi in MXFP4 at its own block scale (below), about 2^-6 relative per value at worst, where
+// one e4m3 term alone (2^-4) is not accurate enough.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
   const uint32_t u = __float_as_uint(amax);
@@ -128,6 +129,31 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t w) {
   return __builtin_amdgcn_cvt_f32_fp8((int)w, SEL);
 }
 
+// ---------------------------------------------------------------------------------------------
+// MXFP4 (OCP e2m1, one e8m0 scale per 32 values) for the low term of the GEMM activations.  A
+// block of residuals with largest magnitude amax gets the smallest power of two 2^(sb - 127) that
+// brings amax to <= 6 (the largest e2m1 magnitude); an all-zero block gets scale byte 0.  Codes
+// round to nearest even and saturate at 6; bit 3 is the sign.  Two codes per byte, the even K
+// index in the low nibble (the MFMA's fp4 operand order).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mx4_scale_byte(float amax) {
+  const uint32_t u = __float_as_uint(amax);
+  const uint32_t be = (u >> 23) & 0xFFu;  // amax = m * 2^(be - 127), m in [1, 2)
+  if (amax <= 0.0f || be == 0u) return 0u;
+  const uint32_t adj = (u & 0x7FFFFFu) > 0x400000u ? 1u : 0u;  // m > 1.5: amax / 2^(be-129) > 6
+  const int sb = (int)be - 2 + (int)adj;
+  return (uint32_t)min(max(sb, 1), 253);
+}
+
+// e2m1 code of v (already divided by the block scale): the midpoints 0.25, 0.75, ..., 5 between
+// the magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6 decide, ties to the even code.
+__device__ __forceinline__ uint32_t f32_to_e2m1(float v) {
+  const float a = fabsf(v);
+  const uint32_t c = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) + (uint32_t)(a >= 1.75f) +
+                     (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) + (uint32_t)(a > 5.0f);
+  return c | ((__float_as_uint(v) >> 28) & 8u);
+}
+
 // Clamped SwiGLU of one (gate, linear) pair (reference src/activation/mod.rs:5-45,
 // src/quant/gpu.rs:140-145): g = min(g, limit), l = clamp(l, +-limit), g * sigmoid(alpha g) * (l + 1).
 __device__ __forceinline__ float swiglu_clamp_f(float g, float l, float alpha, float limit) {
@@ -137,13 +163,14 @@ __device__ __forceinline__ float swiglu_clamp_f(float g, float l, float alpha, f
   return (xg * sig) * (xl + 1.0f);
 }
 
-// One block of 32 values (largest magnitude amax) -> two-term MXFP8: 32 hi codes, 32 lo codes
-// (16-byte aligned destinations) and the two scale bytes.
-__device__ __forceinline__ void mx8_quantize32(const float (&v)[32], float amax, uint8_t *hi, uint8_t *lo,
-                                               uint8_t *shi, uint8_t *slo) {
+// One block of 32 values (largest magnitude amax) -> the GEMM's two activation terms: 32 MXFP8
+// hi codes (e4m3), 16 bytes of MXFP4 lo codes (e2m1 of the residual, two per byte; 16-byte
+// aligned destinations) and the two scale bytes.
+__device__ __forceinline__ void mx84_quantize32(const float (&v)[32], float amax, uint8_t *hi, uint8_t *lo,
+                                                uint8_t *shi, uint8_t *slo) {
   const uint32_t sbh = mx8_scale_byte(amax);
   const float ih = sbh ? mx8_inv_scale(sbh) : 0.0f, sh = e8m0_to_f32(sbh);
-  uint32_t wh[8], wl[8];
+  uint32_t wh[8];
   float r[32], rmax = 0.0f;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
@@ -153,17 +180,14 @@ __device__ __forceinline__ void mx8_quantize32(const float (&v)[32], float amax,
     rmax = fmaxf(rmax, fmaxf(fabsf(r[2 * k]), fabsf(r[2 * k + 1])));
     if (k & 1) wh[k >> 1] |= c << 16; else wh[k >> 1] = c;
   }
-  const uint32_t sbl = mx8_scale_byte(rmax);
+  const uint32_t sbl = mx4_scale_byte(rmax);
   const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
+  uint32_t w4[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const uint32_t c = f32x2_to_fp8x2(r[2 * k] * il, r[2 * k + 1] * il);
-    if (k & 1) wl[k >> 1] |= c << 16; else wl[k >> 1] = c;
-  }
+  for (int k = 0; k < 32; ++k) w4[k >> 3] |= f32_to_e2m1(r[k] * il) << (4 * (k & 7));
   *(uint4 *)hi = make_uint4(wh[0], wh[1], wh[2], wh[3]);
   *(uint4 *)(hi + 16) = make_uint4(wh[4], wh[5], wh[6], wh[7]);
-  *(uint4 *)lo = make_uint4(wl[0], wl[1], wl[2], wl[3]);
-  *(uint4 *)(lo + 16) = make_uint4(wl[4], wl[5], wl[6], wl[7]);
+  *(uint4 *)lo = make_uint4(w4[0], w4[1], w4[2], w4[3]);
   *shi = (uint8_t)sbh;
   *slo = (uint8_t)sbl;
 }
