@@ -8,7 +8,8 @@
 // MXFP8 hi term (blgp 0) and an MXFP4 lo term (blgp 4), e8m0 block scales applied by the matrix
 // core:
 //   A: lane l = 16 g + i holds row i, K [32 g, 32 g + 32) as 16 bytes (low nibble first) -- one
-//      K-group of the tiled weight layout, read straight from HBM -- and that block's scale.
+//      K-group of the tiled weight layout, loaded straight into registers -- and that block's
+//      scale.
 //   B hi (fp8): lane l = 16 g + j holds column (token) j, K [16 g, 16 g + 16) in bytes 0-15 and
 //      K [64 + 16 g, 64 + 16 g + 16) in bytes 16-31; B lo (fp4): lane l holds K [32 g, 32 g + 32)
 //      of column j as 16 bytes, as A does; each term's scale operand is its scale of
@@ -24,28 +25,27 @@ typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
-// One pipeline stage (one 128-wide K-group) in LDS:
-//   B hi codes [token 128][slot 8] x 16 bytes, chunk c of token t in slot c ^ ((t >> 1) & 7):
+// One pipeline stage (one 128-wide K-group of the activations; the weights bypass LDS) in LDS:
+//   B hi codes [token 64][slot 8] x 16 bytes, chunk c of token t in slot c ^ ((t >> 1) & 7):
 //     a fill instruction reads 8 whole 128-byte rows (coalesced) and the 16 lanes reading one
 //     chunk of 16 consecutive tokens hit 16 distinct 16-byte bank groups;
-//   B lo codes [token 128][slot 4] x 16 bytes (64-byte fp4 rows), chunk c of token t in slot
+//   B lo codes [token 64][slot 4] x 16 bytes (64-byte fp4 rows), chunk c of token t in slot
 //     c ^ ((t >> 2) & 3): a fill instruction reads 16 whole rows, one chunk of 16 consecutive
 //     tokens again hits 16 distinct bank groups;
-//   B scale dwords [term 2][token 128] (byte g = scale of K [32 g, 32 g + 32));
-//   A codes [row tile 16][lane 64] x 16 bytes (the tiled weight layout's K-group, unchanged);
-//   A scales [row tile 16][lane 64] bytes.
+//   B scale dwords [term 2][token / 32][64 lanes] (byte g = scale of K [32 g, 32 g + 32) of token
+//     32 (token / 32) + lane; lanes 32-63 repeat lanes 0-31, so one dword fill instruction per
+//     wave serves 32 tokens of one term).
 constexpr uint32_t kRowTiles = kGemmRows / 16u;
 constexpr uint32_t kBHi = 8u * kGemmTok * 16u;
 constexpr uint32_t kBData = kBHi + 4u * kGemmTok * 16u;
-constexpr uint32_t kBScale = 2u * kGemmTok * 4u;
-constexpr uint32_t kAData = kRowTiles * 64u * 16u;
-constexpr uint32_t kAScale = kRowTiles * 64u;
-constexpr uint32_t kStage = kBData + kBScale + kAData + kAScale;
-constexpr uint32_t kStages = 3;
-constexpr uint32_t kWaves = 8;
+constexpr uint32_t kBScale = 2u * kGemmTok * 8u;
+constexpr uint32_t kStage = kBData + kBScale;
+constexpr uint32_t kStages = 5;
+constexpr uint32_t kWaves = 4;
+static_assert(kGemmTok == 64, "four waves of 64 x 64 tiles cover 256 rows x 64 tokens");
 typedef __attribute__((address_space(3))) void lds_void;
-// s_waitcnt with vmcnt(n) only (expcnt and lgkmcnt left at their maxima), n < 16
-constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8); }
+// s_waitcnt with vmcnt(n) only (expcnt and lgkmcnt left at their maxima), n < 64
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 // s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima)
 constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
 
@@ -87,15 +87,18 @@ size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 6
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
 // take a contiguous run of Q = ceil(N / 8) of the N realised items (N = nrb * token tiles, read
 // from tile_off[E]; the grid is sized for the most tiles routing can produce, and sizing the runs
-// by the grid left the last XCD a small remainder while the other seven did all the work), then
-// item = token tile gt * nrb + row block rb (rb fastest): the workgroups sharing a token tile's B
-// run together on one XCD.  A workgroup (8 waves, one
-// per CU) computes kGemmRows weight rows (16 row tiles) x kGemmTok tokens; wave w computes rows
-// 64 (w / 2) .. and tokens 64 (w % 2) .. (4 x 4 MFMA tiles, two terms each).  K-groups stream
-// through a 3-stage LDS ring filled by direct-to-LDS loads two K-groups ahead (48 wave
-// instructions per stage, 6 per wave), one barrier per K-group.
+// by the grid left the last XCD a small remainder while the other seven did all the work).  Items
+// go in groups of 8 token tiles: row block rb of the group's tiles, tiles fastest, so the ~64
+// workgroups an XCD runs at once share about 8 row blocks of weights and 8 tiles of activations
+// in its L2 (gate_up HBM reads 2.1 -> 1.0 GB per launch at C3 against row blocks fastest).
+// A workgroup (4 waves; two workgroups per CU, whose K-loops drift apart, so one's LDS reads
+// and waits overlap the other's MFMAs) computes kGemmRows weight rows (16 row tiles) x kGemmTok
+// tokens; wave w computes rows 64 w .. 64 w + 63 (4 x 4 MFMA tiles of 16 x 16, two terms each).
+// Weights go straight from the tiled layout into registers, two K-groups ahead (two register
+// sets); activations stream through a 5-stage LDS ring filled by direct-to-LDS loads four
+// K-groups ahead (4 instructions per wave per stage); one barrier per K-group.
 template <bool GATE_UP>
-__global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   int32_t *rows_l = (int32_t *)(smem + kStages * kStage);  // [kGemmTok] B row, -1 = none
   int32_t *slot_l = rows_l + kGemmTok;                     // [kGemmTok] down: slot
@@ -105,7 +108,10 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   const uint32_t N = a.nrb * (uint32_t)a.tile_off[a.E], Q = (N + 7u) / 8u;  // 8 * Q <= gridDim.x
   const uint32_t it = (b & 7u) * Q + (b >> 3);
   if ((b >> 3) >= Q || it >= N) return;  // workgroup-uniform: no item
-  const uint32_t gt = it / a.nrb, rb = it - gt * a.nrb;
+  // items in groups of 8 token tiles: row block rb of the group's tiles, tiles fastest
+  const uint32_t NT = (uint32_t)a.tile_off[a.E], grp = it / (8u * a.nrb), r = it - grp * 8u * a.nrb;
+  const uint32_t gsz = min(8u, NT - grp * 8u);
+  const uint32_t rb = r / gsz, gt = grp * 8u + (r - rb * gsz);
   if (threadIdx.x == 0) info_l[0] = -1;
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < a.E; e += blockDim.x) {
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-  const uint32_t wr = wv >> 1, wc = wv & 1u;
+  const uint32_t wr = wv;  // this wave's 64-row quarter of the workgroup's rows
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2, tail = a.nb - 4u * (nkg - 1u);
   const uint32_t kq = a.b.kq, sq = kq >> 5;  // code bytes and scale bytes per B row
@@ -144,12 +150,11 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
 
   // ---- stage fill by direct-to-LDS loads.  Token columns beyond the tile read the tile's first
-  // row and row tiles beyond the expert its last one; their results are never stored.  Lanes
-  // outside a K-group's blocks read the row tile's first 16 bytes; they are neutralised at use.
-  // B hi codes: instruction m (< 2) of wave wv fills tokens 8 (wv + 8 m) + lane / 8; this lane's
+  // row and row tiles beyond the expert its last one; their results are never stored.
+  // B hi codes: instruction m (< 2) of wave wv fills tokens 8 (wv + 4 m) + lane / 8; this lane's
   // two tokens and its swizzled chunk.  B lo codes: wave wv's one instruction fills tokens
   // 16 wv + lane / 4, chunk lane & 3 into slot (lane & 3) ^ ((token >> 2) & 3).
-  const uint32_t tk0 = 8u * wv + (lane >> 3), tk1 = tk0 + 64u;
+  const uint32_t tk0 = 8u * wv + (lane >> 3), tk1 = tk0 + 32u;
   const int32_t rk0 = rows_l[tk0], rk1 = rows_l[tk1];
   const size_t browk0 = (size_t)(rk0 >= 0 ? rk0 : rows_l[0]) * kq, browk1 = (size_t)(rk1 >= 0 ? rk1 : rows_l[0]) * kq;
   const uint32_t bchunk = ((lane & 7u) ^ ((tk0 >> 1) & 7u)) * 16u;  // tk1 has the same swizzle
@@ -157,17 +162,23 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
   const int32_t rkl = rows_l[tkl];
   const size_t browl = (size_t)(rkl >= 0 ? rkl : rows_l[0]) * (kq / 2u);
   const uint32_t lchunk = ((lane & 3u) ^ ((tkl >> 2) & 3u)) * 16u;
-  // B scales (waves 4-7): term (wv - 4) / 2, tokens 64 (wv % 2) + lane
-  const int32_t r0l = rows_l[lane], r1l = rows_l[64u + lane];
-  const size_t row0 = (size_t)(r0l >= 0 ? r0l : rows_l[0]), row1 = (size_t)(r1l >= 0 ? r1l : rows_l[0]);
-  const uint32_t a_rt0 = min(rb * kRowTiles + wv, a.nrt - 1u);       // A codes: row tiles wv, wv + 8
-  const uint32_t a_rt1 = min(rb * kRowTiles + wv + 8u, a.nrt - 1u);
-  const uint32_t as_rt = min(rb * kRowTiles + (wv & 3u) * 4u + (lane >> 4), a.nrt - 1u);  // A scales (waves 0-3)
+  // B scales: term wv / 2, token 32 (wv % 2) + lane % 32
+  const int32_t rsl = rows_l[32u * (wv & 1u) + (lane & 31u)];
+  const size_t rows = (size_t)(rsl >= 0 ? rsl : rows_l[0]);
+  // this wave's 4 row tiles (clamped to the expert's last)
+  const uint8_t *arow[4];
+  const uint8_t *srow[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const uint32_t t = min(rb * kRowTiles + wr * 4u + (uint32_t)rt, a.nrt - 1u);
+    arow[rt] = wexp + (size_t)t * a.nb * 256u + lane * 16u;
+    srow[rt] = sexp + (size_t)t * a.nb * 16u + (lane & ~3u);
+  }
   auto stage = [&](uint32_t kg, uint32_t p) {
     uint8_t *st = smem + p * kStage;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {  // B hi codes: token group wv + 8 m
-      const uint32_t tg = wv + 8u * (uint32_t)m;
+    for (int m = 0; m < 2; ++m) {  // B hi codes: token group wv + 4 m
+      const uint32_t tg = wv + 4u * (uint32_t)m;
       const uint8_t *src = a.b.hi + (m ? browk1 : browk0) + kg * 128u + bchunk;
       __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + tg * 64u * 16u), 16, 0, 0);
     }
@@ -175,23 +186,10 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
       const uint8_t *src = a.b.lo + browl + kg * 64u + lchunk;
       __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBHi + wv * 1024u), 16, 0, 0);
     }
-    {  // A codes of row tiles wv and wv + 8
-      const uint32_t off = lane_ok(kg) ? kg * 1024u + lane * 16u : 0u;
-      __builtin_amdgcn_global_load_lds((const void *)(wexp + (size_t)a_rt0 * a.nb * 256u + off),
-                                       (lds_void *)(st + kBData + kBScale + wv * 1024u), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void *)(wexp + (size_t)a_rt1 * a.nb * 256u + off),
-                                       (lds_void *)(st + kBData + kBScale + (wv + 8u) * 1024u), 16, 0, 0);
-    }
-    if (wv >= 4u) {  // B scales: term (wv - 4) / 2, tokens 64 (wv % 2) + lane
-      const uint32_t term = (wv - 4u) >> 1;
-      const uint8_t *src = (term ? a.b.slo : a.b.shi) + ((wv & 1u) ? row1 : row0) * sq + kg * 4u;
-      __builtin_amdgcn_global_load_lds((const void *)src,
-                                       (lds_void *)(st + kBData + (term * kGemmTok + (wv & 1u) * 64u) * 4u), 4, 0, 0);
-    } else {  // A scales of row tiles 4 wv .. +4: 4 bytes per lane
-      const uint32_t g = lane & 15u;  // 4-byte group of the row tile's 64 scale bytes
-      const uint8_t *src = sexp + (size_t)as_rt * a.nb * 16u + min(kg * 64u + 4u * g, a.nb * 16u - 4u);
-      __builtin_amdgcn_global_load_lds((const void *)src,
-                                       (lds_void *)(st + kBData + kBScale + kAData + wv * 256u), 4, 0, 0);
+    {  // B scales: term wv / 2, tokens 32 (wv % 2) + lane % 32 (lanes 32-63 repeat lanes 0-31 into
+       // the unused half of the wave's 256 bytes)
+      const uint8_t *src = (wv >= 2u ? a.b.slo : a.b.shi) + rows * sq + kg * 4u;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBData + wv * 256u), 4, 0, 0);
     }
   };
 
@@ -201,7 +199,9 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // MFMA operands: the A operands (row tiles) of a K-group, and the B operands of one token tile
+  // MFMA operands: the A operands (row tiles) of a K-group, and the B operands of one token tile.
+  // A scales are whole dwords of the tiled scale layout: byte lane & 3 is this lane's, shifted to
+  // bits 0-7 (the scale operand's byte 0) before use.
   struct AFrag {
     i32x4_t A[4];
     int32_t sa[4];
@@ -211,18 +211,21 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     int32_t sbh, sbl;
   };
   const i32x4_t z4 = {0, 0, 0, 0};
-  auto read_a = [&](uint32_t kg, const uint8_t *st, AFrag &f) {
+  // A straight from the tiled weights into registers.  Lanes outside the last K-group's blocks read
+  // the row tile's first block (finite fp4 codes, scale byte < 255 for finite weights): the B rows
+  // are zero beyond K (codes 0 in the K padding of xq and act), so their products add zeros.
+  auto load_a = [&](uint32_t kg, AFrag &f) {
     const bool ok = lane_ok(kg);
+    const uint32_t off = ok ? kg * 1024u : 0u, soff = ok ? kg * 64u : 0u;
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const uint32_t rtl = wr * 4u + (uint32_t)rt;
-      const i32x4_t w4 = *(const i32x4_t *)(st + kBData + kBScale + (rtl * 64u + lane) * 16u);
-      f.A[rt] = ok ? w4 : z4;
-      f.sa[rt] = ok ? (int32_t)st[kBData + kBScale + kAData + rtl * 64u + lane] : 127;
-    }
+    for (int rt = 0; rt < 4; ++rt) f.A[rt] = *(const i32x4_t *)(arow[rt] + off);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) f.sa[rt] = *(const int32_t *)(srow[rt] + soff);  // byte lane & 3 is ours
+    __builtin_amdgcn_sched_barrier(0);  // the wait counts below assume this issue order
   };
+
   auto read_b = [&](const uint8_t *st, int tt, BFrag &f) {
-    const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+    const uint32_t tok = (uint32_t)tt * 16u + i16;
     // lane group q: hi chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)); lo chunk q
     // (K [32 q, +32))
     const uint32_t sw = (tok >> 1) & 7u;
@@ -232,9 +235,11 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     const i32x4_t l0 = *(const i32x4_t *)(st + kBHi + tok * 64u + (q ^ ((tok >> 2) & 3u)) * 16u);
     f.Bh = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
     f.Bl = __builtin_shufflevector(l0, z4, 0, 1, 2, 3, 4, 5, 6, 7);
-    f.sbh = st[kBData + tok * 4u + q];
-    f.sbl = st[kBData + (kGemmTok + tok) * 4u + q];
+    const uint32_t so = kBData + (tok >> 5) * 256u + (tok & 31u) * 4u + q;
+    f.sbh = st[so];
+    f.sbl = st[so + kBScale / 2u];
   };
+  const uint32_t sshift = 8u * (lane & 3u);
   auto mma = [&](const AFrag &fa, const BFrag &fb, int tt) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
@@ -257,30 +262,42 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
     bias4[rt] = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
   }
-  stage(0, 0);
-  stage(min(1u, nkg - 1u), 1);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(6));  // stage 0 landed (this wave issued 6 after it)
+  // B stages of K-groups 0..3, then A of K-groups 0 and 1 (loads complete in order).  The
+  // compiler must not reorder these groups: the s_waitcnt counts below assume this issue order.
+#pragma unroll
+  for (uint32_t j = 0; j < kStages - 1u; ++j) stage(min(j, nkg - 1u), j);
+  __builtin_amdgcn_sched_barrier(0);
+  AFrag ar0, ar1;
+  load_a(0, ar0);
+  load_a(min(1u, nkg - 1u), ar1);
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(8));  // A(0) and every B stage before it landed
   ring_barrier();
-  for (uint32_t kg = 0; kg < nkg; ++kg) {
-    stage(min(kg + 2u, nkg - 1u), (kg + 2u) % kStages);  // the stage every wave left at the last barrier
+  auto iter = [&](uint32_t kg, AFrag &ar) {
+    stage(min(kg + kStages - 1u, nkg - 1u), (kg + kStages - 1u) % kStages);  // the slot every wave left
+    __builtin_amdgcn_sched_barrier(0);
     const uint8_t *st = smem + (kg % kStages) * kStage;
-    // token tile tt + 1's operands are read while tile tt's MFMAs run
-    AFrag fa;
     BFrag b0, b1;
-    read_a(kg, st, fa);
     read_b(st, 0, b0);
     read_b(st, 1, b1);
-    mma(fa, b0, 0);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) ar.sa[rt] = (int32_t)((uint32_t)ar.sa[rt] >> sshift);  // scale byte to bits 0-7
+    mma(ar, b0, 0);
     read_b(st, 2, b0);
-    mma(fa, b1, 1);
+    mma(ar, b1, 1);
     read_b(st, 3, b1);
-    mma(fa, b0, 2);
-    mma(fa, b1, 3);
-    // this wave issued 6 instructions for stage kg + 2 after stage kg + 1's: stage kg + 1 landed
-    // once at most 6 are outstanding
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(6));
+    mma(ar, b0, 2);
+    mma(ar, b1, 3);
+    load_a(min(kg + 2u, nkg - 1u), ar);
+    // issued after A(kg + 1): B(kg + 4) and A(kg + 2) (4 + 8); B(kg + 1) went out before A(kg + 1)
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(12));
     ring_barrier();
+  };
+  uint32_t kg = 0;
+  for (; kg + 1u < nkg; kg += 2u) {
+    iter(kg, ar0);
+    iter(kg + 1u, ar1);
   }
+  if (kg < nkg) iter(kg, ar0);
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the trailing reloads have landed
 
   // ---- epilogue
@@ -290,7 +307,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     const uint32_t fb = rb * (kGemmRows / 2u) + wr * 32u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+      const uint32_t tok = (uint32_t)tt * 16u + i16;
       float o[8];
       float amax = 0.0f;
 #pragma unroll
@@ -356,7 +373,7 @@ __global__ __launch_bounds__(512, 1) void expert_gemm_kernel(GemmArgs a) {
     // bias b2 added once
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t tok = wc * 64u + (uint32_t)tt * 16u + i16;
+      const uint32_t tok = (uint32_t)tt * 16u + i16;
       if (tok >= ntok) continue;
       uint16_t *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
 #pragma unroll

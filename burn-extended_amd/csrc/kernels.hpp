@@ -139,7 +139,7 @@ constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 // Grouped expert GEMM for prefill-sized batches (expert_gemm_kernel): every active expert's
 // segment is cut into tiles of kGemmTok routed tokens; a workgroup computes kGemmRows weight
 // rows x one token tile with the block-scaled MFMA (MXFP4 weights x MXFP8 hi + MXFP4 lo activations).
-constexpr uint32_t kGemmTok = 128;
+constexpr uint32_t kGemmTok = 64;
 constexpr uint32_t kGemmRows = 256;
 struct GemmArgs {
   const uint8_t *wb, *ws;  // tiled MXFP4 layout (as GemvArgs)

@@ -287,13 +287,13 @@ struct WsLayout {
 };
 
 // bf16 batches of at least kGemmMinTokens tokens with at least kGemmMinPerExpert routed tokens per
-// expert on average run the grouped GEMM (its 128-token tiles are then mostly full); the others,
-// and every f32 batch (the GEMM's two activation terms carry about 2^-6 relative precision), run the expert
-// GEMVs.  Measured crossover (per step): 20B (E = 32) GEMV 192 / 243 / 335 us against GEMM 242 /
-// 243 / 246 us at 64 / 128 / 200 tokens; 120B (E = 128) GEMV 489 / 435 us against GEMM 755 / 761
-// us at 128 / 200 tokens.
-constexpr uint64_t kGemmMinTokens = 128;
-constexpr uint64_t kGemmMinPerExpert = 16;
+// expert on average run the grouped GEMM; the others, and every f32 batch (the GEMM's two activation
+// terms carry about 2^-6 relative precision), run the expert GEMVs.  Measured per step (us, GEMV
+// against GEMM, D = F = 2880, k = 4): E = 32: 145 / 147 at 32 tokens, 175 / 144 at 64, 239 / 155 at
+// 128, 367 / 163 at 256; E = 128: 366 / 390 at 64, 469 / 439 at 128, 438 / 448 at 200, 455 / 461 at
+// 256, 796 / 494 at 512.
+constexpr uint64_t kGemmMinTokens = 64;
+constexpr uint64_t kGemmMinPerExpert = 4;
 inline bool use_gemm_path(const burnext_moe_layer &L, uint64_t n) {
   return n >= kGemmMinTokens && n * L.K >= kGemmMinPerExpert * L.E;
 }

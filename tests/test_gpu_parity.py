@@ -456,7 +456,7 @@ def test_forward_prefill_sampled_rows(M, oracle):
 
 
 # ---------------------------------------------------------------------------------------------
-# grouped-GEMM path (bf16 batches of >= 128 tokens with >= 16 routed tokens per expert on
+# grouped-GEMM path (bf16 batches of >= 64 tokens with >= 4 routed tokens per expert on
 # average): every output row against the oracle
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("D,F,E,K,n,layout,ue8,zipf", [
@@ -464,7 +464,8 @@ def test_forward_prefill_sampled_rows(M, oracle):
     (200, 96, 6, 3, 257, "halves", 14, False),        # K not a multiple of 128 or 32, tail K-groups
     (512, 384, 8, 2, 1024, "interleaved", 0, True),   # skewed segments (multi-tile experts)
     (2880, 2880, 32, 4, 512, "interleaved", 0, False),
-    (2880, 2880, 32, 4, 128, "interleaved", 0, False),  # smallest batch on the GEMM path (n*k = 16 E)
+    (2880, 2880, 32, 4, 64, "interleaved", 0, False),   # smallest batch on the GEMM path (64 tokens)
+    (2880, 2880, 128, 4, 128, "interleaved", 0, False), # 4 routed tokens per expert (n*k = 4 E)
 ])
 def test_forward_gemm_path_all_rows(M, oracle, D, F, E, K, n, layout, ue8, zipf):
     from burnext_amd import synth
