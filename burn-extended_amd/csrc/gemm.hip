@@ -82,7 +82,7 @@ __device__ __forceinline__ void ring_barrier() {
 }
 }  // namespace
 
-size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64; }
+size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64 + 2 * (kMaxExperts + 1) * 4; }
 
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
 // take a contiguous run of Q = ceil(N / 8) of the N realised items (N = nrb * token tiles, read
@@ -103,19 +103,28 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   int32_t *rows_l = (int32_t *)(smem + kStages * kStage);  // [kGemmTok] B row, -1 = none
   int32_t *slot_l = rows_l + kGemmTok;                     // [kGemmTok] down: slot
   int32_t *info_l = slot_l + kGemmTok;                     // [0] expert [1] tile of it
+  int32_t *toff_l = info_l + 16;                           // [E + 1] tile_off
+  int32_t *soff_l = toff_l + kMaxExperts + 1;              // [E + 1] seg_off
 
+  // one round trip for both prefixes (E + 1 <= 257 entries each), then the item and its expert
+  // from LDS
+  for (uint32_t t = threadIdx.x; t <= a.E; t += blockDim.x) {
+    toff_l[t] = a.tile_off[t];
+    soff_l[t] = a.seg_off[t];
+  }
+  if (threadIdx.x == 0) info_l[0] = -1;
+  __syncthreads();
   const uint32_t b = blockIdx.x;
-  const uint32_t N = a.nrb * (uint32_t)a.tile_off[a.E], Q = (N + 7u) / 8u;  // 8 * Q <= gridDim.x
+  const uint32_t NT = (uint32_t)toff_l[a.E];
+  const uint32_t N = a.nrb * NT, Q = (N + 7u) / 8u;  // 8 * Q <= gridDim.x
   const uint32_t it = (b & 7u) * Q + (b >> 3);
   if ((b >> 3) >= Q || it >= N) return;  // workgroup-uniform: no item
   // items in groups of 8 token tiles: row block rb of the group's tiles, tiles fastest
-  const uint32_t NT = (uint32_t)a.tile_off[a.E], grp = it / (8u * a.nrb), r = it - grp * 8u * a.nrb;
+  const uint32_t grp = it / (8u * a.nrb), r = it - grp * 8u * a.nrb;
   const uint32_t gsz = min(8u, NT - grp * 8u);
   const uint32_t rb = r / gsz, gt = grp * 8u + (r - rb * gsz);
-  if (threadIdx.x == 0) info_l[0] = -1;
-  __syncthreads();
   for (uint32_t e = threadIdx.x; e < a.E; e += blockDim.x) {
-    const uint32_t lo = (uint32_t)a.tile_off[e], hi = (uint32_t)a.tile_off[e + 1];
+    const uint32_t lo = (uint32_t)toff_l[e], hi = (uint32_t)toff_l[e + 1];
     if (gt >= lo && gt < hi) {
       info_l[0] = (int32_t)e;
       info_l[1] = (int32_t)(gt - lo);
@@ -124,21 +133,24 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   __syncthreads();
   const int e = info_l[0];
   if (e < 0) return;  // workgroup-uniform: beyond the realised token tiles
-  const int seg0 = a.seg_off[e];
-  const uint32_t M = (uint32_t)(a.seg_off[e + 1] - seg0);
+  const int seg0 = soff_l[e];
+  const uint32_t M = (uint32_t)(soff_l[e + 1] - seg0);
   const uint32_t m0 = (uint32_t)info_l[1] * kGemmTok;
   const uint32_t ntok = min(kGemmTok, M - m0);
-  for (uint32_t i = threadIdx.x; i < kGemmTok; i += blockDim.x) {
-    int32_t row = -1, slot = -1;
-    if (i < ntok) {
-      const int32_t pos = seg0 + (int32_t)(m0 + i);
-      slot = a.perm[pos];
-      row = GATE_UP ? slot / (int32_t)a.topk : pos;
-    }
-    rows_l[i] = row;
-    slot_l[i] = slot;
+  // B rows: gate_up reads token rows (slot / topk of the segment entries, one more round trip);
+  // down reads the segment's own rows, and its output slots are needed only by the epilogue, so
+  // their load is waited for after the K-loop
+  static_assert(kGemmTok <= 256, "one segment entry per thread");
+  // every thread loads (clamped index: no branch around the load); entries >= ntok are dropped
+  const int32_t slot_own = a.perm[seg0 + (int32_t)min(m0 + threadIdx.x, M - 1u)];
+  if (threadIdx.x < kGemmTok) {
+    const uint32_t i = threadIdx.x;
+    if (GATE_UP)
+      rows_l[i] = i < ntok ? slot_own / (int32_t)a.topk : -1;
+    else
+      rows_l[i] = i < ntok ? seg0 + (int32_t)(m0 + i) : -1;
   }
-  __syncthreads();
+  ring_barrier();  // rows_l written (LDS); down's slot load stays in flight
 
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const uint32_t wr = wv;  // this wave's 64-row quarter of the workgroup's rows
@@ -299,6 +311,10 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   }
   if (kg < nkg) iter(kg, ar0);
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the trailing reloads have landed
+  if (!GATE_UP) {
+    if (threadIdx.x < kGemmTok) slot_l[threadIdx.x] = threadIdx.x < ntok ? slot_own : -1;
+    __syncthreads();
+  }
 
   // ---- epilogue
   if constexpr (GATE_UP) {
@@ -337,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       }
       rmax = max_lanes_16_32(rmax);
       const uint32_t sbl = mx4_scale_byte(rmax);
-      const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
+      const float sl = mx4_divisor(sbl);
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
         uint8_t *dh = a.act.hi + row * a.act.kq + fb + 2u * q;
@@ -346,7 +362,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           *(uint16_t *)(dh + 8u * k) = (uint16_t)ch[k];
-          dl[4u * k] = (uint8_t)(f32_to_e2m1(res[2 * k] * il) | (f32_to_e2m1(res[2 * k + 1] * il) << 4));
+          dl[4u * k] = (uint8_t)e2m1x2<0>(0u, res[2 * k], res[2 * k + 1], sl);
         }
         if (q == 0) {
           a.act.shi[row * (a.act.kq >> 5) + (fb >> 5)] = (uint8_t)sbh;

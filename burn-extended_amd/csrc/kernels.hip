@@ -498,11 +498,13 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
           rmax = fmaxf(rmax, dpp_mov<0xB1>(rmax));
           rmax = fmaxf(rmax, dpp_mov<0x4E>(rmax));
           const uint32_t sbl = mx4_scale_byte(rmax);
-          const float il = sbl ? mx8_inv_scale(sbl) : 0.0f;
+          const float sl = mx4_divisor(sbl);
           if (tv && c0 < a.xq.kq) {
             uint32_t cl = 0u;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) cl |= f32_to_e2m1(res[k] * il) << (4 * k);
+            cl = e2m1x2<0>(cl, res[0], res[1], sl);
+            cl = e2m1x2<1>(cl, res[2], res[3], sl);
+            cl = e2m1x2<2>(cl, res[4], res[5], sl);
+            cl = e2m1x2<3>(cl, res[6], res[7], sl);
             *(uint2 *)(a.xq.hi + row * a.xq.kq + c0) = make_uint2(ch[0] | (ch[1] << 16), ch[2] | (ch[3] << 16));
             *(uint32_t *)(a.xq.lo + row * (a.xq.kq / 2u) + c0 / 2u) = cl;
             if ((lane & 3u) == 0u) {
