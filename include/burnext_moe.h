@@ -119,7 +119,7 @@ burnext_status burnext_moe_forward(burnext_moe_layer_t layer, const void *x, bur
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): burnext_moe_forward
  * with the library's own fixed scratch in place of a caller workspace.  The scratch is one 16 MiB
  * device array per GPU, held from the first layer created on that GPU until the process ends;
- * a batch whose burnext_moe_workspace_size exceeds 16 MiB (above about 120 tokens at the GPT-OSS
+ * a batch whose burnext_moe_workspace_size exceeds 16 MiB (above 128 tokens at the GPT-OSS
  * shapes) returns BURNEXT_UNSUPPORTED.  The call allocates nothing (no hipMalloc, no events: the
  * profiling hook does not time it).  Every call on one GPU shares that GPU's scratch, which keeps
  * the last call's contents: calls that overlap on one GPU (other streams or threads) race. */
