@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
   const uint8_t *wt = a.w + ((size_t)tl * a.nkg + kg0) * 1024u + lane * 16u;
 #pragma unroll
   for (uint32_t s = 0; s < kDenseMaxH; ++s)  // unconditional (clamped): a static count of loads in flight
-    wbuf[s] = *(const uint4 *)(wt + (size_t)min(s, nk - 1u) * 1024u);
+    wbuf[s] = load_stream16(wt + (size_t)min(s, nk - 1u) * 1024u);
 #pragma unroll
   for (uint32_t u = 0; u < kXq; ++u) {
     const uint32_t i = threadIdx.x + u * 256u, j = i / kq, qq = i - j * kq;
@@ -391,8 +391,16 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 template <typename KV> struct RawQ;
 template <> struct RawQ<float> { float4 v; };
 template <> struct RawQ<uint16_t> { uint2 v; };
-__device__ __forceinline__ void raw_load(const float *p, RawQ<float> &r) { r.v = *(const float4 *)p; }
-__device__ __forceinline__ void raw_load(const uint16_t *p, RawQ<uint16_t> &r) { r.v = *(const uint2 *)p; }
+// cache rows are read once per step: nontemporal loads
+__device__ __forceinline__ void raw_load(const float *p, RawQ<float> &r) {
+  const f32x4_t v = __builtin_nontemporal_load((const f32x4_t *)p);
+  r.v = make_float4(v[0], v[1], v[2], v[3]);
+}
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void raw_load(const uint16_t *p, RawQ<uint16_t> &r) {
+  const u32x2_t v = __builtin_nontemporal_load((const u32x2_t *)p);
+  r.v = make_uint2(v[0], v[1]);
+}
 __device__ __forceinline__ void raw_vals(const RawQ<float> &r, float (&v)[4]) {
   v[0] = r.v.x;
   v[1] = r.v.y;

@@ -1322,7 +1322,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     for (uint32_t j = 0; j < CJ; ++j) {
       const uint32_t kg = kg_of(h, st, j);
       const bool ok = lane_ok(h, kg);
-      av[j] = *(const uint4 *)(wt + (ok ? kg * 1024u + lane * 16u : 0u));
+      av[j] = load_stream16(wt + (ok ? kg * 1024u + lane * 16u : 0u));
       // the dword holding this lane's scale byte (byte lane & 3), kept raw until use: a byte load
       // would be re-extended at the loop back-edge, which waits for the prefetch to land
       sv[j] = *(const uint32_t *)(stp + (ok ? kg * 64u + (lane & ~3u) : 0u));

@@ -8,6 +8,14 @@ namespace burnext {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte load of weights read once per forward (nontemporal: the load does not keep the line in
+// the caches for reuse; the expert GEMVs measured 2-2.5% shorter with it at 20B T = 8)
+__device__ __forceinline__ uint4 load_stream16(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // 2^(s-127) for an e8m0 exponent byte, built from bits: s = 0 is the subnormal 2^-127,
 // s = 255 is +inf -- the values (2.0f32).powi(s - 127) gives (reference src/loader/mxfp4.rs:46,68).
