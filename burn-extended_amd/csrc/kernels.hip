@@ -1450,7 +1450,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       {
         const uint32_t nkg_ = kg_of(nh, nst_, j);
         const bool nok = lane_ok(nh, nkg_);
-        abuf[j] = *(const uint4 *)(nwt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
+        abuf[j] = load_stream16(nwt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
         sbuf[j] = *(const uint32_t *)(nsp + (nok ? nkg_ * 64u + (lane & ~3u) : 0u));
       }
       // keep each K-group's LDS reads, MFMAs and refill together (bounds the live registers)
@@ -1822,17 +1822,22 @@ __global__ __launch_bounds__(256) void swiglu_parts_kernel(SwigluPartsArgs a) {
   const uint32_t r = blockIdx.y, f = blockIdx.x * blockDim.x + threadIdx.x;
   if (f >= a.F) return;
   const float *p = a.parts + (size_t)r * a.rows_p + 2u * f;
+  float2 v[kGateUpSplit];  // every part requested before the first is summed
+#pragma unroll
+  for (uint32_t h = 0; h < kGateUpSplit; ++h) v[h] = *(const float2 *)(p + h * a.part_stride);
   float g = 0.0f, l = 0.0f;
-  for (uint32_t h = 0; h < a.nparts; ++h) {
-    const float2 v = *(const float2 *)(p + h * a.part_stride);
-    g = g + v.x;
-    l = l + v.y;
+#pragma unroll
+  for (uint32_t h = 0; h < kGateUpSplit; ++h) {
+    g = g + v[h].x;
+    l = l + v[h].y;
   }
   a.act[(size_t)r * a.act_stride + f] = swiglu_clamp_f(g, l, a.alpha, a.limit);
 }
 
 hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s) {
-  if (a.rows == 0 || a.F == 0 || 2u * a.F > a.rows_p || (a.rows_p & 1u) || (a.part_stride & 1u)) return hipErrorInvalidValue;
+  if (a.rows == 0 || a.F == 0 || 2u * a.F > a.rows_p || (a.rows_p & 1u) || (a.part_stride & 1u) ||
+      a.nparts != kGateUpSplit)
+    return hipErrorInvalidValue;
   (void)launch_kernel(swiglu_parts_kernel, dim3((a.F + 255u) / 256u, a.rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }
