@@ -1329,6 +1329,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     }
   };
   const uint32_t sshift = 8u * (lane & 3u);
+  // the dummy refills' offset into the expert's bias rows (rows_p >= 16 floats: in bounds)
+  const uint32_t dummy_off = min(lane * 16u, a.bias_estride * 4u - 16u);
 
   // Staging of the B operand for token pass `pass_`: mt rows x Kp, NT bf16 terms, zero beyond the
   // true K.  Rows: gate_up the routed tokens' xn rows, down the segment's act rows (both
@@ -1416,14 +1418,16 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const uint32_t u = my_first + tstride * ti, rt = unit_rt(u), h = unit_h(u);
     // the bias of this lane's 4 epilogue rows, requested before this step's refills
     const f32x4_t bias4 = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + rt * 16u + 4u * q);
-    // next step: next step of this tile, step 0 of the next tile, or (last step of the pass) the
-    // current step again -- a cache hit that keeps the load count static
+    // next step: next step of this tile, step 0 of the next tile, or (last step of the pass) a
+    // dummy refill that keeps the load count static: 1 KiB of the expert's bias rows, which the
+    // epilogues read, so these loads hit L2 (the weights stream with nontemporal loads)
     const bool more_st = st + 1u < nst;
     const bool more_t = ti + 1u < my_tiles;
+    const bool last = !more_st && !more_t;
     const uint32_t nu = more_st ? u : (more_t ? u + tstride : u);
     const uint32_t nrt_ = unit_rt(nu), nh = unit_h(nu);
     const uint32_t nst_ = more_st ? st + 1u : (more_t ? 0u : st);
-    const uint8_t *nwt = wexp + (size_t)nrt_ * a.nb * 256u;
+    const uint8_t *nwt = last ? (const uint8_t *)(a.bias + (size_t)e * a.bias_estride) : wexp + (size_t)nrt_ * a.nb * 256u;
     const uint8_t *nsp = sexp + (size_t)nrt_ * a.nb * 16u;
     const bool bval = i16 < mt;
     const uint16_t *brow = bs + (size_t)min(i16, mtm - 1u) * ldk;  // rows >= mt: zeroed at use
@@ -1460,7 +1464,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       {
         const uint32_t nkg_ = kg_of(nh, nst_, j);
         const bool nok = lane_ok(nh, nkg_);
-        abuf[j] = load_stream16(nwt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
+        abuf[j] = load_stream16(nwt + (last ? dummy_off : (nok ? nkg_ * 1024u + lane * 16u : 0u)));
         sbuf[j] = *(const uint32_t *)(nsp + (nok ? nkg_ * 64u + (lane & ~3u) : 0u));
       }
       // keep each K-group's LDS reads, MFMAs and refill together (bounds the live registers)
