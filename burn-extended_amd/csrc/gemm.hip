@@ -299,6 +299,19 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     read_b(st, 3, b1);
     mma(ar, b0, 2);
     mma(ar, b1, 3);
+    // schedule: tile 0's operand reads, then each next tile's reads one by one between the MFMAs
+    // of the tile before it (gate_up 474 -> 468 us at C3 against the compiler's own order)
+    __builtin_amdgcn_sched_group_barrier(0x100, 5, 0);  // 0x100: LDS reads, 0x008: MFMAs
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     load_a(min(kg + 2u, nkg - 1u), ar);
     // issued after A(kg + 1): B(kg + 4) and A(kg + 2) (4 + 8); B(kg + 1) went out before A(kg + 1)
     __builtin_amdgcn_s_waitcnt(vmcnt_only(12));
