@@ -1881,7 +1881,7 @@ __global__ __launch_bounds__(256) void combine_rows8_kernel(CombineArgs a) {
     for (uint32_t u = 0; u < 8u; ++u) {
       const uint32_t p = min(p0 + u, a.K - 1u);
       wv[u] = a.topk_w[(size_t)t * a.K + p];
-      yr[u] = *(const uint4 *)((const uint16_t *)a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 32 == 0
+      yr[u] = load_stream16((const uint16_t *)a.ypart + ((size_t)t * a.K + p) * a.Dp + d0);  // Dp % 32 == 0; read once
     }
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
