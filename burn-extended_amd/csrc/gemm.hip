@@ -329,10 +329,16 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     __syncthreads();
   }
 
-  // ---- epilogue
+  // ---- epilogue: results are staged in LDS (the stage ring is free once every wave's last
+  // direct-to-LDS loads have landed) and leave as whole 16-byte row segments: scattered 1-, 2- and
+  // 8-byte stores write each line piecewise
+  ring_barrier();
+  uint8_t *ep = smem;
   if constexpr (GATE_UP) {
     // wave wr owns features rb*128 + wr*32 .. +32: one MX block per token.  Lane (q, j) holds
     // features 8 rt + 2 q + {0, 1} (interleaved gate/linear row pairs) of its token columns.
+    // LDS: hi codes [token 64][128], lo codes [token 64][64], scale bytes [term 2][token 64][4].
+    uint8_t *hi_l = ep, *lo_l = ep + kGemmTok * 128u, *sc_l = ep + kGemmTok * 192u;
     const uint32_t fb = rb * (kGemmRows / 2u) + wr * 32u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -367,20 +373,40 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       rmax = max_lanes_16_32(rmax);
       const uint32_t sbl = mx4_scale_byte(rmax);
       const float sl = mx4_divisor(sbl);
+      // lo: features 8 k + 2 q and 8 k + 2 q + 1 of the block are one byte of e2m1 codes
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        *(uint16_t *)(hi_l + tok * 128u + wr * 32u + 8u * k + 2u * q) = (uint16_t)ch[k];
+        lo_l[tok * 64u + wr * 16u + 4u * k + q] = (uint8_t)e2m1x2<0>(0u, res[2 * k], res[2 * k + 1], sl);
+      }
+      if (q == 0) {
+        sc_l[tok * 4u + wr] = (uint8_t)sbh;
+        sc_l[(kGemmTok + tok) * 4u + wr] = (uint8_t)sbl;
+      }
+    }
+    __syncthreads();
+    // rows seg0 + m0 + tok (consecutive): hi 128 bytes, lo 64 bytes and 4 + 4 scale bytes each
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (uint32_t m = 0; m < 2u; ++m) {
+      const uint32_t c = t + 256u * m, tok = c >> 3, part = c & 7u;
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
-        uint8_t *dh = a.act.hi + row * a.act.kq + fb + 2u * q;
-        // lo: features 8 k + 2 q and 8 k + 2 q + 1 of the block are one byte of e2m1 codes
-        uint8_t *dl = a.act.lo + row * (a.act.kq / 2u) + fb / 2u + q;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          *(uint16_t *)(dh + 8u * k) = (uint16_t)ch[k];
-          dl[4u * k] = (uint8_t)e2m1x2<0>(0u, res[2 * k], res[2 * k + 1], sl);
-        }
-        if (q == 0) {
-          a.act.shi[row * (a.act.kq >> 5) + (fb >> 5)] = (uint8_t)sbh;
-          a.act.slo[row * (a.act.kq >> 5) + (fb >> 5)] = (uint8_t)sbl;
-        }
+        *(uint4 *)(a.act.hi + row * a.act.kq + rb * 128u + 16u * part) = *(const uint4 *)(hi_l + tok * 128u + 16u * part);
+      }
+    }
+    {
+      const uint32_t tok = t >> 2, part = t & 3u;
+      if (tok < ntok) {
+        const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
+        *(uint4 *)(a.act.lo + row * (a.act.kq / 2u) + rb * 64u + 16u * part) = *(const uint4 *)(lo_l + tok * 64u + 16u * part);
+      }
+    }
+    if (t < 2u * kGemmTok) {
+      const uint32_t term = t / kGemmTok, tok = t - term * kGemmTok;
+      if (tok < ntok) {
+        const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
+        *(uint32_t *)((term ? a.act.slo : a.act.shi) + row * (a.act.kq >> 5) + rb * 4u) = *(const uint32_t *)(sc_l + (term * kGemmTok + tok) * 4u);
       }
     }
     // zero the K padding of the act rows beyond the last row block's features
@@ -399,26 +425,35 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     }
   } else {
     // token-major slot rows t * topk + p in bf16 (the layer output is bf16 on this path), expert
-    // bias b2 added once
+    // bias b2 added once.  LDS: [token 64][256 rows] bf16.
+    uint16_t *o_l = (uint16_t *)ep;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const uint32_t tok = (uint32_t)tt * 16u + i16;
-      if (tok >= ntok) continue;
-      uint16_t *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        if (rb * kRowTiles + wr * 4u + (uint32_t)rt >= a.nrt) continue;
-        const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
+        const uint32_t rl = wr * 64u + (uint32_t)rt * 16u + 4u * q;  // row within the block
         const f32x4_t bb = bias4[rt];
         uint16_t o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = f32_to_bf16_bits(acc[rt][tt][r] + bb[r]);
-        if (r0 + 3u < a.out_rows) {
-          *(uint2 *)(orow + r0) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-        } else {
-          for (uint32_t r = 0; r < 4u; ++r)
-            if (r0 + r < a.out_rows) orow[r0 + r] = o[r];
-        }
+        *(uint2 *)(o_l + tok * 256u + rl) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+      }
+    }
+    __syncthreads();
+    // 64 tokens x 32 chunks of 8 rows
+    for (uint32_t c = threadIdx.x; c < kGemmTok * 32u; c += blockDim.x) {
+      const uint32_t tok = c >> 5, part = c & 31u;
+      if (tok >= ntok) continue;
+      const uint32_t r0 = rb * kGemmRows + 8u * part;
+      if (r0 >= a.out_rows) continue;
+      uint16_t *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
+      const uint16_t *src = o_l + tok * 256u + 8u * part;
+      if (r0 + 7u < a.out_rows) {
+        *(uint4 *)(orow + r0) = *(const uint4 *)src;
+      } else {
+        for (uint32_t r = 0; r < 8u; ++r)
+          if (r0 + r < a.out_rows) orow[r0 + r] = src[r];
       }
     }
   }
