@@ -338,7 +338,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     // wave wr owns features rb*128 + wr*32 .. +32: one MX block per token.  Lane (q, j) holds
     // features 8 rt + 2 q + {0, 1} (interleaved gate/linear row pairs) of its token columns.
     // LDS: hi codes [token 64][128], lo codes [token 64][64], scale bytes [term 2][token 64][4].
-    uint8_t *hi_l = ep, *lo_l = ep + kGemmTok * 128u, *sc_l = ep + kGemmTok * 192u;
+    constexpr uint32_t kHs = 144u, kLs = 80u;  // padded LDS row strides: few bank conflicts for the per-lane writes
+    uint8_t *hi_l = ep, *lo_l = ep + kGemmTok * kHs, *sc_l = ep + kGemmTok * (kHs + kLs);
     const uint32_t fb = rb * (kGemmRows / 2u) + wr * 32u;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -376,8 +377,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       // lo: features 8 k + 2 q and 8 k + 2 q + 1 of the block are one byte of e2m1 codes
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        *(uint16_t *)(hi_l + tok * 128u + wr * 32u + 8u * k + 2u * q) = (uint16_t)ch[k];
-        lo_l[tok * 64u + wr * 16u + 4u * k + q] = (uint8_t)e2m1x2<0>(0u, res[2 * k], res[2 * k + 1], sl);
+        *(uint16_t *)(hi_l + tok * kHs + wr * 32u + 8u * k + 2u * q) = (uint16_t)ch[k];
+        lo_l[tok * kLs + wr * 16u + 4u * k + q] = (uint8_t)e2m1x2<0>(0u, res[2 * k], res[2 * k + 1], sl);
       }
       if (q == 0) {
         sc_l[tok * 4u + wr] = (uint8_t)sbh;
@@ -392,14 +393,14 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       const uint32_t c = t + 256u * m, tok = c >> 3, part = c & 7u;
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
-        *(uint4 *)(a.act.hi + row * a.act.kq + rb * 128u + 16u * part) = *(const uint4 *)(hi_l + tok * 128u + 16u * part);
+        *(uint4 *)(a.act.hi + row * a.act.kq + rb * 128u + 16u * part) = *(const uint4 *)(hi_l + tok * kHs + 16u * part);
       }
     }
     {
       const uint32_t tok = t >> 2, part = t & 3u;
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
-        *(uint4 *)(a.act.lo + row * (a.act.kq / 2u) + rb * 64u + 16u * part) = *(const uint4 *)(lo_l + tok * 64u + 16u * part);
+        *(uint4 *)(a.act.lo + row * (a.act.kq / 2u) + rb * 64u + 16u * part) = *(const uint4 *)(lo_l + tok * kLs + 16u * part);
       }
     }
     if (t < 2u * kGemmTok) {
@@ -426,6 +427,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   } else {
     // token-major slot rows t * topk + p in bf16 (the layer output is bf16 on this path), expert
     // bias b2 added once.  LDS: [token 64][256 rows] bf16.
+    constexpr uint32_t kOs = 264u;  // padded row stride (elements)
     uint16_t *o_l = (uint16_t *)ep;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
         uint16_t o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = f32_to_bf16_bits(acc[rt][tt][r] + bb[r]);
-        *(uint2 *)(o_l + tok * 256u + rl) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        *(uint2 *)(o_l + tok * kOs + rl) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
       }
     }
     __syncthreads();
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       const uint32_t r0 = rb * kGemmRows + 8u * part;
       if (r0 >= a.out_rows) continue;
       uint16_t *orow = a.out + (size_t)slot_l[tok] * a.out_stride;
-      const uint16_t *src = o_l + tok * 256u + 8u * part;
+      const uint16_t *src = o_l + tok * kOs + 8u * part;
       if (r0 + 7u < a.out_rows) {
         *(uint4 *)(orow + r0) = *(const uint4 *)src;
       } else {
