@@ -16,6 +16,8 @@
 //      K [32 g, 32 g + 32) of column j.
 //   C: lane l = 16 q + j holds rows 4 q .. 4 q + 3 of column j.
 // Activations are two terms (hi + lo), so each product is two MFMAs into one accumulator.
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "mx_device.hpp"
 
@@ -30,17 +32,20 @@ namespace {
 //     a fill instruction reads 8 whole 128-byte rows (coalesced) and the 16 lanes reading one
 //     chunk of 16 consecutive tokens hit 16 distinct 16-byte bank groups;
 //   B lo codes [token 64][slot 4] x 16 bytes (64-byte fp4 rows), chunk c of token t in slot
-//     c ^ ((t >> 2) & 3): a fill instruction reads 16 whole rows, one chunk of 16 consecutive
-//     tokens again hits 16 distinct bank groups;
-//   B scale dwords [term 2][token / 32][64 lanes] (byte g = scale of K [32 g, 32 g + 32) of token
-//     32 (token / 32) + lane; lanes 32-63 repeat lanes 0-31, so one dword fill instruction per
-//     wave serves 32 tokens of one term).
+//     c ^ ((t >> 2) & 2): a fill instruction reads 16 whole rows, and the operand reads are free
+//     of bank conflicts (slot c ^ ((t >> 2) & 3) measured 2-way conflicted on gfx950).
+// The B scales come in blocks of 4 K-groups, outside the stage ring: two slots (double buffer)
+// of [term 2][token 64][16 bytes] (byte 4 k + g = scale of K [32 g, 32 g + 32) of K-group 4 j + k
+// of block j).  One 16-byte fill instruction per wave and block (32 tokens of one term, the
+// upper 32 lanes masked) replaces four gathers of 4-byte pieces: the gathers' per-row cost in the
+// address and data paths took 35 of gate_up's 412 us at C3.
 constexpr uint32_t kRowTiles = kGemmRows / 16u;
 constexpr uint32_t kBHi = 8u * kGemmTok * 16u;
 constexpr uint32_t kBData = kBHi + 4u * kGemmTok * 16u;
-constexpr uint32_t kBScale = 2u * kGemmTok * 8u;
-constexpr uint32_t kStage = kBData + kBScale;
+constexpr uint32_t kStage = kBData;
 constexpr uint32_t kStages = 5;
+constexpr uint32_t kScaleSlot = 2u * kGemmTok * 16u;
+constexpr uint32_t kScaleRing = 2u * kScaleSlot;
 constexpr uint32_t kWaves = 4;
 static_assert(kGemmTok == 64, "four waves of 64 x 64 tiles cover 256 rows x 64 tokens");
 typedef __attribute__((address_space(3))) void lds_void;
@@ -82,7 +87,7 @@ __device__ __forceinline__ void ring_barrier() {
 }
 }  // namespace
 
-size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 64 + 2 * (kMaxExperts + 1) * 4; }
+size_t gemm_lds_bytes() { return (size_t)kStages * kStage + kScaleRing + 2 * kGemmTok * 4 + 64 + 2 * (kMaxExperts + 1) * 4; }
 
 // Work item of workgroup b: blockIdx is remapped so that the workgroups of one XCD (b mod 8)
 // take a contiguous run of Q = ceil(N / 8) of the N realised items (N = nrb * token tiles, read
@@ -96,11 +101,13 @@ size_t gemm_lds_bytes() { return (size_t)kStages * kStage + 2 * kGemmTok * 4 + 6
 // tokens; wave w computes rows 64 w .. 64 w + 63 (4 x 4 MFMA tiles of 16 x 16, two terms each).
 // Weights go straight from the tiled layout into registers, two K-groups ahead (two register
 // sets); activations stream through a 5-stage LDS ring filled by direct-to-LDS loads four
-// K-groups ahead (4 instructions per wave per stage); one barrier per K-group.
+// K-groups ahead (3 instructions per wave per stage, and one per 4 K-groups for the scales);
+// one barrier per K-group.
 template <bool GATE_UP>
 __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  int32_t *rows_l = (int32_t *)(smem + kStages * kStage);  // [kGemmTok] B row, -1 = none
+  uint8_t *scl = smem + kStages * kStage;                      // B scale blocks [slot 2]
+  int32_t *rows_l = (int32_t *)(scl + kScaleRing);              // [kGemmTok] B row, -1 = none
   int32_t *slot_l = rows_l + kGemmTok;                     // [kGemmTok] down: slot
   int32_t *info_l = slot_l + kGemmTok;                     // [0] expert [1] tile of it
   int32_t *toff_l = info_l + 16;                           // [E + 1] tile_off
@@ -156,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   const uint32_t wr = wv;  // this wave's 64-row quarter of the workgroup's rows
   const uint32_t i16 = lane & 15u, q = lane >> 4;
   const uint32_t nkg = (a.nb + 3u) >> 2, tail = a.nb - 4u * (nkg - 1u);
-  const uint32_t kq = a.b.kq, sq = kq >> 5;  // code bytes and scale bytes per B row
+  const uint32_t kq = a.b.kq, ss = a.b.ss;  // code bytes and scale bytes per B row
   const uint8_t *wexp = a.wb + (size_t)e * a.wb_estride;
   const uint8_t *sexp = a.ws + (size_t)e * a.ws_estride;
   auto lane_ok = [&](uint32_t kg) { return kg < nkg && q < (kg + 1u == nkg ? tail : 4u); };
@@ -165,7 +172,11 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   // row and row tiles beyond the expert its last one; their results are never stored.
   // B hi codes: instruction m (< 2) of wave wv fills tokens 8 (wv + 4 m) + lane / 8; this lane's
   // two tokens and its swizzled chunk.  B lo codes: wave wv's one instruction fills tokens
-  // 16 wv + lane / 4, chunk lane & 3 into slot (lane & 3) ^ ((token >> 2) & 3).
+  // 16 wv + lane / 4, chunk lane & 3 into slot (lane & 3) ^ ((token >> 2) & 2).  On gfx950 the
+  // operand reads of this layout are conflict free, while slot (lane & 3) ^ ((token >> 2) & 3),
+  // free under a plain 64-bank model, measured 2-way conflicted (LDS bank-conflict counters over
+  // all 256 XOR maps of token bits into the slot: only token bits 2-3 matter, and bit 3 alone
+  // into slot bit 1 is one of the conflict-free maps).
   const uint32_t tk0 = 8u * wv + (lane >> 3), tk1 = tk0 + 32u;
   const int32_t rk0 = rows_l[tk0], rk1 = rows_l[tk1];
   const size_t browk0 = (size_t)(rk0 >= 0 ? rk0 : rows_l[0]) * kq, browk1 = (size_t)(rk1 >= 0 ? rk1 : rows_l[0]) * kq;
@@ -173,8 +184,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   const uint32_t tkl = 16u * wv + (lane >> 2);
   const int32_t rkl = rows_l[tkl];
   const size_t browl = (size_t)(rkl >= 0 ? rkl : rows_l[0]) * (kq / 2u);
-  const uint32_t lchunk = ((lane & 3u) ^ ((tkl >> 2) & 3u)) * 16u;
-  // B scales: term wv / 2, token 32 (wv % 2) + lane % 32
+  const uint32_t lchunk = ((lane & 3u) ^ ((tkl >> 2) & 2u)) * 16u;
+  // B scale blocks: term wv / 2, token 32 (wv % 2) + lane (lanes < 32)
   const int32_t rsl = rows_l[32u * (wv & 1u) + (lane & 31u)];
   const size_t rows = (size_t)(rsl >= 0 ? rsl : rows_l[0]);
   // this wave's 4 row tiles (clamped to the expert's last)
@@ -198,11 +209,12 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       const uint8_t *src = a.b.lo + browl + kg * 64u + lchunk;
       __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBHi + wv * 1024u), 16, 0, 0);
     }
-    {  // B scales: term wv / 2, tokens 32 (wv % 2) + lane % 32 (lanes 32-63 repeat lanes 0-31 into
-       // the unused half of the wave's 256 bytes)
-      const uint8_t *src = (wv >= 2u ? a.b.slo : a.b.shi) + rows * sq + kg * 4u;
-      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + kBData + wv * 256u), 4, 0, 0);
-    }
+  };
+  // B scale block j (K-groups 4 j .. 4 j + 3) into slot p: 16 bytes per token and term
+  auto stage_scales = [&](uint32_t j, uint32_t p) {
+    const uint8_t *src = (wv >= 2u ? a.b.slo : a.b.shi) + rows * ss + j * 16u;
+    if (lane < 32u)
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(scl + p * kScaleSlot + wv * 512u), 16, 0, 0);
   };
 
   f32x4_t acc[4][4];
@@ -236,7 +248,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);  // the wait counts below assume this issue order
   };
 
-  auto read_b = [&](const uint8_t *st, int tt, BFrag &f) {
+  // st: the K-group's stage; sc: its scale block slot plus 4 (K-group mod 4)
+  auto read_b = [&](const uint8_t *st, const uint8_t *sc, int tt, BFrag &f) {
     const uint32_t tok = (uint32_t)tt * 16u + i16;
     // lane group q: hi chunks q and 4 + q (K [16 q, +16) and [64 + 16 q, +16)); lo chunk q
     // (K [32 q, +32))
@@ -244,12 +257,11 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     const uint8_t *r = st + tok * 128u;
     const uint32_t s1 = (q ^ sw) * 16u, s2 = ((4u + q) ^ sw) * 16u;
     const i32x4_t h0 = *(const i32x4_t *)(r + s1), h1 = *(const i32x4_t *)(r + s2);
-    const i32x4_t l0 = *(const i32x4_t *)(st + kBHi + tok * 64u + (q ^ ((tok >> 2) & 3u)) * 16u);
+    const i32x4_t l0 = *(const i32x4_t *)(st + kBHi + tok * 64u + (q ^ ((tok >> 2) & 2u)) * 16u);
     f.Bh = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
     f.Bl = __builtin_shufflevector(l0, z4, 0, 1, 2, 3, 4, 5, 6, 7);
-    const uint32_t so = kBData + (tok >> 5) * 256u + (tok & 31u) * 4u + q;
-    f.sbh = st[so];
-    f.sbl = st[so + kBScale / 2u];
+    f.sbh = sc[tok * 16u + q];
+    f.sbl = sc[kGemmTok * 16u + tok * 16u + q];
   };
   const uint32_t sshift = 8u * (lane & 3u);
   auto mma = [&](const AFrag &fa, const BFrag &fb, int tt) {
@@ -274,29 +286,37 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
     bias4[rt] = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
   }
-  // B stages of K-groups 0..3, then A of K-groups 0 and 1 (loads complete in order).  The
-  // compiler must not reorder these groups: the s_waitcnt counts below assume this issue order.
+  // B stages of K-groups 0..3 and scale block 0, then A of K-groups 0 and 1 (loads complete in
+  // order).  The compiler must not reorder these groups: the s_waitcnt counts below assume this
+  // issue order.
 #pragma unroll
   for (uint32_t j = 0; j < kStages - 1u; ++j) stage(min(j, nkg - 1u), j);
+  stage_scales(0, 0);
   __builtin_amdgcn_sched_barrier(0);
   AFrag ar0, ar1;
   load_a(0, ar0);
   load_a(min(1u, nkg - 1u), ar1);
   __builtin_amdgcn_s_waitcnt(vmcnt_only(8));  // A(0) and every B stage before it landed
   ring_barrier();
-  auto iter = [&](uint32_t kg, AFrag &ar) {
+  // K-group kg at position P = kg mod 4 of its scale block (a compile-time constant: the block
+  // loads, one per 4 K-groups, change the wait count)
+  auto iter = [&](uint32_t kg, AFrag &ar, auto P) {
+    constexpr uint32_t kP = decltype(P)::value;
     stage(min(kg + kStages - 1u, nkg - 1u), (kg + kStages - 1u) % kStages);  // the slot every wave left
+    // the next scale block into the slot of the previous one (every wave is past its last K-group)
+    if constexpr (kP == 0u) stage_scales(min((kg >> 2) + 1u, (nkg - 1u) >> 2), ((kg >> 2) + 1u) & 1u);
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t *st = smem + (kg % kStages) * kStage;
+    const uint8_t *sc = scl + ((kg >> 2) & 1u) * kScaleSlot + kP * 4u;
     BFrag b0, b1;
-    read_b(st, 0, b0);
-    read_b(st, 1, b1);
+    read_b(st, sc, 0, b0);
+    read_b(st, sc, 1, b1);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) ar.sa[rt] = (int32_t)((uint32_t)ar.sa[rt] >> sshift);  // scale byte to bits 0-7
     mma(ar, b0, 0);
-    read_b(st, 2, b0);
+    read_b(st, sc, 2, b0);
     mma(ar, b1, 1);
-    read_b(st, 3, b1);
+    read_b(st, sc, 3, b1);
     mma(ar, b0, 2);
     mma(ar, b1, 3);
     // schedule: tile 0's operand reads, then each next tile's reads one by one between the MFMAs
@@ -313,16 +333,25 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     load_a(min(kg + 2u, nkg - 1u), ar);
-    // issued after A(kg + 1): B(kg + 4) and A(kg + 2) (4 + 8); B(kg + 1) went out before A(kg + 1)
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(12));
+    // issued after A(kg + 1): B(kg + 4), at position 0 a scale block, and A(kg + 2) (3 [+ 1] + 8);
+    // B(kg + 1) and kg + 1's scale block went out before A(kg + 1)
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(kP == 0u ? 12 : 11));
     ring_barrier();
   };
+  using P0 = std::integral_constant<uint32_t, 0>;
+  using P1 = std::integral_constant<uint32_t, 1>;
+  using P2 = std::integral_constant<uint32_t, 2>;
+  using P3 = std::integral_constant<uint32_t, 3>;
   uint32_t kg = 0;
-  for (; kg + 1u < nkg; kg += 2u) {
-    iter(kg, ar0);
-    iter(kg + 1u, ar1);
+  for (; kg + 3u < nkg; kg += 4u) {
+    iter(kg, ar0, P0{});
+    iter(kg + 1u, ar1, P1{});
+    iter(kg + 2u, ar0, P2{});
+    iter(kg + 3u, ar1, P3{});
   }
-  if (kg < nkg) iter(kg, ar0);
+  if (kg < nkg) iter(kg, ar0, P0{});
+  if (kg + 1u < nkg) iter(kg + 1u, ar1, P1{});
+  if (kg + 2u < nkg) iter(kg + 2u, ar0, P2{});
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the trailing reloads have landed
   if (!GATE_UP) {
     if (threadIdx.x < kGemmTok) slot_l[threadIdx.x] = threadIdx.x < ntok ? slot_own : -1;
@@ -407,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       const uint32_t term = t / kGemmTok, tok = t - term * kGemmTok;
       if (tok < ntok) {
         const size_t row = (size_t)(seg0 + (int32_t)(m0 + tok));
-        *(uint32_t *)((term ? a.act.slo : a.act.shi) + row * (a.act.kq >> 5) + rb * 4u) = *(const uint32_t *)(sc_l + (term * kGemmTok + tok) * 4u);
+        *(uint32_t *)((term ? a.act.slo : a.act.shi) + row * a.act.ss + rb * 4u) = *(const uint32_t *)(sc_l + (term * kGemmTok + tok) * 4u);
       }
     }
     // zero the K padding of the act rows beyond the last row block's features
@@ -419,8 +448,8 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
         a.act.hi[row * a.act.kq + f_end + c] = 0;
         if ((c & 1u) == 0u) a.act.lo[row * (a.act.kq / 2u) + (f_end + c) / 2u] = 0;
         if ((c & 31u) == 0u) {
-          a.act.shi[row * (a.act.kq >> 5) + ((f_end + c) >> 5)] = 0;
-          a.act.slo[row * (a.act.kq >> 5) + ((f_end + c) >> 5)] = 0;
+          a.act.shi[row * a.act.ss + ((f_end + c) >> 5)] = 0;
+          a.act.slo[row * a.act.ss + ((f_end + c) >> 5)] = 0;
         }
       }
     }
@@ -469,7 +498,10 @@ hipError_t configure_gemm_kernels() {
 }
 
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s) {
-  if (grid == 0 || (grid & 7u) != 0 || a.nrb == 0 || a.b.kq % 128u != 0) return hipErrorInvalidValue;
+  // B scale rows hold whole 16-byte blocks of 4 K-groups (ss >= kq / 32, a multiple of 16)
+  if (grid == 0 || (grid & 7u) != 0 || a.nrb == 0 || a.b.kq % 128u != 0 || a.b.ss % 16u != 0 || a.b.ss * 32u < a.b.kq)
+    return hipErrorInvalidValue;
+  if (gate_up && (a.act.kq % 128u != 0 || a.act.ss * 32u < a.act.kq)) return hipErrorInvalidValue;
   if (gate_up)
     (void)launch_kernel(expert_gemm_kernel<true>, dim3(grid), dim3(64 * kWaves), gemm_lds_bytes(), s, a);
   else

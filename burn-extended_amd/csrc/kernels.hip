@@ -278,7 +278,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
       }
       const size_t row = t0 + tt;
       mx84_quantize32(v, amax, a.xq.hi + row * a.xq.kq + bk * 32u, a.xq.lo + row * (a.xq.kq / 2u) + bk * 16u,
-                      a.xq.shi + row * nbk + bk, a.xq.slo + row * nbk + bk);
+                      a.xq.shi + row * a.xq.ss + bk, a.xq.slo + row * a.xq.ss + bk);
     }
   }
 
@@ -457,7 +457,6 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
   // two-term form zero padded to the K-group length; written before the dot products so
   // the stores drain meanwhile
   if (active && (a.xn || a.xq.hi)) {
-    const uint32_t nbk = a.xq.kq >> 5;
 #pragma unroll
     for (int i = 0; i < RC; ++i) {
       const uint32_t c0 = 512u * i + 8u * lane;
@@ -508,8 +507,8 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
             *(uint2 *)(a.xq.hi + row * a.xq.kq + c0) = make_uint2(ch[0] | (ch[1] << 16), ch[2] | (ch[3] << 16));
             *(uint32_t *)(a.xq.lo + row * (a.xq.kq / 2u) + c0 / 2u) = cl;
             if ((lane & 3u) == 0u) {
-              a.xq.shi[row * nbk + (c0 >> 5)] = (uint8_t)sbh;
-              a.xq.slo[row * nbk + (c0 >> 5)] = (uint8_t)sbl;
+              a.xq.shi[row * a.xq.ss + (c0 >> 5)] = (uint8_t)sbh;
+              a.xq.slo[row * a.xq.ss + (c0 >> 5)] = (uint8_t)sbl;
             }
           }
         }

@@ -30,11 +30,12 @@ inline hipError_t launch_kernel(void (*k)(A), dim3 grid, dim3 block, size_t lds,
 // The grouped GEMM's activation rows (see mx_device.hpp): kq codes per row, K padded to whole
 // 128-wide K-groups with zero codes and zero scale bytes, natural K order -- the hi term as MXFP8
 // (kq bytes per row), the lo term as MXFP4 (kq / 2 bytes per row, two codes per byte); kq / 32
-// scale bytes per row and term.
+// scale bytes per row and term, in rows of ss = kq / 32 rounded up to 16 bytes (the GEMM stages
+// the scales of 4 K-groups of a row with one 16-byte load; the bytes past kq / 32 are not used).
 struct QRows {
   uint8_t *hi, *lo;    // [rows, kq], [rows, kq / 2]
-  uint8_t *shi, *slo;  // [rows, kq / 32]
-  uint32_t kq;
+  uint8_t *shi, *slo;  // [rows, ss]
+  uint32_t kq, ss;
 };
 
 // Router logits for a block of tokens x a group of experts.  With apply_norm the rows are the

@@ -301,6 +301,8 @@ inline bool use_gemm_path(const burnext_moe_layer &L, uint64_t n) {
 // Codes per row of the GEMM's activation rows over K = cols of a tiled projection (whole 128-wide
 // K-groups): the hi term's bytes; the lo term takes half as many.
 inline uint32_t qrow_bytes(const TiledMx &t) { return ((t.nb + 3u) / 4u) * 128u; }
+// Scale bytes per row and term of those rows: one per 32 codes, rows padded to 16 bytes.
+inline uint32_t qscale_bytes(const TiledMx &t) { return (uint32_t)align_up(qrow_bytes(t) / 32u, 16); }
 
 // Largest batch m <= min(n, kSmallRouteMaxTokens) that still splits gate_up in K-parts (0: none).
 // gate_up_split holds for m = 1 .. some bound, since the touched-expert bound min(E, m k) grows
@@ -343,12 +345,12 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     const uint64_t kx = qrow_bytes(L.w1), ka = qrow_bytes(L.w2);
     w.xq[0] = take(n * kx);
     w.xq[1] = take(n * kx / 2);  // e2m1 lo codes, two per byte
-    w.xq[2] = take(n * kx / 32);
-    w.xq[3] = take(n * kx / 32);
+    w.xq[2] = take(n * qscale_bytes(L.w1));
+    w.xq[3] = take(n * qscale_bytes(L.w1));
     w.aq[0] = take(nk * ka);
     w.aq[1] = take(nk * ka / 2);
-    w.aq[2] = take(nk * ka / 32);
-    w.aq[3] = take(nk * ka / 32);
+    w.aq[2] = take(nk * qscale_bytes(L.w2));
+    w.aq[3] = take(nk * qscale_bytes(L.w2));
   }
   // decode-sized batches split the down projection's K range in parts (kDownSplitFew when gate_up
   // is split too, else kDownSplit): a partial-sum buffer each, sized for the largest m <= n
@@ -389,8 +391,8 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.xn = b + w.xn;
   if (w.gemm) {
     p.tile_off = (int32_t *)(b + w.tile_off);
-    p.xq = QRows{b + w.xq[0], b + w.xq[1], b + w.xq[2], b + w.xq[3], qrow_bytes(L.w1)};
-    p.aq = QRows{b + w.aq[0], b + w.aq[1], b + w.aq[2], b + w.aq[3], qrow_bytes(L.w2)};
+    p.xq = QRows{b + w.xq[0], b + w.xq[1], b + w.xq[2], b + w.xq[3], qrow_bytes(L.w1), qscale_bytes(L.w1)};
+    p.aq = QRows{b + w.aq[0], b + w.aq[1], b + w.aq[2], b + w.aq[3], qrow_bytes(L.w2), qscale_bytes(L.w2)};
   }
   p.perm = (int32_t *)(b + w.perm);
   p.pos_of = (int32_t *)(b + w.pos_of);
