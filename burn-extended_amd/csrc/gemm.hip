@@ -188,15 +188,16 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   // B scale blocks: term wv / 2, token 32 (wv % 2) + lane (lanes < 32)
   const int32_t rsl = rows_l[32u * (wv & 1u) + (lane & 31u)];
   const size_t rows = (size_t)(rsl >= 0 ? rsl : rows_l[0]);
-  // this wave's 4 row tiles (clamped to the expert's last)
+  // this wave's 4 row tiles (clamped to the expert's last) and their group in the GEMM's scale
+  // copy (clamped to the last group: rows beyond the expert are never stored)
   const uint8_t *arow[4];
-  const uint8_t *srow[4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     const uint32_t t = min(rb * kRowTiles + wr * 4u + (uint32_t)rt, a.nrt - 1u);
     arow[rt] = wexp + (size_t)t * a.nb * 256u + lane * 16u;
-    srow[rt] = sexp + (size_t)t * a.nb * 16u + (lane & ~3u);
   }
+  const uint32_t nkq = (nkg + 3u) >> 2, ngr = (a.nrt + 3u) >> 2;
+  const uint8_t *srow = sexp + (size_t)min(rb * (kRowTiles / 4u) + wr, ngr - 1u) * nkq * 1024u + lane * 16u;
   auto stage = [&](uint32_t kg, uint32_t p) {
     uint8_t *st = smem + p * kStage;
 #pragma unroll
@@ -224,11 +225,10 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     for (int tt = 0; tt < 4; ++tt) acc[rt][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // MFMA operands: the A operands (row tiles) of a K-group, and the B operands of one token tile.
-  // A scales are whole dwords of the tiled scale layout: byte lane & 3 is this lane's, shifted to
-  // bits 0-7 (the scale operand's byte 0) before use.
+  // The A scales of 4 K-groups come in one 16-byte load (dword rt: byte k = K-group 4 j + k of row
+  // tile rt); the MFMA picks byte k by the scale operand's op_sel.
   struct AFrag {
     i32x4_t A[4];
-    int32_t sa[4];
   };
   struct BFrag {
     i32x8_t Bh, Bl;
@@ -236,16 +236,18 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
   };
   const i32x4_t z4 = {0, 0, 0, 0};
   // A straight from the tiled weights into registers.  Lanes outside the last K-group's blocks read
-  // the row tile's first block (finite fp4 codes, scale byte < 255 for finite weights): the B rows
+  // the row tile's first block (finite fp4 codes; their scale byte in the copy is 0): the B rows
   // are zero beyond K (codes 0 in the K padding of xq and act), so their products add zeros.
   auto load_a = [&](uint32_t kg, AFrag &f) {
-    const bool ok = lane_ok(kg);
-    const uint32_t off = ok ? kg * 1024u : 0u, soff = ok ? kg * 64u : 0u;
+    const uint32_t off = lane_ok(kg) ? kg * 1024u : 0u;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) f.A[rt] = *(const i32x4_t *)(arow[rt] + off);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) f.sa[rt] = *(const int32_t *)(srow[rt] + soff);  // byte lane & 3 is ours
     __builtin_amdgcn_sched_barrier(0);  // the wait counts below assume this issue order
+  };
+  // A scales of K-groups 4 j .. 4 j + 3 (lanes beyond the blocks read scale byte 0)
+  auto load_as = [&](uint32_t j, i32x4_t &s4) {
+    s4 = *(const i32x4_t *)(srow + j * 1024u);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // st: the K-group's stage; sc: its scale block slot plus 4 (K-group mod 4)
@@ -263,17 +265,18 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     f.sbh = sc[tok * 16u + q];
     f.sbl = sc[kGemmTok * 16u + tok * 16u + q];
   };
-  const uint32_t sshift = 8u * (lane & 3u);
-  auto mma = [&](const AFrag &fa, const BFrag &fb, int tt) {
+  // KP: the K-group's position in its scale block, the op_sel byte of the A scale dwords
+  auto mma = [&](const AFrag &fa, const i32x4_t &sa, const BFrag &fb, int tt, auto KP) {
+    constexpr int kp = (int)decltype(KP)::value;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const i32x8_t A8 = __builtin_shufflevector(fa.A[rt], z4, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bh, acc[rt][tt], 4, 0, 0, fa.sa[rt], 0, fb.sbh);
+      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bh, acc[rt][tt], 4, 0, kp, sa[rt], 0, fb.sbh);
     }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const i32x8_t A8 = __builtin_shufflevector(fa.A[rt], z4, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bl, acc[rt][tt], 4, 4, 0, fa.sa[rt], 0, fb.sbl);
+      acc[rt][tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A8, fb.Bl, acc[rt][tt], 4, 4, kp, sa[rt], 0, fb.sbl);
     }
   };
 
@@ -286,17 +289,19 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     const uint32_t r0 = rb * kGemmRows + wr * 64u + (uint32_t)rt * 16u + 4u * q;
     bias4[rt] = *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + min(r0, a.bias_estride - 4u));
   }
-  // B stages of K-groups 0..3 and scale block 0, then A of K-groups 0 and 1 (loads complete in
-  // order).  The compiler must not reorder these groups: the s_waitcnt counts below assume this
-  // issue order.
+  // B stages of K-groups 0..3 and scale block 0, then A of K-group 0, A scale block 0 and A of
+  // K-group 1 (loads complete in order).  The compiler must not reorder these groups: the
+  // s_waitcnt counts below assume this issue order.
 #pragma unroll
   for (uint32_t j = 0; j < kStages - 1u; ++j) stage(min(j, nkg - 1u), j);
   stage_scales(0, 0);
   __builtin_amdgcn_sched_barrier(0);
   AFrag ar0, ar1;
+  i32x4_t sa_cur, sa_nxt;  // A scales of the current block, and of the next (loaded at position 2)
   load_a(0, ar0);
+  load_as(0, sa_cur);
   load_a(min(1u, nkg - 1u), ar1);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(8));  // A(0) and every B stage before it landed
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(4));  // A(0), its scales and every B stage before them landed
   ring_barrier();
   // K-group kg at position P = kg mod 4 of its scale block (a compile-time constant: the block
   // loads, one per 4 K-groups, change the wait count)
@@ -311,14 +316,12 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     BFrag b0, b1;
     read_b(st, sc, 0, b0);
     read_b(st, sc, 1, b1);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) ar.sa[rt] = (int32_t)((uint32_t)ar.sa[rt] >> sshift);  // scale byte to bits 0-7
-    mma(ar, b0, 0);
+    mma(ar, sa_cur, b0, 0, P);
     read_b(st, sc, 2, b0);
-    mma(ar, b1, 1);
+    mma(ar, sa_cur, b1, 1, P);
     read_b(st, sc, 3, b1);
-    mma(ar, b0, 2);
-    mma(ar, b1, 3);
+    mma(ar, sa_cur, b0, 2, P);
+    mma(ar, sa_cur, b1, 3, P);
     // schedule: tile 0's operand reads, then each next tile's reads one by one between the MFMAs
     // of the tile before it (gate_up 474 -> 468 us at C3 against the compiler's own order)
     __builtin_amdgcn_sched_group_barrier(0x100, 5, 0);  // 0x100: LDS reads, 0x008: MFMAs
@@ -333,9 +336,13 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     load_a(min(kg + 2u, nkg - 1u), ar);
-    // issued after A(kg + 1): B(kg + 4), at position 0 a scale block, and A(kg + 2) (3 [+ 1] + 8);
-    // B(kg + 1) and kg + 1's scale block went out before A(kg + 1)
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(kP == 0u ? 12 : 11));
+    // at position 2, the next block's A scales (needed from K-group kg + 2 on)
+    if constexpr (kP == 2u) load_as(min((kg >> 2) + 1u, nkq - 1u), sa_nxt);
+    // issued after A(kg + 1): B(kg + 4), at position 0 a B scale block, A(kg + 2) and at position 2
+    // the A scale block (3 [+ 1] + 4 [+ 1]); B(kg + 1) and kg + 1's B scale block went out before
+    // A(kg + 1).  At position 3 the A scale block issued after A(kg + 1) is waited for too (3 + 4).
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(kP == 0u || kP == 2u ? 8 : 7));
+    if constexpr (kP == 3u) sa_cur = sa_nxt;
     ring_barrier();
   };
   using P0 = std::integral_constant<uint32_t, 0>;

@@ -143,7 +143,8 @@ constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 constexpr uint32_t kGemmTok = 64;
 constexpr uint32_t kGemmRows = 256;
 struct GemmArgs {
-  const uint8_t *wb, *ws;  // tiled MXFP4 layout (as GemvArgs)
+  const uint8_t *wb, *ws;  // tiled MXFP4 codes (as GemvArgs); scales in the GEMM's copy (groups of
+                           // 4 row tiles x blocks of 4 K-groups, 16 bytes per lane)
   uint64_t wb_estride, ws_estride;
   const float *bias;       // [E, rows_p]
   uint32_t bias_estride;

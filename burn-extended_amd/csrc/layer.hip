@@ -77,8 +77,13 @@ burnext_status set_error(burnext_status st, const std::string &msg) { return fai
 // Tiled MXFP4 layout of one projection (see the expert_gemv comment in kernels.hip).
 struct TiledMx {
   uint32_t rows = 0, rows_p = 0, cols = 0, nb = 0, nrt = 0;
-  uint64_t blocks_per_expert = 0, scales_per_expert = 0;
+  uint64_t blocks_per_expert = 0, scales_per_expert = 0, gscales_per_expert = 0;
   uint8_t *blocks = nullptr, *scales = nullptr;
+  // the grouped GEMM's copy of the scales: per group of 4 row tiles and block of 4 K-groups, lane
+  // l's 16 bytes hold its scale byte of row tile 4 g + r and K-group 4 j + k at byte 4 r + k (one
+  // 16-byte load per wave and 4 K-groups instead of 16 single-dword loads); zero where the row
+  // tile or the block does not exist
+  uint8_t *gscales = nullptr;
 };
 
 struct burnext_moe_layer {
@@ -157,7 +162,8 @@ void repack_expert(const uint8_t *src_b, const uint8_t *src_s, uint64_t bpr, uin
 // so create can prepare everything before it touches the GPU).
 burnext_status repack_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols, const uint8_t *blocks,
                             const uint8_t *scales, const burnext_mxfp4_desc &d, bool is_w1, uint32_t F,
-                            burnext_gate_up_layout layout, std::vector<uint8_t> &hb, std::vector<uint8_t> &hs) {
+                            burnext_gate_up_layout layout, std::vector<uint8_t> &hb, std::vector<uint8_t> &hs,
+                            std::vector<uint8_t> &hg) {
   t.rows = rows;
   t.rows_p = (uint32_t)align_up(rows, 16);
   t.cols = cols;
@@ -165,9 +171,12 @@ burnext_status repack_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols
   t.nrt = t.rows_p / 16;
   t.blocks_per_expert = (uint64_t)t.rows_p * t.nb * 16;
   t.scales_per_expert = (uint64_t)t.rows_p * t.nb;
+  const uint32_t nkg = (t.nb + 3u) / 4u, nkq = (nkg + 3u) / 4u, ngr = (t.nrt + 3u) / 4u;
+  t.gscales_per_expert = (uint64_t)ngr * nkq * 1024u;
   try {
     hb.resize(t.blocks_per_expert * E);
     hs.resize(t.scales_per_expert * E);
+    hg.assign(t.gscales_per_expert * E, 0);
   } catch (const std::bad_alloc &) {
     return fail(BURNEXT_OUT_OF_MEMORY, "host allocation failed while repacking MXFP4 weights");
   }
@@ -183,14 +192,30 @@ burnext_status repack_tiled(TiledMx &t, uint32_t E, uint32_t rows, uint32_t cols
     });
   }
   for (auto &th : pool) th.join();
+  // the GEMM's scale copy, from the tiled scales (byte kg * 64 + l of row tile rt; lanes whose
+  // block 4 kg + l / 16 is beyond nb stay zero)
+  for (uint32_t e = 0; e < E; ++e) {
+    const uint8_t *se = hs.data() + e * t.scales_per_expert;
+    uint8_t *ge = hg.data() + e * t.gscales_per_expert;
+    for (uint32_t rt = 0; rt < t.nrt; ++rt)
+      for (uint32_t kg = 0; kg < nkg; ++kg)
+        for (uint32_t l = 0; l < 64; ++l) {
+          if (4u * kg + l / 16u >= t.nb) continue;
+          const uint64_t dst = (((uint64_t)(rt / 4u) * nkq + kg / 4u) * 64u + l) * 16u + (rt % 4u) * 4u + kg % 4u;
+          ge[dst] = se[(uint64_t)rt * t.nb * 16u + kg * 64u + l];
+        }
+  }
   return BURNEXT_OK;
 }
 
-burnext_status upload_tiled(TiledMx &t, const std::vector<uint8_t> &hb, const std::vector<uint8_t> &hs) {
-  if (hipMalloc(&t.blocks, hb.size()) != hipSuccess || hipMalloc(&t.scales, hs.size()) != hipSuccess)
+burnext_status upload_tiled(TiledMx &t, const std::vector<uint8_t> &hb, const std::vector<uint8_t> &hs,
+                            const std::vector<uint8_t> &hg) {
+  if (hipMalloc(&t.blocks, hb.size()) != hipSuccess || hipMalloc(&t.scales, hs.size()) != hipSuccess ||
+      hipMalloc(&t.gscales, hg.size()) != hipSuccess)
     return fail(BURNEXT_OUT_OF_MEMORY, "hipMalloc failed for MXFP4 weights");
   if (hipMemcpy(t.blocks, hb.data(), hb.size(), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(t.scales, hs.data(), hs.size(), hipMemcpyHostToDevice) != hipSuccess)
+      hipMemcpy(t.scales, hs.data(), hs.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(t.gscales, hg.data(), hg.size(), hipMemcpyHostToDevice) != hipSuccess)
     return fail(BURNEXT_DEVICE_ERROR, "hipMemcpy of MXFP4 weights failed");
   return BURNEXT_OK;
 }
@@ -208,7 +233,8 @@ void free_layer(burnext_moe_layer *L) {
   if (!L) return;
   DeviceGuard g(L->device);
   if (L->router_wg == L->router_w) L->router_wg = nullptr;
-  for (void *p : {(void *)L->w1.blocks, (void *)L->w1.scales, (void *)L->w2.blocks, (void *)L->w2.scales,
+  for (void *p : {(void *)L->w1.blocks, (void *)L->w1.scales, (void *)L->w1.gscales, (void *)L->w2.blocks,
+                  (void *)L->w2.scales, (void *)L->w2.gscales,
                   (void *)L->b1, (void *)L->b2, L->router_w, L->router_wg, (void *)L->router_b, (void *)L->gamma})
     if (p) (void)hipFree(p);
   for (auto &pp : L->prof) {
@@ -612,9 +638,9 @@ burnext_status forward_gemm(burnext_moe_layer *L, const void *x, bool xb, uint64
     const TiledMx &t = up ? L->w1 : L->w2;
     GemmArgs g{};
     g.wb = t.blocks;
-    g.ws = t.scales;
+    g.ws = t.gscales;
     g.wb_estride = t.blocks_per_expert;
-    g.ws_estride = t.scales_per_expert;
+    g.ws_estride = t.gscales_per_expert;
     g.bias = up ? L->b1 : L->b2;
     g.bias_estride = t.rows_p;
     g.nrt = t.nrt;
@@ -726,9 +752,11 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   // host preparation (no device call): tiled experts, biases in the internal row order, gamma and
   // the gamma-folded router rows
   TiledMx t1, t2;
-  std::vector<uint8_t> hb1t, hs1t, hb2t, hs2t;
-  burnext_status st = repack_tiled(t1, E, 2 * F, D, w1_blocks, w1_scales, *w1_desc, true, F, gate_up_layout, hb1t, hs1t);
-  if (st == BURNEXT_OK) st = repack_tiled(t2, E, D, F, w2_blocks, w2_scales, *w2_desc, false, F, gate_up_layout, hb2t, hs2t);
+  std::vector<uint8_t> hb1t, hs1t, hg1t, hb2t, hs2t, hg2t;
+  burnext_status st =
+      repack_tiled(t1, E, 2 * F, D, w1_blocks, w1_scales, *w1_desc, true, F, gate_up_layout, hb1t, hs1t, hg1t);
+  if (st == BURNEXT_OK)
+    st = repack_tiled(t2, E, D, F, w2_blocks, w2_scales, *w2_desc, false, F, gate_up_layout, hb2t, hs2t, hg2t);
   if (st != BURNEXT_OK) return st;
   std::vector<float> hb1((size_t)E * t1.rows_p, 0.0f), hb2((size_t)E * t2.rows_p, 0.0f), hrb(E, 0.0f), hg(D, 1.0f);
   for (uint32_t e = 0; e < E; ++e) {
@@ -782,8 +810,8 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
   L->w1 = t1;
   L->w2 = t2;
 
-  st = upload_tiled(L->w1, hb1t, hs1t);
-  if (st == BURNEXT_OK) st = upload_tiled(L->w2, hb2t, hs2t);
+  st = upload_tiled(L->w1, hb1t, hs1t, hg1t);
+  if (st == BURNEXT_OK) st = upload_tiled(L->w2, hb2t, hs2t, hg2t);
   // biases (f32 on device), b1 permuted to the interleaved internal row order
   if (st == BURNEXT_OK) st = upload_vec(&L->b1, hb1);
   if (st == BURNEXT_OK) st = upload_vec(&L->b2, hb2);
