@@ -466,6 +466,8 @@ def test_forward_prefill_sampled_rows(M, oracle):
     (2880, 2880, 32, 4, 512, "interleaved", 0, False),
     (2880, 2880, 32, 4, 64, "interleaved", 0, False),   # smallest batch on the GEMM path (64 tokens)
     (2880, 2880, 128, 4, 128, "interleaved", 0, False), # 4 routed tokens per expert (n*k = 4 E)
+    (640, 1152, 8, 2, 256, "interleaved", 0, False),   # 5 and 9 K-groups: the K-loop's 4-group blocks plus a tail
+    (704, 608, 8, 2, 200, "halves", 0, True),          # 6 / 5 K-groups, row tiles not a whole group of 4
 ])
 def test_forward_gemm_path_all_rows(M, oracle, D, F, E, K, n, layout, ue8, zipf):
     from burnext_amd import synth
