@@ -54,12 +54,6 @@ constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 // s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima)
 constexpr int kLgkmcnt0 = 0xF | (7 << 4) | (3 << 14);
 
-// Barrier of the stage ring.  Each wave has already waited (vmcnt) for its own direct-to-LDS
-// loads of the stage the others read next; its LDS reads are complete (lgkmcnt(0)) before it
-// arrives, so a slot refilled after the barrier has no pending readers.  Loads of later stages
-// stay in flight: __syncthreads() would wait for every outstanding load (its fence covers the
-// direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
-// accesses across.
 // Clamped SwiGLU with the hardware exp2 and reciprocal (about 1 ulp each): the epilogue feeds it
 // straight into the two-term quantisation (2^-6-level), so the precise expf and division
 // of swiglu_clamp_f would only cost VALU time there.
@@ -79,6 +73,12 @@ __device__ __forceinline__ float max_lanes_16_32(float v) {
   return fmaxf(__uint_as_float(p2[0]), __uint_as_float(p2[1]));
 }
 
+// Barrier of the stage ring.  Each wave has already waited (vmcnt) for its own direct-to-LDS
+// loads of the stage the others read next; its LDS reads are complete (lgkmcnt(0)) before it
+// arrives, so a slot refilled after the barrier has no pending readers.  Loads of later stages
+// stay in flight: __syncthreads() would wait for every outstanding load (its fence covers the
+// direct-to-LDS writes).  The empty asm statements keep the compiler from moving memory
+// accesses across.
 __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
@@ -100,7 +100,8 @@ size_t gemm_lds_bytes() { return (size_t)kStages * kStage + kScaleRing + 2 * kGe
 // and waits overlap the other's MFMAs) computes kGemmRows weight rows (16 row tiles) x kGemmTok
 // tokens; wave w computes rows 64 w .. 64 w + 63 (4 x 4 MFMA tiles of 16 x 16, two terms each).
 // Weights go straight from the tiled layout into registers, two K-groups ahead (two register
-// sets); activations stream through a 5-stage LDS ring filled by direct-to-LDS loads four
+// sets), their scales from the GEMM scale copy (one 16-byte load per wave and 4 K-groups, the byte
+// picked by the MFMA's op_sel; the K-loop is unrolled by 4 for it); activations stream through a 5-stage LDS ring filled by direct-to-LDS loads four
 // K-groups ahead (3 instructions per wave per stage, and one per 4 K-groups for the scales);
 // one barrier per K-group.
 template <bool GATE_UP>
