@@ -3,7 +3,7 @@
 // Per decode step (batch rows b < B, one token each, absolute position pos):
 //   embed_kernel        hidden[b] = tok_emb[token[b]]                       (f32 residual stream)
 //   per layer l:
-//     rmsnorm_kernel    xn = RmsNorm(hidden) with norm_attn[l]
+//     rmsnorm_kernel    xn = RmsNorm(hidden) with norm_attn[l] (layer 0; see the MoE combine below)
 //     dense_gemv_kernel the fused q|k|v projection as K-part partial sums (bf16 weights on
 //                       v_mfma_f32_16x16x32_bf16, activations as two bf16 terms)
 //     qkv_post_kernel   sum of parts + bias, RoPE on q and k (YaRN table), k and v written into the
@@ -12,8 +12,10 @@
 //                       maximum, exp, sums and the weighted value sum (flash-decoding split)
 //     attn_combine_kernel  chunks merged with the learned sink in the softmax denominator
 //     dense_gemv_kernel the output projection; o_post_kernel hidden += sum + bias
-//     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels
-//   rmsnorm_kernel (norm_final), dense_gemv_kernel (LM head), logits_kernel + argmax_kernel
+//     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels;
+//                       its combine (combine_norm_kernel) also writes the next layer's xn (after
+//                       the last layer: norm_final), so rmsnorm_kernel runs for layer 0 only
+//   dense_gemv_kernel (LM head), logits_kernel + argmax_kernel
 //
 // Replaces src/models/gpt_oss.rs:101-113,226-252 and src/attention/streaming_mqa.rs:239-419
 // (Burn tensor ops on WGPU).
@@ -36,6 +38,9 @@ struct burnext_moe_layer;
 namespace burnext {
 burnext_status set_error(burnext_status st, const std::string &msg);
 void moe_layer_shape(const burnext_moe_layer *L, uint32_t *d_model, int *device);
+burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
+                                     uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
+                                     const float *gamma, float eps, float *xn, bool *norm_done);
 }  // namespace burnext
 
 using namespace burnext;
@@ -1254,10 +1259,14 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     st = hip_check(launch_kernel(embed_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, a), "embedding launch");
     if (st != BURNEXT_OK) return st;
   }
+  bool normed = false;  // xn already holds the norm the next step needs (fused into the MoE combine)
   for (uint32_t l = 0; l < c.n_layers; ++l) {
-    NormArgs na{hid, M->norm_attn + (size_t)l * D, xn, D, c.rms_eps};
-    st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, na), "RmsNorm launch");
-    if (st == BURNEXT_OK) st = dense_gemv(M->qkv[l], xn, B, part, s);
+    if (!normed) {
+      NormArgs na{hid, M->norm_attn + (size_t)l * D, xn, D, c.rms_eps};
+      st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, na), "RmsNorm launch");
+      if (st != BURNEXT_OK) return st;
+    }
+    st = dense_gemv(M->qkv[l], xn, B, part, s);
     if (st != BURNEXT_OK) return st;
     QkvPostArgs qa{};
     qa.part = part;
@@ -1310,7 +1319,11 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     OPostArgs oa{part, (uint64_t)B * D, M->wo[l].parts, D, M->bo + (size_t)l * D, hid};
     st = hip_check(launch_kernel(o_post_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, oa), "o post launch");
     if (st != BURNEXT_OK) return st;
-    st = burnext_moe_forward(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes, stream);
+    // the MoE layer; its combine also writes the next norm of the new hidden rows (the next
+    // layer's attention norm, after the last layer the final norm) when its path allows
+    const float *next_gamma = l + 1 < c.n_layers ? M->norm_attn + (size_t)(l + 1) * D : M->norm_final;
+    st = moe_forward_post_norm(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
+                               stream, next_gamma, c.rms_eps, xn, &normed);
     if (st != BURNEXT_OK) return st;
     std::swap(hid, hid2);
   }
@@ -1318,9 +1331,12 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     st = hip_check(hipMemcpyAsync(hidden, hid, (size_t)B * D * 4, hipMemcpyDeviceToDevice, s), "hidden copy");
     if (st != BURNEXT_OK) return st;
   }
-  NormArgs nf{hid, M->norm_final, xn, D, c.rms_eps};
-  st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, nf), "final RmsNorm launch");
-  if (st == BURNEXT_OK) st = dense_gemv(M->lm, xn, B, part, s);
+  if (!normed) {
+    NormArgs nf{hid, M->norm_final, xn, D, c.rms_eps};
+    st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, nf), "final RmsNorm launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  st = dense_gemv(M->lm, xn, B, part, s);
   if (st != BURNEXT_OK) return st;
   LogitsArgs la{part, (uint64_t)B * c.vocab_size, M->lm.parts, c.vocab_size, w.nblk, logits, bval, bidx};
   st = hip_check(launch_kernel(logits_kernel, dim3(w.nblk, B), dim3(256), 0, s, la), "logits launch");

@@ -17,6 +17,7 @@
 //                   replaces w1_swiglu_dense_kernel / w2_scatter_dense_kernel (src/quant/gpu.rs:89-192)
 // combine_kernel    y = x + sum_p w_p * (down_p + b2), deterministic slot order
 //                   replaces the accumulate + residual of src/moe/mod.rs:405-411
+//                   (combine_norm_kernel: the same, then a decoder's next RmsNorm of y)
 // dequant_kernel    test hook: exact dequantisation (src/loader/mxfp4.rs:56-79)
 #include "kernels.hpp"
 #include "mx_device.hpp"
@@ -1608,6 +1609,101 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Combine followed by the RmsNorm of its output (a decoder's next norm, one launch instead of
+// two): f32 x, y and nout, f32 slot rows in NP K-parts, D % 4 == 0, D <= 4096, 16-byte aligned
+// rows.  One workgroup of 256 threads per token row; thread i computes output quads q = i + 256 r
+// with combine_kernel's arithmetic (parts summed in order, slots p ascending), keeps them in
+// registers and normalises the row: sum of squares over r then x, y, z, w (zeros past the row),
+// wave butterfly, (w0 + w1) + (w2 + w3); nout = (y / sqrt(sum / D + eps)) * gamma.  The quads of
+// all slots of a pass (4 slots, 2 with 4 K-parts) are requested together: one memory round trip
+// per pass.
+// ---------------------------------------------------------------------------------------------
+template <int NP>
+__global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
+  constexpr uint32_t kR = 4, kP = NP >= 4 ? 2 : 4;  // slots per pass (register budget)
+  __shared__ float red[4];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, nq = a.D / 4u;
+  const float4 *x4 = (const float4 *)((const float *)a.x + (size_t)t * a.D);
+  const float4 *g4 = (const float4 *)a.ngamma;
+  const float *yp = (const float *)a.ypart;
+  float4 xv[kR], gv[kR];
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    const uint32_t q = min(tid + 256u * r, nq - 1u);  // clamped: quads past the row reload a valid one
+    xv[r] = a.add_residual ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    gv[r] = g4[q];
+  }
+  float acc[kR][4];
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0.0f;
+  for (uint32_t p0 = 0; p0 < a.K; p0 += kP) {
+    float wv[kP];
+    float4 yv[kR][kP], yh[NP > 1 ? NP - 1 : 1][kR][kP];
+#pragma unroll
+    for (uint32_t u = 0; u < kP; ++u) {
+      const uint32_t p = min(p0 + u, a.K - 1u);
+      wv[u] = a.topk_w[(size_t)t * a.K + p];
+#pragma unroll
+      for (uint32_t r = 0; r < kR; ++r) {
+        const size_t row = ((size_t)t * a.K + p) * a.Dp + 4u * min(tid + 256u * r, nq - 1u);
+        yv[r][u] = *(const float4 *)(yp + row);
+#pragma unroll
+        for (int h = 1; h < NP; ++h) yh[h - 1][r][u] = *(const float4 *)(yp + h * a.part_stride + row);
+      }
+    }
+#pragma unroll
+    for (int h = 1; h < NP; ++h)
+#pragma unroll
+      for (uint32_t r = 0; r < kR; ++r)
+#pragma unroll
+        for (uint32_t u = 0; u < kP; ++u)
+          yv[r][u] = make_float4(yv[r][u].x + yh[h - 1][r][u].x, yv[r][u].y + yh[h - 1][r][u].y,
+                                 yv[r][u].z + yh[h - 1][r][u].z, yv[r][u].w + yh[h - 1][r][u].w);
+#pragma unroll
+    for (uint32_t u = 0; u < kP; ++u) {
+      if (p0 + u >= a.K) break;
+#pragma unroll
+      for (uint32_t r = 0; r < kR; ++r) {
+        acc[r][0] = acc[r][0] + yv[r][u].x * wv[u];
+        acc[r][1] = acc[r][1] + yv[r][u].y * wv[u];
+        acc[r][2] = acc[r][2] + yv[r][u].z * wv[u];
+        acc[r][3] = acc[r][3] + yv[r][u].w * wv[u];
+      }
+    }
+  }
+  float4 *y4 = (float4 *)((float *)a.y + (size_t)t * a.D);
+  float4 v[kR];
+  float ss = 0.0f;
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    const uint32_t q = tid + 256u * r;
+    v[r] = q < nq ? make_float4(xv[r].x + acc[r][0], xv[r].y + acc[r][1], xv[r].z + acc[r][2], xv[r].w + acc[r][3])
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (q < nq) y4[q] = v[r];
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    ss = fmaf(v[r].x, v[r].x, ss);
+    ss = fmaf(v[r].y, v[r].y, ss);
+    ss = fmaf(v[r].z, v[r].z, ss);
+    ss = fmaf(v[r].w, v[r].w, ss);
+  }
+  ss = wave_sum_butterfly(ss);
+  if ((tid & 63u) == 0u) red[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rr = sqrtf(tot / (float)a.D + a.neps);
+  float4 *n4 = (float4 *)(a.nout + (size_t)t * a.D);
+#pragma unroll
+  for (uint32_t r = 0; r < kR; ++r) {
+    const uint32_t q = tid + 256u * r;
+    if (q < nq)
+      n4[q] = make_float4((v[r].x / rr) * gv[r].x, (v[r].y / rr) * gv[r].y, (v[r].z / rr) * gv[r].z,
+                          (v[r].w / rr) * gv[r].w);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Dequant hook: one thread per packed byte.  f32 output uses the bit-built LUT value times the
 // bit-built 2^(s-127); bf16 output uses the same v_cvt_scalef32_pk_bf16_fp4 conversion as the
 // expert projections, so the exhaustive test of this hook covers their dequantisation.
@@ -1902,6 +1998,18 @@ hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s) {
   const dim3 grid((a.D + 1023) / 1024, a.n), block(256);
   if (a.nparts != 1u && a.nparts != kDownSplit && a.nparts != kDownSplitFew) return hipErrorInvalidValue;
   if (a.part_bf16 && a.nparts != 1u) return hipErrorInvalidValue;
+  if (a.nout) {
+    if (x_bf16 || a.part_bf16 || !a.ngamma || a.D == 0u || a.D % 4u != 0u || a.D > 4096u || a.Dp % 4u != 0u ||
+        (((uintptr_t)a.x | (uintptr_t)a.y | (uintptr_t)a.nout | (uintptr_t)a.ngamma | (uintptr_t)a.ypart) & 15u))
+      return hipErrorInvalidValue;
+    if (a.nparts == 1u)
+      (void)launch_kernel(combine_norm_kernel<1>, dim3(a.n), dim3(256), 0, s, a);
+    else if (a.nparts == kDownSplit)
+      (void)launch_kernel(combine_norm_kernel<kDownSplit>, dim3(a.n), dim3(256), 0, s, a);
+    else
+      (void)launch_kernel(combine_norm_kernel<kDownSplitFew>, dim3(a.n), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   if (a.part_bf16 && x_bf16 && a.D % 8u == 0u && (((uintptr_t)a.x | (uintptr_t)a.y) & 15u) == 0u) {
     (void)launch_kernel(combine_rows8_kernel, dim3((a.D + 2047u) / 2048u, a.n), dim3(256), 0, s, a);
   } else if (a.part_bf16) {

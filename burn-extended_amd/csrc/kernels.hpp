@@ -172,6 +172,11 @@ struct CombineArgs {
   const float *topk_w;
   uint32_t n, D, Dp, K;
   int add_residual;
+  // optional RmsNorm of the result (combine_norm_kernel; f32 x and y, unsplit or K-part f32 slot
+  // rows): nout[t] = y[t] / sqrt(mean(y[t]^2) + neps) * ngamma, when nout is not null
+  const float *ngamma;
+  float *nout;
+  float neps;
 };
 
 // act[r, f] = SwiGLU(sum_h part_h[r, 2f], sum_h part_h[r, 2f + 1]) (h ascending) for the

@@ -599,8 +599,16 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
 }
 
 // The weighted combine + residual of every path (token-major slot rows in p.ypart).
+// An RmsNorm of the layer's output fused into its combine (internal: the decoder's next norm).
+struct PostNorm {
+  const float *gamma;
+  float eps;
+  float *out;
+};
+
 burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
-                       const WsPtrs &p, hipStream_t s, uint32_t nparts = 1, bool part_bf16 = false) {
+                       const WsPtrs &p, hipStream_t s, uint32_t nparts = 1, bool part_bf16 = false,
+                       const PostNorm *pn = nullptr) {
   CombineArgs c{};
   c.x = x;
   c.y = y;
@@ -614,6 +622,11 @@ burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, ui
   c.Dp = L->Dp;
   c.K = L->K;
   c.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1 : 0;
+  if (pn) {
+    c.ngamma = pn->gamma;
+    c.nout = pn->out;
+    c.neps = pn->eps;
+  }
   burnext_status st;
   {
     ProfScope ps(L, s, kKCombine);
@@ -716,6 +729,145 @@ burnext_status scratch_address(int device, void **out) {
   return BURNEXT_OK;
 }
 }  // namespace
+
+namespace burnext {
+
+// burnext_moe_forward; with pn, the RmsNorm of y (pn->gamma, pn->eps into pn->out) runs inside the
+// combine where the path allows it (decode-sized GEMV path, f32 rows), and *norm_done says whether
+// it did (otherwise the caller normalises y itself).
+burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
+                            uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream, const PostNorm *pn,
+                            bool *norm_done) {
+  if (norm_done) *norm_done = false;
+  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
+  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
+  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
+  if (n == 0) return ok();
+  if (!x || !y) return fail(BURNEXT_INVALID_ARG, "x or y is null");
+  if (x == y) return fail(BURNEXT_INVALID_ARG, "x and y must not alias");
+  const bool xb = x_dtype == BURNEXT_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  DeviceGuard guard(L->device);
+  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
+  if (L->disabled) {  // identity, src/moe/mod.rs:106-108
+    const burnext_status cs =
+        check_launch(hipMemcpyAsync(y, x, n * L->D * (xb ? 2 : 4), hipMemcpyDeviceToDevice, s), "identity copy");
+    return cs == BURNEXT_OK ? ok() : cs;
+  }
+  WsLayout w;
+  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
+  if (st != BURNEXT_OK) return st;
+  const WsPtrs p = ws_ptrs(*L, w, workspace);
+  const bool norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
+  if (w.gemm && xb) {
+    st = forward_gemm(L, x, xb, n, norm, p, s);
+    if (st != BURNEXT_OK) return st;
+    return combine(L, x, y, xb, n, flags, p, s, 1, true);  // bf16 slot rows from the down GEMM
+  }
+  // f32 activations: two bf16 terms (hi + bf16 of the residual, ~2^-17 relative per value)
+  const int nt = xb ? 1 : 2;
+  const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
+  // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
+  // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
+  // evenly over the waves; measured slower from 64 tokens on)
+  const bool up_split = gate_up_split(*L, n) && p.upart;
+  // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
+  const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
+                        : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
+                                  : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
+  if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
+    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
+  } else if (st == BURNEXT_OK) {
+    st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
+    if (st == BURNEXT_OK)
+      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
+  }
+  if (st != BURNEXT_OK) return st;
+
+  auto gemv = [&](bool gate_up) -> burnext_status {
+    const GemvCfg &cf = gate_up ? cfg_up : cfg_dn;
+    const TiledMx &t = gate_up ? L->w1 : L->w2;
+    GemvArgs g{};
+    g.wb = t.blocks;
+    g.ws = t.scales;
+    g.wb_estride = t.blocks_per_expert;
+    g.ws_estride = t.scales_per_expert;
+    g.bias = gate_up ? L->b1 : L->b2;
+    g.bias_estride = t.rows_p;  // multiple of 16: 16-byte aligned rows of 4 for the epilogue
+    g.nrt = t.nrt;
+    g.nb = t.nb;
+    g.kt = t.cols;
+    g.out_rows = gate_up ? L->F : L->D;
+    g.mt_max = cf.mt;
+    g.seg_off = p.seg_off;
+    g.active = p.active;
+    g.num_active = p.num_active;
+    g.perm = p.perm;
+    g.exrec = p.exrec;
+    g.topk = L->K;
+    g.brows = gate_up ? p.xn : (const void *)p.act;
+    g.out = gate_up ? p.act : p.ypart;
+    g.out_stride = gate_up ? L->Fp : L->Dp;
+    g.alpha = L->alpha;
+    g.limit = L->limit;
+    g.nrec = cf.nrec;
+    g.num_cus = (uint32_t)L->num_cus;
+    g.weighted = n <= kSmallRouteMaxTokens ? 1u : 0u;  // measured: strided shares faster from 64 tokens on
+    if (!gate_up && ksplit > 1u) {
+      g.ksplit = ksplit;
+      g.out_half = n * L->K * L->Dp;
+    }
+    if (gate_up && up_split) {  // raw pre-activation K-parts, finished by swiglu_parts_kernel
+      g.ksplit = kGateUpSplit;
+      g.out = p.upart;
+      g.out_stride = L->w1.rows_p;
+      g.out_rows = 2 * L->F;
+      g.out_half = n * L->K * L->w1.rows_p;
+    }
+    ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
+    return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
+  };
+  st = gemv(true);
+  if (st != BURNEXT_OK) return st;
+  if (up_split) {
+    SwigluPartsArgs sa{};
+    sa.parts = p.upart;
+    sa.part_stride = n * L->K * L->w1.rows_p;
+    sa.act = p.act;
+    sa.nparts = kGateUpSplit;
+    sa.rows = (uint32_t)(n * L->K);
+    sa.F = L->F;
+    sa.rows_p = L->w1.rows_p;
+    sa.act_stride = L->Fp;
+    sa.alpha = L->alpha;
+    sa.limit = L->limit;
+    ProfScope ps(L, s, kKSwiglu);
+    st = check_launch(launch_swiglu_parts(sa, s), "gate_up SwiGLU launch");
+    if (st != BURNEXT_OK) return st;
+  }
+  st = gemv(false);
+  if (st != BURNEXT_OK) return st;
+
+  // the fused RmsNorm of y: f32 rows of at most 4096 values (combine_norm_kernel)
+  const bool fuse = pn && !xb && L->D % 4 == 0 && L->D <= 4096 &&
+                    (((uintptr_t)x | (uintptr_t)y | (uintptr_t)pn->out | (uintptr_t)pn->gamma) & 15u) == 0;
+  st = combine(L, x, y, xb, n, flags, p, s, ksplit, false, fuse ? pn : nullptr);
+  if (st == BURNEXT_OK && norm_done) *norm_done = fuse;
+  return st;
+}
+
+// The decoder's entry: burnext_moe_forward with the next RmsNorm fused where possible.
+burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
+                                     uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
+                                     const float *gamma, float eps, float *xn, bool *norm_done) {
+  const PostNorm pn{gamma, eps, xn};
+  return forward_impl(L, x, x_dtype, y, n, flags, workspace, ws_bytes, stream, gamma && xn ? &pn : nullptr,
+                      norm_done);
+}
+
+}  // namespace burnext
 
 extern "C" {
 
@@ -864,118 +1016,7 @@ burnext_status burnext_moe_workspace_size(burnext_moe_layer_t L, uint64_t n_toke
 
 burnext_status burnext_moe_forward(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, void *y,
                                    uint64_t n, uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream) {
-  if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
-  if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
-  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
-  if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
-  if (n == 0) return ok();
-  if (!x || !y) return fail(BURNEXT_INVALID_ARG, "x or y is null");
-  if (x == y) return fail(BURNEXT_INVALID_ARG, "x and y must not alias");
-  const bool xb = x_dtype == BURNEXT_BF16;
-  hipStream_t s = (hipStream_t)stream;
-  DeviceGuard guard(L->device);
-  if (!guard.ok) return fail(BURNEXT_DEVICE_ERROR, "hipSetDevice failed");
-  if (L->disabled) {  // identity, src/moe/mod.rs:106-108
-    const burnext_status cs =
-        check_launch(hipMemcpyAsync(y, x, n * L->D * (xb ? 2 : 4), hipMemcpyDeviceToDevice, s), "identity copy");
-    return cs == BURNEXT_OK ? ok() : cs;
-  }
-  WsLayout w;
-  burnext_status st = check_ws(L, n, workspace, ws_bytes, w);
-  if (st != BURNEXT_OK) return st;
-  const WsPtrs p = ws_ptrs(*L, w, workspace);
-  const bool norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
-  if (w.gemm && xb) {
-    st = forward_gemm(L, x, xb, n, norm, p, s);
-    if (st != BURNEXT_OK) return st;
-    return combine(L, x, y, xb, n, flags, p, s, 1, true);  // bf16 slot rows from the down GEMM
-  }
-  // f32 activations: two bf16 terms (hi + bf16 of the residual, ~2^-17 relative per value)
-  const int nt = xb ? 1 : 2;
-  const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
-  // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
-  // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
-  // evenly over the waves; measured slower from 64 tokens on)
-  const bool up_split = gate_up_split(*L, n) && p.upart;
-  // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
-  const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
-                        : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
-  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
-                                  : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
-  if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
-  } else if (st == BURNEXT_OK) {
-    st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
-    if (st == BURNEXT_OK)
-      st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
-  }
-  if (st != BURNEXT_OK) return st;
-
-  auto gemv = [&](bool gate_up) -> burnext_status {
-    const GemvCfg &cf = gate_up ? cfg_up : cfg_dn;
-    const TiledMx &t = gate_up ? L->w1 : L->w2;
-    GemvArgs g{};
-    g.wb = t.blocks;
-    g.ws = t.scales;
-    g.wb_estride = t.blocks_per_expert;
-    g.ws_estride = t.scales_per_expert;
-    g.bias = gate_up ? L->b1 : L->b2;
-    g.bias_estride = t.rows_p;  // multiple of 16: 16-byte aligned rows of 4 for the epilogue
-    g.nrt = t.nrt;
-    g.nb = t.nb;
-    g.kt = t.cols;
-    g.out_rows = gate_up ? L->F : L->D;
-    g.mt_max = cf.mt;
-    g.seg_off = p.seg_off;
-    g.active = p.active;
-    g.num_active = p.num_active;
-    g.perm = p.perm;
-    g.exrec = p.exrec;
-    g.topk = L->K;
-    g.brows = gate_up ? p.xn : (const void *)p.act;
-    g.out = gate_up ? p.act : p.ypart;
-    g.out_stride = gate_up ? L->Fp : L->Dp;
-    g.alpha = L->alpha;
-    g.limit = L->limit;
-    g.nrec = cf.nrec;
-    g.num_cus = (uint32_t)L->num_cus;
-    g.weighted = n <= kSmallRouteMaxTokens ? 1u : 0u;  // measured: strided shares faster from 64 tokens on
-    if (!gate_up && ksplit > 1u) {
-      g.ksplit = ksplit;
-      g.out_half = n * L->K * L->Dp;
-    }
-    if (gate_up && up_split) {  // raw pre-activation K-parts, finished by swiglu_parts_kernel
-      g.ksplit = kGateUpSplit;
-      g.out = p.upart;
-      g.out_stride = L->w1.rows_p;
-      g.out_rows = 2 * L->F;
-      g.out_half = n * L->K * L->w1.rows_p;
-    }
-    ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
-    return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
-  };
-  st = gemv(true);
-  if (st != BURNEXT_OK) return st;
-  if (up_split) {
-    SwigluPartsArgs sa{};
-    sa.parts = p.upart;
-    sa.part_stride = n * L->K * L->w1.rows_p;
-    sa.act = p.act;
-    sa.nparts = kGateUpSplit;
-    sa.rows = (uint32_t)(n * L->K);
-    sa.F = L->F;
-    sa.rows_p = L->w1.rows_p;
-    sa.act_stride = L->Fp;
-    sa.alpha = L->alpha;
-    sa.limit = L->limit;
-    ProfScope ps(L, s, kKSwiglu);
-    st = check_launch(launch_swiglu_parts(sa, s), "gate_up SwiGLU launch");
-    if (st != BURNEXT_OK) return st;
-  }
-  st = gemv(false);
-  if (st != BURNEXT_OK) return st;
-
-  return combine(L, x, y, xb, n, flags, p, s, ksplit);
+  return burnext::forward_impl(L, x, x_dtype, y, n, flags, workspace, ws_bytes, stream, nullptr, nullptr);
 }
 
 burnext_status burnext_moe_forward_noalloc(burnext_moe_layer_t L, const void *x, burnext_dtype x_dtype, void *y,

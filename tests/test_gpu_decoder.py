@@ -59,6 +59,12 @@ CASES = {
     "groups1": dict(n_heads=4, kv_heads=4, head_dim=64),
     "groups16": dict(n_heads=16, kv_heads=1, head_dim=16),
     "dk128": dict(n_heads=4, kv_heads=2, head_dim=128, cache_len=300, window=200, max_seq_len=512),
+    # the MoE combine that also writes the next norm, over its slot-row layouts: 4 down K-parts
+    # (few touched experts, F = 512), unsplit rows (F = 96); d_model 4160 > 4096 keeps the
+    # separate rmsnorm_kernel after every MoE layer
+    "combine_norm_4parts": dict(ffn_hidden=512),
+    "combine_norm_unsplit": dict(ffn_hidden=96),
+    "wide_d_unfused": dict(d_model=4160, n_layers=2),
 }
 
 
