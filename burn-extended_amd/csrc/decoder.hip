@@ -11,7 +11,8 @@
 //     attn_chunk_kernel one query row per head against 256 cached keys per workgroup: chunk
 //                       maximum, exp, sums and the weighted value sum (flash-decoding split)
 //     attn_combine_kernel  chunks merged with the learned sink in the softmax denominator
-//     dense_gemv_kernel the output projection; o_post_kernel hidden += sum + bias
+//     dense_gemv_kernel the output projection; o_post_kernel hidden += sum + bias (where the MoE
+//                       router cannot: router_front_kernel forms that row itself for decode batches)
 //     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels;
 //                       its combine (combine_norm_kernel) also writes the next layer's xn (after
 //                       the last layer: norm_final), so rmsnorm_kernel runs for layer 0 only
@@ -40,7 +41,9 @@ burnext_status set_error(burnext_status st, const std::string &msg);
 void moe_layer_shape(const burnext_moe_layer *L, uint32_t *d_model, int *device);
 burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                                      uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
-                                     const float *gamma, float eps, float *xn, bool *norm_done);
+                                     const float *gamma, float eps, float *xn, bool *norm_done, const float *part,
+                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid);
+bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n);
 }  // namespace burnext
 
 using namespace burnext;
@@ -1317,16 +1320,26 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
                    "attention combine launch");
     if (st == BURNEXT_OK) st = dense_gemv(M->wo[l], ctx, B, part, s);
     if (st != BURNEXT_OK) return st;
-    OPostArgs oa{part, (uint64_t)B * D, M->wo[l].parts, D, M->bo + (size_t)l * D, hid};
-    st = hip_check(launch_kernel(o_post_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, oa), "o post launch");
-    if (st != BURNEXT_OK) return st;
     // the MoE layer; its combine also writes the next norm of the new hidden rows (the next
     // layer's attention norm, after the last layer the final norm) when its path allows
     const float *next_gamma = l + 1 < c.n_layers ? M->norm_attn + (size_t)(l + 1) * D : M->norm_final;
-    st = moe_forward_post_norm(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
-                               stream, next_gamma, c.rms_eps, xn, &normed);
-    if (st != BURNEXT_OK) return st;
-    std::swap(hid, hid2);
+    const float *bo = M->bo + (size_t)l * D;
+    if (moe_front_fusable(M->moe[l], B)) {
+      // its router also forms the residual hid2 = hid + (sum of the output projection's parts + bo)
+      st = moe_forward_post_norm(M->moe[l], hid2, BURNEXT_F32, hid, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
+                                 stream, next_gamma, c.rms_eps, xn, &normed, part, (uint64_t)B * D, M->wo[l].parts,
+                                 bo, hid);
+      if (st != BURNEXT_OK) return st;
+    } else {
+      OPostArgs oa{part, (uint64_t)B * D, M->wo[l].parts, D, bo, hid};
+      st = hip_check(launch_kernel(o_post_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, oa),
+                     "o post launch");
+      if (st != BURNEXT_OK) return st;
+      st = moe_forward_post_norm(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
+                                 stream, next_gamma, c.rms_eps, xn, &normed, nullptr, 0, 0, nullptr, nullptr);
+      if (st != BURNEXT_OK) return st;
+      std::swap(hid, hid2);
+    }
   }
   if (hidden) {
     st = hip_check(hipMemcpyAsync(hidden, hid, (size_t)B * D * 4, hipMemcpyDeviceToDevice, s), "hidden copy");

@@ -1183,6 +1183,112 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Decode router with its input rows formed first (a decoder's residual after the attention
+// block): workgroup (t, g) of 8 waves serves token t and experts 8 g .. 8 g + 7, one per wave.
+//   1. every wave requests its expert's router row chunks; the workgroup then forms the row
+//      x = resid + (sum_h part_h + bias) (parts in order from 0, the arithmetic of a separate
+//      residual-add kernel), chunk c (8 values) by thread c, into LDS; workgroup c mod G writes
+//      chunk c to xout;
+//   2. wave w forms the logit of expert 8 g + w exactly as router_small_kernel does for (e, t):
+//      lane l owns chunks 512 i + 8 l + j, fmaf over i then j for the dot and the sum of squares,
+//      xor butterfly, logit = dot / r + b with r = sqrt(sum / D + eps);
+//   3. xn_t = x (1/r) gamma (zero padded to Dp) chunk by chunk, chunk c by workgroup c mod G.
+// Logits, r and xn take router_small_kernel's arithmetic on x = xout.  f32 rows, n <= 16,
+// D % 8 == 0, D <= 512 * kFrontChunks, nparts <= kFrontMaxParts, 16-byte aligned rows.
+// ---------------------------------------------------------------------------------------------
+template <typename WT>
+__global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
+  constexpr int RC = kFrontChunks;
+  __shared__ __align__(16) float xs[512u * RC];
+  const FrontArgs &f = a.f;
+  const uint32_t D = f.D, E = f.E, t = blockIdx.x, g = blockIdx.y, G = gridDim.y;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const uint32_t e = 8u * g + w;
+  const bool ev = e < E;  // wave-uniform
+  const WT *rw = (const WT *)f.rw + (size_t)min(e, E - 1u) * D;
+  Chunk8<WT> wc[RC];
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const uint32_t c0 = min(512u * i + 8u * lane, D - 8u);  // clamped: lanes past D reload a valid chunk
+    chunk_load(wc[i], rw + c0);
+  }
+  // this thread's xn chunk (written in step 3) and its gamma values, requested early
+  const uint32_t nc = D / 8u, c = tid;
+  const bool own = c < f.Dp / 8u && c % G == g && f.xn != nullptr;
+  Chunk8<float> gc;
+  if (own && f.apply_norm && c < nc) chunk_load(gc, f.gamma + 8u * c);
+  // 1. the row
+  if (c < nc) {
+    const size_t o = (size_t)t * D + 8u * c;
+    float sv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t h0 = 0; h0 < a.nparts; h0 += 8u) {
+      Chunk8<float> pc[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) chunk_load(pc[u], a.part + (size_t)min(h0 + u, a.nparts - 1u) * a.part_stride + o);
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        if (h0 + u >= a.nparts) break;
+        float pv[8];
+        chunk_vals(pc[u], pv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[j] = sv[j] + pv[j];
+      }
+    }
+    Chunk8<float> rc, bc;
+    chunk_load(rc, a.resid + o);
+    chunk_load(bc, a.bias + 8u * c);
+    float rv[8], bv[8], xv[8];
+    chunk_vals(rc, rv);
+    chunk_vals(bc, bv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = rv[j] + (sv[j] + bv[j]);
+    *(float4 *)(xs + 8u * c) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+    *(float4 *)(xs + 8u * c + 4u) = make_float4(xv[4], xv[5], xv[6], xv[7]);
+    if (c % G == g) store8(a.xout + o, xv);
+  }
+  __syncthreads();
+  // 2. logit of expert e (every wave forms r: step 3 needs it)
+  float acc[2] = {0.0f, 0.0f};  // dot, sum of squares
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const uint32_t c0 = 512u * i + 8u * lane;
+    if (c0 >= D) continue;
+    float wv[8], x0[8];
+    chunk_vals(wc[i], wv);
+    const float4 lo = *(const float4 *)(xs + c0), hi = *(const float4 *)(xs + c0 + 4u);
+    x0[0] = lo.x; x0[1] = lo.y; x0[2] = lo.z; x0[3] = lo.w; x0[4] = hi.x; x0[5] = hi.y; x0[6] = hi.z; x0[7] = hi.w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[0] = fmaf(x0[j], wv[j], acc[0]);
+      acc[1] = fmaf(x0[j], x0[j], acc[1]);
+    }
+  }
+  wave_sum_butterfly_n<2>(acc);
+  const float r = f.apply_norm ? sqrtf(acc[1] / (float)D + f.eps) : 1.0f;
+  if (lane == 0u && ev) f.logits[(size_t)t * E + e] = (f.apply_norm ? acc[0] / r : acc[0]) + f.rb[e];
+  if (tid == 0u && g == 0u && f.rms) f.rms[t] = r;
+  // 3. normalised row chunk c
+  if (own) {
+    float u[8];
+    if (c < nc) {
+      const float4 lo = *(const float4 *)(xs + 8u * c), hi = *(const float4 *)(xs + 8u * c + 4u);
+      u[0] = lo.x; u[1] = lo.y; u[2] = lo.z; u[3] = lo.w; u[4] = hi.x; u[5] = hi.y; u[6] = hi.z; u[7] = hi.w;
+      if (f.apply_norm) {
+        const float ir = 1.0f / r;
+        float gv[8];
+        chunk_vals(gc, gv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) u[j] = (u[j] * ir) * gv[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] = 0.0f;
+    }
+    store8((float *)f.xn + (size_t)t * f.Dp + 8u * c, u);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Expert projection on MFMA.  Tiled MXFP4 layout of one expert (written by the layer upload):
 //   row tile rt (16 rows) occupies nb*256 bytes; inside it K-group kg (4 blocks of 32 columns)
 //   occupies 1024 bytes (tail group: 256 per block) where lane l = q*16 + i holds the 16 bytes
@@ -1837,6 +1943,22 @@ hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s) {
     (void)launch_kernel(small_route_kernel<2>, dim3(1), block, 0, s, a);
   else
     (void)launch_kernel(small_route_kernel<4>, dim3(1), block, 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_front(const PreFrontArgs &a, bool w_bf16, hipStream_t s) {
+  const FrontArgs &f = a.f;
+  if (f.n == 0 || f.n > kSmallRouteMaxTokens || f.D % 8u != 0 || f.D > 512u * kFrontChunks || f.Dp > 512u * kFrontChunks ||
+      f.Dp % 8u != 0 || f.E == 0 || f.E > kMaxExperts || !f.logits || f.x != a.xout || a.nparts == 0 ||
+      a.nparts > kFrontMaxParts || !a.part || !a.bias || !a.resid || !a.xout ||
+      (((uintptr_t)a.part | (uintptr_t)a.bias | (uintptr_t)a.resid | (uintptr_t)a.xout | (uintptr_t)f.rw |
+        (uintptr_t)f.gamma | (uintptr_t)f.xn) & 15u) || (a.part_stride & 3u))
+    return hipErrorInvalidValue;
+  const dim3 g(f.n, (f.E + 7u) / 8u), b(512);
+  if (w_bf16)
+    (void)launch_kernel(router_front_kernel<uint16_t>, g, b, 0, s, a);
+  else
+    (void)launch_kernel(router_front_kernel<float>, g, b, 0, s, a);
   return hipGetLastError();
 }
 

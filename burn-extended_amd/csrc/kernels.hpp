@@ -137,6 +137,20 @@ struct FrontArgs {
 };
 constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 
+// The decode router with the input rows formed first (router_front_kernel, f32 rows): a decoder's
+// attention residual x = resid + (sum_h part_h + bias) of the output projection's K-part partials
+// [nparts][n][D] is written to xout and routed as router_small_kernel routes f.x = xout.
+struct PreFrontArgs {
+  FrontArgs f;
+  const float *part;
+  uint64_t part_stride;
+  uint32_t nparts;
+  const float *bias;   // [D]
+  const float *resid;  // [n, D]
+  float *xout;         // [n, D]
+};
+constexpr uint32_t kFrontMaxParts = 16;
+
 // Grouped expert GEMM for prefill-sized batches (expert_gemm_kernel): every active expert's
 // segment is cut into tiles of kGemmTok routed tokens; a workgroup computes kGemmRows weight
 // rows x one token tile with the block-scaled MFMA (MXFP4 weights x MXFP8 hi + MXFP4 lo activations).
@@ -241,6 +255,7 @@ hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec
 hipError_t launch_router_rows(const RouterArgs &a, bool x_bf16, bool w_bf16, int tokens_per_wave, hipStream_t s);
 hipError_t launch_small_route(const SmallRouteArgs &a, hipStream_t s);
 hipError_t launch_router_small(const FrontArgs &a, bool x_bf16, bool w_bf16, hipStream_t s);
+hipError_t launch_router_front(const PreFrontArgs &a, bool w_bf16, hipStream_t s);
 hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);

@@ -598,6 +598,50 @@ burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16
   return check_launch(launch_router_small(a, x_bf16, w_bf16, s), "router kernel launch");
 }
 
+// The layer input formed by the router (internal: a decoder's residual add after its attention
+// block): x = resid + (sum_h part_h + bias), written to xout (router_front_kernel).
+struct PreAdd {
+  const float *part;
+  uint64_t part_stride;
+  uint32_t nparts;
+  const float *bias;
+  const float *resid;
+  float *xout;
+};
+
+bool front_ok(const burnext_moe_layer &L, uint64_t n) {
+  return !L.disabled && n >= 1 && n <= kSmallRouteMaxTokens && L.D % 8 == 0 && L.D <= 512u * kFrontChunks &&
+         L.Dp <= 512u * kFrontChunks && ((uintptr_t)L.router_wg & 15u) == 0 && ((uintptr_t)L.router_w & 15u) == 0;
+}
+
+burnext_status run_router_front(burnext_moe_layer *L, const PreAdd &pa, uint64_t n, bool norm, float *rms,
+                                float *logits, void *xn, hipStream_t s) {
+  PreFrontArgs a{};
+  FrontArgs &f = a.f;
+  f.x = pa.xout;
+  f.rw = norm ? L->router_wg : L->router_w;
+  const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
+  f.rb = L->router_b;
+  f.gamma = L->gamma;
+  f.xn = xn;
+  f.logits = logits;
+  f.rms = rms;
+  f.n = (uint32_t)n;
+  f.D = L->D;
+  f.Dp = L->Dp;
+  f.E = L->E;
+  f.eps = L->eps;
+  f.apply_norm = norm ? 1 : 0;
+  a.part = pa.part;
+  a.part_stride = pa.part_stride;
+  a.nparts = pa.nparts;
+  a.bias = pa.bias;
+  a.resid = pa.resid;
+  a.xout = pa.xout;
+  ProfScope ps(L, s, kKRouter);
+  return check_launch(launch_router_front(a, w_bf16, s), "router front launch");
+}
+
 // The weighted combine + residual of every path (token-major slot rows in p.ypart).
 // An RmsNorm of the layer's output fused into its combine (internal: the decoder's next norm).
 struct PostNorm {
@@ -737,9 +781,11 @@ namespace burnext {
 // it did (otherwise the caller normalises y itself).
 burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                             uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream, const PostNorm *pn,
-                            bool *norm_done) {
+                            bool *norm_done, const PreAdd *pa = nullptr) {
   if (norm_done) *norm_done = false;
   if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
+  if (pa && (x != pa->xout || x_dtype != BURNEXT_F32 || !front_ok(*L, n)))
+    return fail(BURNEXT_INVALID_ARG, "formed input rows need f32 rows, x == xout and a decode-sized batch");
   if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
   if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
   if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
@@ -775,8 +821,9 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
   const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
                         : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
-  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
-                                  : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
+  st = pa                               ? run_router_front(L, *pa, n, norm, p.rms, p.logits, p.xn, s)
+       : router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
+                                         : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
     st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
   } else if (st == BURNEXT_OK) {
@@ -858,14 +905,20 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   return st;
 }
 
-// The decoder's entry: burnext_moe_forward with the next RmsNorm fused where possible.
+// The decoder's entry: burnext_moe_forward with the next RmsNorm fused where possible, and with
+// the layer input x = resid + (sum_h part_h + bias) formed by the router when part is not null
+// (then x must be the f32 rows xout that receive it, and moe_front_fusable must hold).
 burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                                      uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
-                                     const float *gamma, float eps, float *xn, bool *norm_done) {
+                                     const float *gamma, float eps, float *xn, bool *norm_done, const float *part,
+                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid) {
   const PostNorm pn{gamma, eps, xn};
+  const PreAdd pa{part, part_stride, nparts, bias, resid, (float *)x};
   return forward_impl(L, x, x_dtype, y, n, flags, workspace, ws_bytes, stream, gamma && xn ? &pn : nullptr,
-                      norm_done);
+                      norm_done, part ? &pa : nullptr);
 }
+
+bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n) { return L && front_ok(*L, n); }
 
 }  // namespace burnext
 
