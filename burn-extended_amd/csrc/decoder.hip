@@ -51,6 +51,7 @@ using namespace burnext;
 namespace {
 
 constexpr uint32_t kDenseMaxH = 16;   // K-groups (32 inputs each) per GEMV work unit
+constexpr uint32_t kDenseWaves = 8;   // row tiles (one per wave) per GEMV workgroup
 constexpr uint32_t kAttnChunk = 256;  // cached keys per attention workgroup
 constexpr uint32_t kMaxGroups = 16;   // query heads per kv head
 constexpr uint32_t kMaxHeadDim = 128;
@@ -118,7 +119,7 @@ __host__ __device__ __forceinline__ size_t v_index(uint32_t b, uint32_t g, uint3
 // Dense decode GEMV.  Weights W [N, K] bf16, repacked at create into tiles of 16 rows x 32
 // inputs (1 KiB): tile t, K-group kg at (t * nkg + kg) KiB, lane l = 16 q + i holding
 // W[16 t + i][32 kg + 8 q .. +8] -- the A operand of v_mfma_f32_16x16x32_bf16 for one K step.
-// Workgroup (x, h): 4 waves, row tiles 4 x .. 4 x + 3, K-groups [h H, (h + 1) H).  Every wave
+// Workgroup (x, h): NW waves, row tiles NW x .. NW x + NW - 1, K-groups [h H, (h + 1) H).  Every wave
 // first issues all its H weight loads (16 KiB in flight at H = 16); while they are in flight the
 // workgroup stages the B token rows of its K range in LDS as two bf16 terms (hi, lo = bf16 of the
 // residual; together f32-accurate to ~2^-17).  Lanes of token columns >= B feed zeros to the
@@ -132,24 +133,25 @@ struct DenseArgs {
   uint64_t part_stride;
 };
 
-__global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
+template <uint32_t NW>
+__global__ __launch_bounds__(NW * 64) void dense_gemv_kernel(DenseArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const uint32_t H = a.H, ldk = H * 32u + 8u;  // +8: consecutive token rows start on other banks
   uint16_t *bs = (uint16_t *)smem;             // [2 terms][16 tokens][ldk]
   const uint32_t h = blockIdx.y, kg0 = h * H, kg1 = min(kg0 + H, a.nkg), nk = kg1 - kg0;
   const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-  const uint32_t tile = blockIdx.x * 4u + wv;
+  const uint32_t tile = blockIdx.x * NW + wv;
   const bool tv = tile < a.ntiles;  // wave-uniform
   const uint32_t tl = tv ? tile : a.ntiles - 1u;
   // activation quads of rows j < B in this K range (at most 16 x 16 x 8 / 256 = 8 per thread),
   // requested before the weights: the in-order load counter then lets the staging wait for
   // them alone
   const uint32_t k0 = kg0 * 32u, kq = nk * 8u;  // quads per row
-  constexpr uint32_t kXq = 16u * kDenseMaxH * 8u / 256u;
+  constexpr uint32_t kXq = 16u * kDenseMaxH * 8u / (NW * 64u);
   float4 xv[kXq];
 #pragma unroll
   for (uint32_t u = 0; u < kXq; ++u) {
-    const uint32_t i = threadIdx.x + u * 256u, j = i / kq, qq = i - j * kq, k = k0 + 4u * qq;
+    const uint32_t i = threadIdx.x + u * NW * 64u, j = i / kq, qq = i - j * kq, k = k0 + 4u * qq;
     xv[u] = (i < a.B * kq && k < a.K) ? *(const float4 *)(a.x + (size_t)j * a.K + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   uint4 wbuf[kDenseMaxH];
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseArgs a) {
     wbuf[s] = load_stream16(wt + (size_t)min(s, nk - 1u) * 1024u);
 #pragma unroll
   for (uint32_t u = 0; u < kXq; ++u) {
-    const uint32_t i = threadIdx.x + u * 256u, j = i / kq, qq = i - j * kq;
+    const uint32_t i = threadIdx.x + u * NW * 64u, j = i / kq, qq = i - j * kq;
     if (i >= a.B * kq) continue;
     const float vv[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
     uint32_t hi[2], lo[2];
@@ -943,7 +945,8 @@ burnext_status dense_gemv(const DenseMat &m, const float *x, uint32_t B, float *
   a.H = m.H;
   a.part_stride = (uint64_t)B * m.N;
   const size_t lds = 2ull * 16 * (m.H * 32 + 8) * 2;
-  return hip_check(launch_kernel(dense_gemv_kernel, dim3((uint32_t)cdiv(m.ntiles, 4), m.parts), dim3(256), lds, s, a),
+  return hip_check(launch_kernel(dense_gemv_kernel<kDenseWaves>, dim3((uint32_t)cdiv(m.ntiles, kDenseWaves), m.parts),
+                                 dim3(kDenseWaves * 64), lds, s, a),
                    "dense GEMV launch");
 }
 
