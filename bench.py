@@ -134,12 +134,22 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / steps
 
-    # per-kernel execution times over a second pass of the same steps
+    # per-kernel execution times over a second pass of the same steps.  A first recorded pass fills
+    # each layer's pool of event pairs (read and discarded), so the measured pass creates no events
+    # between its launches; the measured pass's own step time is kept beside the untimed one.
     for L in layers:
         L.profile_enable(True)
     for i in range(steps):
         step(i)
     torch.cuda.synchronize()
+    for L in layers:
+        L.profile_read()
+    start.record()
+    for i in range(steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    ms_step_prof = start.elapsed_time(end) / steps
     kern = {}
     for L in layers:
         L.profile_enable(False)
@@ -148,7 +158,13 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
             a[0] += ms
             a[1] += cnt
     kavg_us = {k: (v[0] / v[1] * 1e3) for k, v in kern.items() if v[1]}
-    log(f"{name}: {ms_step * 1e3:.1f} us/step, kernels {', '.join(f'{k} {v:.1f}' for k, v in kavg_us.items())}")
+    # every kernel of a step runs on one stream, one launch each: their durations cannot sum past the step
+    ksum_us = sum(v[0] for v in kern.values()) * 1e3 / steps
+    log(f"{name}: {ms_step * 1e3:.1f} us/step ({ms_step_prof * 1e3:.1f} in the timed-dispatch pass), kernels "
+        f"{', '.join(f'{k} {v:.1f}' for k, v in kavg_us.items())}, sum {ksum_us:.1f}")
+    if ksum_us > ms_step_prof * 1e3:
+        log(f"{name}: WARNING kernel durations sum to {ksum_us:.1f} us, above the timed pass's "
+            f"{ms_step_prof * 1e3:.1f} us step")
 
     # algorithmic bytes / FLOPs per launch (realised routing; bf16 biases, router, activations)
     nk = T * K
@@ -198,6 +214,8 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         "layer_hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "layer_algorithmic_bytes": layer_bytes,
         "kernels_avg_us": {k: round(v, 2) for k, v in kavg_us.items()},
+        "kernels_sum_us": round(ksum_us, 2),
+        "ms_per_step_timed_pass": round(ms_step_prof, 5),
         "roofline": roof,
     }
     if prefill:
@@ -435,8 +453,9 @@ def main():
                 use = layers[:WORKLOADS[name]["copies"]]
                 r = measure(name, use, bdata, args.steps, args.warmup, False, 0)
                 sweep[name.split("_")[1]] = {k: r[k] for k in ("value", "unit", "ms_per_step", "layer_hbm_frac",
-                                                                "layer_fp4_mfma_util", "kernels_avg_us", "roofline",
-                                                                "config") if k in r}
+                                                                "layer_fp4_mfma_util", "kernels_avg_us",
+                                                                "kernels_sum_us", "ms_per_step_timed_pass",
+                                                                "roofline", "config") if k in r}
             out["sweep_120b"] = sweep
             for L in layers:
                 L.close()

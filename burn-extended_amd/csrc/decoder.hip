@@ -43,7 +43,7 @@ burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnex
                                      uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
                                      const float *gamma, float eps, float *xn, bool *norm_done, const float *part,
                                      uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid);
-bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n);
+bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n, uint32_t nparts);
 }  // namespace burnext
 
 using namespace burnext;
@@ -848,6 +848,7 @@ struct burnext_gptoss {
   uint32_t cap_p = 0;        // cache_len rounded up to 64 rows
   uint64_t layer_cache = 0;  // elements per layer
   uint32_t used = 0;         // cache rows held
+  uint32_t cache_batch = 0;  // batch rows whose cache holds all `used` rows (0 while used == 0)
   uint64_t pos_next = 0;     // positions seen
   std::vector<void *> allocs;
 };
@@ -1193,6 +1194,7 @@ burnext_status burnext_gptoss_workspace_size(burnext_gptoss_t M, uint32_t batch,
 burnext_status burnext_gptoss_reset(burnext_gptoss_t M) {
   if (!M) return set_error(BURNEXT_INVALID_ARG, "null model");
   M->used = 0;
+  M->cache_batch = 0;
   M->pos_next = 0;
   return set_error(BURNEXT_OK, "");
 }
@@ -1225,6 +1227,7 @@ burnext_status burnext_gptoss_cache_load(burnext_gptoss_t M, const float *k, con
       if (st != BURNEXT_OK) return st;
     }
   M->used = len;
+  M->cache_batch = len ? batch : 0u;
   M->pos_next = len;
   return set_error(BURNEXT_OK, "");
 }
@@ -1235,6 +1238,14 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
   if (!M || !tokens || !next_tokens) return set_error(BURNEXT_INVALID_ARG, "null model, tokens or next_tokens");
   const auto &c = M->cfg;
   if (B == 0 || B > c.max_batch) return set_error(BURNEXT_INVALID_ARG, "batch must be in [1, max_batch]");
+  if (M->used > 0 && B > M->cache_batch) {
+    // rows >= cache_batch hold no entries for the cached positions (the reference's cache is
+    // sized for one batch): decoding them would attend over rows that were never written
+    char buf[160];
+    snprintf(buf, sizeof(buf), "batch %u exceeds the %u batch rows the cache holds (reset first)", B,
+             M->cache_batch);
+    return set_error(BURNEXT_INVALID_ARG, buf);
+  }
   if (pos != M->pos_next) {
     char buf[160];
     snprintf(buf, sizeof(buf), "pos %u is not the next position (%llu positions seen)", pos,
@@ -1327,7 +1338,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     // layer's attention norm, after the last layer the final norm) when its path allows
     const float *next_gamma = l + 1 < c.n_layers ? M->norm_attn + (size_t)(l + 1) * D : M->norm_final;
     const float *bo = M->bo + (size_t)l * D;
-    if (moe_front_fusable(M->moe[l], B)) {
+    if (moe_front_fusable(M->moe[l], B, M->wo[l].parts)) {
       // its router also forms the residual hid2 = hid + (sum of the output projection's parts + bo)
       st = moe_forward_post_norm(M->moe[l], hid2, BURNEXT_F32, hid, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
                                  stream, next_gamma, c.rms_eps, xn, &normed, part, (uint64_t)B * D, M->wo[l].parts,
@@ -1362,6 +1373,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
   st = hip_check(launch_kernel(argmax_kernel, dim3(B), dim3(256), 0, s, ga), "argmax launch");
   if (st != BURNEXT_OK) return st;
   M->used = used;
+  M->cache_batch = B;  // only rows < B received this position's entry
   M->pos_next = (uint64_t)pos + 1;
   return set_error(BURNEXT_OK, "");
 }

@@ -104,7 +104,8 @@ struct burnext_moe_layer {
   int num_cus = 256;
   std::mutex prof_mu;
   bool profiling = false;
-  std::vector<ProfPair> prof;
+  std::vector<ProfPair> prof;  // pairs bound to dispatches since the last read
+  std::vector<ProfPair> prof_free;  // created pairs not in use (reused by later launches)
 };
 
 namespace burnext {
@@ -237,10 +238,11 @@ void free_layer(burnext_moe_layer *L) {
                   (void *)L->w2.scales, (void *)L->w2.gscales,
                   (void *)L->b1, (void *)L->b2, L->router_w, L->router_wg, (void *)L->router_b, (void *)L->gamma})
     if (p) (void)hipFree(p);
-  for (auto &pp : L->prof) {
-    (void)hipEventDestroy(pp.a);
-    (void)hipEventDestroy(pp.b);
-  }
+  for (auto *v : {&L->prof, &L->prof_free})
+    for (auto &pp : *v) {
+      (void)hipEventDestroy(pp.a);
+      (void)hipEventDestroy(pp.b);
+    }
   delete L;
 }
 
@@ -464,13 +466,24 @@ struct ProfScope final : LaunchTimer {
   }
   bool pair(hipEvent_t &a, hipEvent_t &b) override {
     a = b = nullptr;
-    if (hipEventCreate(&a) != hipSuccess) return false;
-    if (hipEventCreate(&b) != hipSuccess) {
+    std::lock_guard<std::mutex> lk(L->prof_mu);
+    if (!L->prof_free.empty()) {  // a pair from an earlier read: no event creation between launches
+      ProfPair pp = L->prof_free.back();
+      L->prof_free.pop_back();
+      pp.kernel = k;
+      L->prof.push_back(pp);
+      a = pp.a;
+      b = pp.b;
+      return true;
+    }
+    // timing-only events: no system-scope fence when they complete (that fence's cache write-back
+    // and invalidate would be charged to the dispatch and slow the next one)
+    if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return false;
+    if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
       (void)hipEventDestroy(a);
       a = nullptr;
       return false;
     }
-    std::lock_guard<std::mutex> lk(L->prof_mu);
     L->prof.push_back({a, b, k});
     return true;
   }
@@ -776,6 +789,8 @@ burnext_status scratch_address(int device, void **out) {
 
 namespace burnext {
 
+bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n, uint32_t nparts);
+
 // burnext_moe_forward; with pn, the RmsNorm of y (pn->gamma, pn->eps into pn->out) runs inside the
 // combine where the path allows it (decode-sized GEMV path, f32 rows), and *norm_done says whether
 // it did (otherwise the caller normalises y itself).
@@ -784,7 +799,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
                             bool *norm_done, const PreAdd *pa = nullptr) {
   if (norm_done) *norm_done = false;
   if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
-  if (pa && (x != pa->xout || x_dtype != BURNEXT_F32 || !front_ok(*L, n)))
+  if (pa && (x != pa->xout || x_dtype != BURNEXT_F32 || !moe_front_fusable(L, n, pa->nparts)))
     return fail(BURNEXT_INVALID_ARG, "formed input rows need f32 rows, x == xout and a decode-sized batch");
   if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
   if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
@@ -918,7 +933,11 @@ burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnex
                       norm_done, part ? &pa : nullptr);
 }
 
-bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n) { return L && front_ok(*L, n); }
+// nparts: the K-part partial sums of the output projection the router adds (router_front_kernel
+// takes at most kFrontMaxParts of them; more run the separate residual add).
+bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n, uint32_t nparts) {
+  return L && nparts >= 1u && nparts <= kFrontMaxParts && front_ok(*L, n);
+}
 
 }  // namespace burnext
 
@@ -1222,12 +1241,14 @@ burnext_status burnext_moe_profile_read(burnext_moe_layer_t L, double *ms_total,
     float ms = 0.0f;
     if (hipEventSynchronize(pp.b) != hipSuccess || hipEventElapsedTime(&ms, pp.a, pp.b) != hipSuccess)
       st = BURNEXT_DEVICE_ERROR;
-    if (pp.kernel < n_kernels) {
+    if (pp.kernel >= 0 && pp.kernel < n_kernels) {
       ms_total[pp.kernel] += ms;
       launches[pp.kernel] += 1;
     }
-    (void)hipEventDestroy(pp.a);
-    (void)hipEventDestroy(pp.b);
+  }
+  {  // the pairs are complete: back to the pool for the next launches
+    std::lock_guard<std::mutex> lk(L->prof_mu);
+    L->prof_free.insert(L->prof_free.end(), pend.begin(), pend.end());
   }
   if (st != BURNEXT_OK) return fail(st, "event synchronisation failed");
   return ok();

@@ -87,7 +87,9 @@ burnext_status burnext_gptoss_cache_load(burnext_gptoss_t model, const float *k,
                                          uint32_t len, void *stream);
 
 /* One decode step: tokens[batch] (device int32) at absolute position `pos`, which must equal the
- * number of positions seen so far.  `window` is the caller's AttnWindow (0 = Full, w > 0 =
+ * number of positions seen so far.  While the cache holds rows, batch may not exceed the batch
+ * rows it holds them for (those of the last cache_load or decode; BURNEXT_INVALID_ARG, reset
+ * first).  `window` is the caller's AttnWindow (0 = Full, w > 0 =
  * Window(w)), combined with each layer's policy window as combine_windows does (the smaller).
  * next_tokens[batch] (device int32) = argmax of the logits (lowest index on ties, NaN lowest);
  * logits [batch, V] f32 (device, nullable); hidden [batch, D] f32 (device, nullable): the last

@@ -156,7 +156,9 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
                                      void *out, burnext_dtype out_dtype, void *stream);
 
 /* Per-kernel timing hook (a HIP event pair bound to each kernel dispatch of forward through
- * hipExtLaunchKernel: the kernel's own begin and end timestamps).
+ * hipExtLaunchKernel: the kernel's own begin and end timestamps; timing-only events without the
+ * system-scope fence, kept in a per-layer pool: a read returns its pairs to the pool, so a second
+ * recorded pass creates no events between its launches).
  * enable != 0 starts recording; read returns, per kernel id, accumulated milliseconds and
  * launch counts since the last read (it synchronises on the recorded events) and resets.
  * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine, 6 SwiGLU of the gate_up

@@ -150,6 +150,40 @@ def test_decode_argument_errors(D):
     torch.cuda.synchronize()
 
 
+def test_decode_c5_full_size(D, oracle):
+    """The benchmark's C5 decoder itself (24 layers, d_model 2880, 64 q / 8 kv heads of 64,
+    alternating 128-row window and full layers with learned sinks, YaRN factor 32 base 150000,
+    vocabulary 201088, 32 experts top-4, f32 cache of 8192 rows, batch 8; the bench's weights,
+    seed 0): the cache loaded with 8191 rows, two greedy steps -- the first fills the cache, the
+    second evicts its oldest row -- against the decoder oracle's logits, hidden state and tokens."""
+    cfg = D.GptOssConfig(max_seq_len=8192 + 64)
+    assert (cfg.n_layers, cfg.vocab_size, cfg.cache_len) == (24, 201088, 8192)
+    print("[decoder] C5 full size: generating weights", flush=True)
+    data = D.make_decoder(cfg, seed=0, sinks_std=0.5)
+    B, pre = 8, cfg.cache_len - 1
+    rng = np.random.default_rng(7)
+    shape = (cfg.n_layers, B, pre, cfg.kv_heads, cfg.head_dim)
+    k = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.6)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    dev.cache_load(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    orc = oracle.DecoderOracle(data, B)
+    orc.load(k, v)
+    del k, v
+    tok = (np.arange(B, dtype=np.int32) * 1009) % cfg.vocab_size
+    for pos in range(pre, pre + 2):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        torch.cuda.synchronize()
+        print(f"[decoder] C5 full size: GPU step at pos {pos} done, oracle step", flush=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        print(f"C5 pos {pos}: logits max-abs-rel {oracle.max_abs_rel(_np(lg), o_lg):.3e}, hidden "
+              f"{oracle.max_abs_rel(_np(hid), o_hid):.3e}, tokens {_np(nxt).astype(int).tolist()} / {o_nxt.tolist()}",
+              flush=True)
+        _check_step(oracle, TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, pos)
+        tok = o_nxt
+    dev.close()
+
+
 @pytest.mark.parametrize("kv_bf16", [False, True])
 def test_decode_20b_shapes_full_cache(D, oracle, kv_bf16):
     """GPT-OSS-20B layer shapes (d_model 2880, 64 q / 8 kv heads of 64, 32 experts top-4, 128-row
