@@ -63,7 +63,8 @@ class GptOssConfigC(ctypes.Structure):
                                                "max_batch", "cache_len", "window_policy", "window", "full_on_even",
                                                "rope_head_stride", "max_positions", "kv_bf16")] + \
                [(n, ctypes.c_float) for n in ("rms_eps", "rope_theta", "rope_scaling_factor", "rope_initial_context",
-                                              "rope_ntk_alpha", "rope_ntk_beta", "scale_dk")]
+                                              "rope_ntk_alpha", "rope_ntk_beta", "scale_dk")] + \
+               [("sink_tokens", ctypes.c_uint32)]
 
 
 class GptOssWeightsC(ctypes.Structure):

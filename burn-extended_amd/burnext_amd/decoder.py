@@ -31,7 +31,10 @@ class GptOssConfig:
 
     ``window_policy`` / ``window`` / ``full_on_even`` are WindowPolicy (Full, Fixed(window),
     EveryOther { window, full_on_even }); ``max_seq_len`` bounds the
-    decode positions (the RoPE table length).  Beyond the reference: ``rope_theta`` (the reference
+    decode positions (the RoPE table length); ``sink_tokens`` (default 0, as the reference's
+    default, src/models/gpt_oss.rs:70) keeps the first positions' cache rows through eviction and
+    widens each window by that many rows (src/attention/streaming_mqa.rs:332-339).  Beyond the
+    reference: ``rope_theta`` (the reference
     takes Burn's default base 10000; GPT-OSS uses 150000), ``rope_head_stride`` (1 = the
     reference's head-indexed RoPE positions, 0 = one position per token), ``scale_dk`` (scores
     divided by sqrt(scale_dk); 1 = pre-scaled q/k as the reference's GPT-OSS layers) and
@@ -63,6 +66,7 @@ class GptOssConfig:
     scale_dk: float = 1.0
     rms_eps: float = 1e-5
     kv_bf16: bool = False
+    sink_tokens: int = 0  # rows of the first positions the cache keeps through eviction (< cache_len)
 
     @property
     def window_policy_code(self) -> int:
@@ -83,7 +87,8 @@ class GptOssConfig:
                                int(self.full_on_even),
                                int(self.rope_head_stride), self.max_seq_len, int(self.kv_bf16), self.rms_eps,
                                self.rope_theta, self.rope_scaling_factor if yarn else 1.0,
-                               self.rope_initial_context, self.rope_ntk_alpha, self.rope_ntk_beta, self.scale_dk)
+                               self.rope_initial_context, self.rope_ntk_alpha, self.rope_ntk_beta, self.scale_dk,
+                               self.sink_tokens)
 
 
 GPT_OSS_20B = GptOssConfig()

@@ -251,8 +251,8 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Attention, flash-decoding split.  Workgroup (chunk c, kv head g, batch b) covers positions
-// p = p_lo + 256 c + t (t < 256, p <= p_hi) of the active window [p_lo, p_hi], slot p mod cap,
-// for the G query heads of kv head g.
+// keys i = 256 c + t (t < 256, i < nkeys) of the active window (slots by key_slot), for the G
+// query heads of kv head g.
 //   scores: thread t, s[j] = (q[j] . k[p]) / sqrt(scale_dk) (q broadcast from LDS, k in
 //     dimension quads from the tiled K layout)
 //   m[j] = chunk maximum (wave maxima, then the 4 waves), e = exp(s - m) (0 outside the window),
@@ -266,9 +266,20 @@ struct AttnArgs {
   const float *q;        // [B][nH * dk]
   const void *kc, *vc;   // this layer's cache
   float *part;           // [B][kvH][nchunk][groups][dk + 2]
-  uint32_t nH, kvH, dk, cap, cap_p, p_lo, p_hi, nchunk;
+  uint32_t nH, kvH, dk, cap_p, nchunk;
+  // the active window's keys i < nkeys: the sink rows first (i < nsk: slot sk_lo + i, holding
+  // position sk_lo + i), then the recent positions p_lo + (i - nsk) at their ring slots
+  uint32_t nkeys, nsk, sk_lo, p_lo, sink, ring;  // ring = cache_len - sink
   float inv_scale;       // 1 / sqrt(scale_dk)
 };
+
+// Cache slot of key i of the active window.  The cache keeps the first `sink` positions in slots
+// 0 .. sink - 1 and every later position p in slot sink + (p - sink) mod (cache_len - sink): the
+// rows the reference's evict-and-roll keeps (src/attention/cache_ops.rs:64-117), without moving
+// any row (sink = 0: slot p mod cache_len).
+__device__ __forceinline__ uint32_t key_slot(const AttnArgs &a, uint32_t i) {
+  return i < a.nsk ? a.sk_lo + i : a.sink + (a.p_lo - a.sink + (i - a.nsk)) % a.ring;
+}
 
 template <typename KV, uint32_t G>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
@@ -281,15 +292,15 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
   const KV *kc = (const KV *)a.kc, *vc = (const KV *)a.vc;
   for (uint32_t i = t; i < G * dk; i += blockDim.x) q_l[i] = a.q[(size_t)b * a.nH * dk + (size_t)g * G * dk + i];
   __syncthreads();
-  const uint32_t p0 = a.p_lo + c * kAttnChunk, p = p0 + t;
-  const bool valid = p <= a.p_hi;
+  const uint32_t i0 = c * kAttnChunk, ki = i0 + t;  // this chunk's first key, this thread's key
+  const bool valid = ki < a.nkeys;
   float s[G];
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) s[j] = 0.0f;
   {
     // dimension quads in batches of 8 loads in flight (quads past dk and keys outside the window
     // read a valid slot and are not used)
-    const KV *kr = kc + k_index(b, g, valid ? p % a.cap : 0u, 0u, a.kvH, a.cap_p, dk);
+    const KV *kr = kc + k_index(b, g, valid ? key_slot(a, ki) : 0u, 0u, a.kvH, a.cap_p, dk);
     for (uint32_t q0 = 0; q0 < nq; q0 += 8u) {
       float kv[8][4];
 #pragma unroll
@@ -326,7 +337,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
   }
   __syncthreads();
   const uint32_t kq = t >> 4, dq = t & 15u;
-  const uint32_t nkeys = min(kAttnChunk, a.p_hi + 1u - p0);
+  const uint32_t nkeys = min(kAttnChunk, a.nkeys - i0);
   float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)G * (dk + 2u);
   for (uint32_t dbase = 0; dbase < nq; dbase += 16u) {
     const uint32_t dqq = dbase + dq;
@@ -340,7 +351,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
         for (uint32_t u = 0; u < 4u; ++u) {
           const uint32_t key = min(k0 + 16u * u, nkeys - 1u);
-          kv_load4(vc + v_index(b, g, (p0 + key) % a.cap, 4u * dqq, a.kvH, a.cap_p, dk), v[u]);
+          kv_load4(vc + v_index(b, g, key_slot(a, i0 + key), 4u * dqq, a.kvH, a.cap_p, dk), v[u]);
         }
 #pragma unroll
         for (uint32_t u = 0; u < 4u; ++u) {
@@ -438,16 +449,16 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
   const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const uint32_t dk = a.dk, nq = dk / 4u, t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const KV *kc = (const KV *)a.kc, *vc = (const KV *)a.vc;
-  const uint32_t p0 = a.p_lo + c * kAttnChunk, p = p0 + t;
-  const bool valid = p <= a.p_hi;
-  const uint32_t nkeys = min(kAttnChunk, a.p_hi + 1u - p0);
+  const uint32_t i0 = c * kAttnChunk, ki = i0 + t;  // this chunk's first key, this thread's key
+  const bool valid = ki < a.nkeys;
+  const uint32_t nkeys = min(kAttnChunk, a.nkeys - i0);
   // requests: q quad, K quads, value quads
   const uint32_t nqq = G * nq;  // q quads of this kv head's G query heads (<= 128)
   const float *qsrc = a.q + (size_t)b * a.nH * dk + (size_t)g * G * dk;
   const float4 qv = *(const float4 *)(qsrc + 4u * min(t, nqq - 1u));
   __builtin_amdgcn_sched_barrier(0);  // q first: its wait then leaves the K and V loads in flight
   RawQ<KV> kr[16];
-  const KV *kb = kc + k_index(b, g, (valid ? p : p0) % a.cap, 0u, a.kvH, a.cap_p, dk);
+  const KV *kb = kc + k_index(b, g, key_slot(a, valid ? ki : i0), 0u, a.kvH, a.cap_p, dk);
 #pragma unroll
   for (uint32_t u = 0; u < 16u; ++u) raw_load(kb + (size_t)min(u, nq - 1u) * 256u, kr[u]);
   const uint32_t kq = t >> 4, dq = t & 15u, dqc = min(dq, nq - 1u);
@@ -455,7 +466,7 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
 #pragma unroll
   for (uint32_t i = 0; i < 16u; ++i) {
     const uint32_t key = min(kq + 16u * i, nkeys - 1u);
-    raw_load(vc + v_index(b, g, (p0 + key) % a.cap, 4u * dqc, a.kvH, a.cap_p, dk), vr[i]);
+    raw_load(vc + v_index(b, g, key_slot(a, i0 + key), 4u * dqc, a.kvH, a.cap_p, dk), vr[i]);
   }
   if (t < nqq) *(float4 *)(q_l + 4u * t) = qv;
   __syncthreads();
@@ -1048,6 +1059,7 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
     return set_error(BURNEXT_INVALID_ARG, "rope_head_stride, kv_bf16 and full_on_even must be 0 or 1");
   if (c.window_policy > 2) return set_error(BURNEXT_INVALID_ARG, "window_policy must be 0 (Full), 1 (Fixed) or 2 (EveryOther)");
   if (c.window_policy != 0 && c.window == 0) return set_error(BURNEXT_INVALID_ARG, "window must be positive");
+  if (c.sink_tokens >= c.cache_len) return set_error(BURNEXT_INVALID_ARG, "sink_tokens must be below cache_len");
   if (c.cache_len > (1u << 30) || c.max_positions > (1u << 30))
     return set_error(BURNEXT_UNSUPPORTED, "cache_len and max_positions above 2^30 are not supported");
   if ((c.n_heads % c.kv_heads) == 0 && (cdiv(c.cache_len, kAttnChunk) + 1) * (c.n_heads / c.kv_heads) > 16384)
@@ -1271,7 +1283,15 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
   int32_t *bidx = (int32_t *)(base + w.bidx);
   void *moe_ws = base + w.moe;
   const uint32_t D = c.d_model, dk = c.head_dim, cap = c.cache_len, N3 = M->qd + 2 * M->kd;
-  const uint32_t used = (uint32_t)std::min<uint64_t>((uint64_t)M->used + 1, cap), slot = pos % cap;
+  // cache rows after this step's append (the reference's local_end_index) and the new row's slot:
+  // the first sink positions keep slots 0 .. sink - 1, later positions cycle over the others
+  const uint32_t S = c.sink_tokens, ring = cap - S;
+  const uint32_t used = (uint32_t)std::min<uint64_t>((uint64_t)M->used + 1, cap);
+  const uint32_t slot = pos < S ? pos : S + (pos - S) % ring;
+  if (used < S)  // Window(w) spans the last sink + min(w, rows - sink) rows: it needs the sink rows
+    for (uint32_t l = 0; l < c.n_layers; ++l)
+      if (layer_window(c, l, window) != 0)
+        return set_error(BURNEXT_INVALID_ARG, "a windowed layer needs at least sink_tokens cache rows");
   {
     EmbedArgs a{tokens, M->emb, hid, D, c.vocab_size};
     st = hip_check(launch_kernel(embed_kernel, dim3((uint32_t)cdiv(D, 256), B), dim3(256), 0, s, a), "embedding launch");
@@ -1309,7 +1329,8 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
                    "q/k/v post launch");
     if (st != BURNEXT_OK) return st;
     const uint32_t lw = layer_window(c, l, window);  // 0 = Full
-    const uint32_t active = lw ? std::min(lw, used) : used;
+    // Full: every row; Window(lw): the last sink + min(lw, rows - sink) rows (used >= S checked)
+    const uint32_t active = lw ? S + std::min(lw, used - S) : used;
     AttnArgs aa{};
     aa.q = qb;
     aa.kc = qa.kc;
@@ -1318,11 +1339,18 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     aa.nH = c.n_heads;
     aa.kvH = c.kv_heads;
     aa.dk = dk;
-    aa.cap = cap;
     aa.cap_p = M->cap_p;
-    aa.p_hi = pos;
-    aa.p_lo = pos + 1 - active;
-    aa.nchunk = (uint32_t)cdiv(active, kAttnChunk);
+    // window rows [used - active, used) of the reference's cache order: the sink rows among them
+    // (rows < sink hold positions 0 .. sink - 1), then rows >= sink, which hold the latest positions
+    const uint32_t wstart = used - active, nsink_rows = std::min(S, used);
+    aa.nsk = wstart < nsink_rows ? nsink_rows - wstart : 0u;
+    aa.sk_lo = wstart;
+    const uint32_t nrec = used - std::max(wstart, S < used ? S : used);
+    aa.p_lo = pos + 1 - nrec;
+    aa.nkeys = aa.nsk + nrec;
+    aa.sink = S;
+    aa.ring = ring;
+    aa.nchunk = (uint32_t)cdiv(aa.nkeys, kAttnChunk);
     aa.inv_scale = 1.0f / std::sqrt(c.scale_dk);
     const dim3 agrid(aa.nchunk, c.kv_heads, B);
     st = hip_check(launch_attention(c.kv_bf16 != 0, M->groups, agrid, s, aa), "attention launch");

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <new>
 #include <string>
@@ -62,10 +63,29 @@ struct DeviceGuard {
   }
 };
 
-struct ProfPair {
-  hipEvent_t a, b;
-  int kernel;
+// Timed dispatches of the profiling hook (process-wide: the previous dispatch on a stream may
+// belong to another layer).  A dispatch queued behind a running kernel can take its begin stamp
+// before that kernel ends, so a dispatch's time is the exclusive part of its interval:
+// end - max(begin, end of the previous timed dispatch on the same stream).  Pairs read by a
+// layer wait in `done` until the next enable finds nothing pending (a pending record may still
+// refer to their end events), then return to the device's pool.
+struct ProfRec {
+  hipEvent_t a, b;      // dispatch begin / end
+  hipEvent_t prev_end;  // end event of the previous timed dispatch on the same stream, or null
+  const void *layer;
+  int kernel, device;
 };
+struct Profiler {
+  std::mutex mu;
+  std::vector<ProfRec> pending;
+  std::vector<ProfRec> done;
+  std::map<int, std::vector<std::pair<hipEvent_t, hipEvent_t>>> pool;  // per device
+  std::map<hipStream_t, hipEvent_t> last_end;
+};
+Profiler &profiler() {
+  static Profiler *p = new Profiler;  // never destroyed: its events may outlive every layer
+  return *p;
+}
 
 }  // namespace
 
@@ -102,10 +122,7 @@ struct burnext_moe_layer {
   float *router_b = nullptr;  // [E]
   float *gamma = nullptr;     // [D]
   int num_cus = 256;
-  std::mutex prof_mu;
   bool profiling = false;
-  std::vector<ProfPair> prof;  // pairs bound to dispatches since the last read
-  std::vector<ProfPair> prof_free;  // created pairs not in use (reused by later launches)
 };
 
 namespace burnext {
@@ -238,11 +255,17 @@ void free_layer(burnext_moe_layer *L) {
                   (void *)L->w2.scales, (void *)L->w2.gscales,
                   (void *)L->b1, (void *)L->b2, L->router_w, L->router_wg, (void *)L->router_b, (void *)L->gamma})
     if (p) (void)hipFree(p);
-  for (auto *v : {&L->prof, &L->prof_free})
-    for (auto &pp : *v) {
-      (void)hipEventDestroy(pp.a);
-      (void)hipEventDestroy(pp.b);
-    }
+  {  // its unread timed dispatches: their events stay (later records may refer to them)
+    Profiler &P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    for (size_t i = 0; i < P.pending.size();)
+      if (P.pending[i].layer == L) {
+        P.done.push_back(P.pending[i]);
+        P.pending.erase(P.pending.begin() + (std::ptrdiff_t)i);
+      } else {
+        ++i;
+      }
+  }
   delete L;
 }
 
@@ -451,14 +474,15 @@ thread_local bool g_untimed = false;
 
 // While profiling is on, binds a HIP event pair to every kernel dispatch launched in its scope
 // (hipExtLaunchKernel through the thread's LaunchTimer), recorded under kernel id k: the pair
-// measures each dispatch's own execution, as rocprofv3's kernel trace does.
+// carries the dispatch's own begin and end, as rocprofv3's kernel trace does.
 struct ProfScope final : LaunchTimer {
   burnext_moe_layer *L;
+  hipStream_t s;
   int k;
   LaunchTimer *prev;
   bool on;
-  ProfScope(burnext_moe_layer *L_, hipStream_t, int k_)
-      : L(L_), k(k_), prev(g_launch_timer), on(L_->profiling && !g_untimed) {
+  ProfScope(burnext_moe_layer *L_, hipStream_t s_, int k_)
+      : L(L_), s(s_), k(k_), prev(g_launch_timer), on(L_->profiling && !g_untimed) {
     if (on) g_launch_timer = this;
   }
   ~ProfScope() override {
@@ -466,25 +490,26 @@ struct ProfScope final : LaunchTimer {
   }
   bool pair(hipEvent_t &a, hipEvent_t &b) override {
     a = b = nullptr;
-    std::lock_guard<std::mutex> lk(L->prof_mu);
-    if (!L->prof_free.empty()) {  // a pair from an earlier read: no event creation between launches
-      ProfPair pp = L->prof_free.back();
-      L->prof_free.pop_back();
-      pp.kernel = k;
-      L->prof.push_back(pp);
-      a = pp.a;
-      b = pp.b;
-      return true;
+    Profiler &P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    auto &pool = P.pool[L->device];
+    if (!pool.empty()) {  // a pair from an earlier pass: no event creation between launches
+      a = pool.back().first;
+      b = pool.back().second;
+      pool.pop_back();
+    } else {
+      // timing-only events: no system-scope fence when they complete (that fence's cache
+      // write-back and invalidate would be charged to the dispatch and slow the next one)
+      if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return false;
+      if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        a = nullptr;
+        return false;
+      }
     }
-    // timing-only events: no system-scope fence when they complete (that fence's cache write-back
-    // and invalidate would be charged to the dispatch and slow the next one)
-    if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return false;
-    if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
-      (void)hipEventDestroy(a);
-      a = nullptr;
-      return false;
-    }
-    L->prof.push_back({a, b, k});
+    auto it = P.last_end.find(s);
+    P.pending.push_back({a, b, it == P.last_end.end() ? nullptr : it->second, L, k, L->device});
+    P.last_end[s] = b;
     return true;
   }
 };
@@ -1221,6 +1246,15 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t L, int enable) {
   if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
   L->profiling = enable != 0;
+  if (enable) {
+    Profiler &P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    if (P.pending.empty()) {  // nothing refers to the read pairs any more: reuse them
+      for (auto &r : P.done) P.pool[r.device].push_back({r.a, r.b});
+      P.done.clear();
+      P.last_end.clear();
+    }
+  }
   return ok();
 }
 
@@ -1230,25 +1264,34 @@ burnext_status burnext_moe_profile_read(burnext_moe_layer_t L, double *ms_total,
     ms_total[k] = 0.0;
     launches[k] = 0;
   }
-  std::vector<ProfPair> pend;
+  Profiler &P = profiler();
+  std::vector<ProfRec> mine;
   {
-    std::lock_guard<std::mutex> lk(L->prof_mu);
-    pend.swap(L->prof);
+    std::lock_guard<std::mutex> lk(P.mu);
+    for (size_t i = 0; i < P.pending.size();)
+      if (P.pending[i].layer == L) {
+        mine.push_back(P.pending[i]);
+        P.pending.erase(P.pending.begin() + (std::ptrdiff_t)i);
+      } else {
+        ++i;
+      }
   }
   DeviceGuard guard(L->device);
   burnext_status st = BURNEXT_OK;
-  for (auto &pp : pend) {
-    float ms = 0.0f;
-    if (hipEventSynchronize(pp.b) != hipSuccess || hipEventElapsedTime(&ms, pp.a, pp.b) != hipSuccess)
+  for (auto &r : mine) {
+    float ms = 0.0f, gap = 0.0f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess)
       st = BURNEXT_DEVICE_ERROR;
-    if (pp.kernel >= 0 && pp.kernel < n_kernels) {
-      ms_total[pp.kernel] += ms;
-      launches[pp.kernel] += 1;
+    // exclusive part: not before the previous timed dispatch on the stream ended
+    if (r.prev_end && hipEventElapsedTime(&gap, r.prev_end, r.b) == hipSuccess && gap >= 0.0f && gap < ms) ms = gap;
+    if (r.kernel >= 0 && r.kernel < n_kernels) {
+      ms_total[r.kernel] += ms;
+      launches[r.kernel] += 1;
     }
   }
-  {  // the pairs are complete: back to the pool for the next launches
-    std::lock_guard<std::mutex> lk(L->prof_mu);
-    L->prof_free.insert(L->prof_free.end(), pend.begin(), pend.end());
+  {
+    std::lock_guard<std::mutex> lk(P.mu);
+    P.done.insert(P.done.end(), mine.begin(), mine.end());
   }
   if (st != BURNEXT_OK) return fail(st, "event synchronisation failed");
   return ok();

@@ -49,6 +49,12 @@ typedef struct burnext_gptoss_config {
   float rope_theta;        /* RoPE base */
   float rope_scaling_factor, rope_initial_context, rope_ntk_alpha, rope_ntk_beta; /* init_ntk_yarn */
   float scale_dk;          /* scores divided by sqrt(scale_dk): 1 for pre-scaled q/k (GPT-OSS) */
+  uint32_t sink_tokens;    /* GptOssConfig.sink_tokens (src/models/gpt_oss.rs:35,211), < cache_len: the
+                              cache keeps the rows of the first sink_tokens positions through eviction
+                              (src/attention/cache_ops.rs:64-117), and Window(w) attends over the last
+                              sink_tokens + min(w, rows - sink_tokens) cache rows
+                              (src/attention/streaming_mqa.rs:332-339); a windowed layer needs at least
+                              sink_tokens cache rows (BURNEXT_INVALID_ARG before any launch otherwise) */
 } burnext_gptoss_config;
 
 /* Dense weights (host, bf16 bit patterns, row-major [out, in] as Burn Linear's transposed weight;

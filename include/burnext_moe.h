@@ -157,10 +157,13 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
 
 /* Per-kernel timing hook (a HIP event pair bound to each kernel dispatch of forward through
  * hipExtLaunchKernel: the kernel's own begin and end timestamps; timing-only events without the
- * system-scope fence, kept in a per-layer pool: a read returns its pairs to the pool, so a second
- * recorded pass creates no events between its launches).
+ * system-scope fence).  A dispatch's time is the exclusive part of its interval, from
+ * max(begin, end of the previous timed dispatch on the same stream) to its end: a dispatch queued
+ * behind a running kernel can be stamped as begun before that kernel ends.
  * enable != 0 starts recording; read returns, per kernel id, accumulated milliseconds and
- * launch counts since the last read (it synchronises on the recorded events) and resets.
+ * launch counts since the last read (it synchronises on the recorded events) and resets.  Event
+ * pairs are pooled per process: an enable call made when every layer's records have been read
+ * returns them to the pool, so a later recorded pass creates no events between its launches.
  * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine, 6 SwiGLU of the gate_up
  * K-parts (batches of at most 16 tokens run top-k and dispatch as one kernel, recorded under id 1;
  * id 2 then records nothing; id 6 records only decode batches that touch few experts). */

@@ -51,6 +51,7 @@ typedef struct {
   int64_t vocab, d_model, n_layers, n_heads, kv_heads, head_dim, batch, cache_len;
   int64_t window_policy, window, full_on_even, rope_head_stride;
   float rms_eps, scale_dk;
+  int64_t sink_tokens;
 } oracle_dec_cfg;
 typedef struct {
   const float *tok_emb, *norm_attn, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo, *sinks, *norm_final, *lm_head,
@@ -208,10 +209,10 @@ static void moe_cases(void) {
 }
 
 static void decoder_cases(void) {
-  /* (V, D, L, nH, kvH, dk, B, cap, policy, window, full_on_even, stride, caller window) */
-  const int64_t cases[][13] = {{37, 40, 3, 4, 2, 16, 2, 5, 2, 3, 1, 1, 0},
-                               {29, 64, 2, 8, 1, 8, 3, 4, 1, 2, 0, 0, 3},
-                               {50, 32, 2, 2, 2, 32, 1, 6, 0, 1, 0, 1, 0}};
+  /* (V, D, L, nH, kvH, dk, B, cap, policy, window, full_on_even, stride, caller window, sink tokens) */
+  const int64_t cases[][14] = {{37, 40, 3, 4, 2, 16, 2, 5, 2, 3, 1, 1, 0, 0},
+                               {29, 64, 2, 8, 1, 8, 3, 4, 1, 2, 0, 0, 3, 1},
+                               {50, 32, 2, 2, 2, 32, 1, 6, 0, 1, 0, 1, 0, 2}};
   for (size_t ci = 0; ci < sizeof(cases) / sizeof(cases[0]); ++ci) {
     const int64_t *q = cases[ci];
     oracle_dec_cfg c;
@@ -229,6 +230,7 @@ static void decoder_cases(void) {
     c.rope_head_stride = q[11];
     c.rms_eps = 1e-5f;
     c.scale_dk = 1.0f;
+    c.sink_tokens = q[13];
     const int64_t V = c.vocab, D = c.d_model, L = c.n_layers, qd = c.n_heads * c.head_dim,
                   kd = c.kv_heads * c.head_dim, B = c.batch, steps = c.cache_len + 3;
     const int64_t npos = steps + c.n_heads;

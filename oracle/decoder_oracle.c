@@ -173,6 +173,7 @@ typedef struct {
   int64_t rope_head_stride; /* 1: reference positions (start_pos + head index), 0: start_pos */
   float rms_eps;
   float scale_dk;           /* 1 with pre-scaled q/k (GPT-OSS) */
+  int64_t sink_tokens;      /* StreamingMqaCache::sink_tokens (src/attention/streaming_mqa.rs:143) */
 } oracle_dec_cfg;
 
 /* Weights as f32 (the device's bf16 values), per layer l at offset l * (layer size). */
@@ -209,8 +210,8 @@ int oracle_decoder_step(const oracle_dec_cfg *c, const oracle_dec_weights *w, co
                         const int32_t *tokens, int64_t pos, int64_t caller_window, float *cache_k, float *cache_v,
                         int64_t *cache_used, float *logits, float *hidden_out, int32_t *next_tok) {
   const int64_t B = c->batch, D = c->d_model, nH = c->n_heads, kvH = c->kv_heads, dk = c->head_dim;
-  const int64_t qd = nH * dk, kd = kvH * dk, cap = c->cache_len;
-  if (B <= 0 || nH % kvH || cap <= 0) return ORACLE_INVALID;
+  const int64_t qd = nH * dk, kd = kvH * dk, cap = c->cache_len, sink = c->sink_tokens;
+  if (B <= 0 || nH % kvH || cap <= 0 || sink < 0 || sink > cap) return ORACLE_INVALID;
   float *h = (float *)malloc(sizeof(float) * B * D);
   float *xn = (float *)malloc(sizeof(float) * B * D);
   float *q = (float *)malloc(sizeof(float) * B * qd);
@@ -220,13 +221,28 @@ int oracle_decoder_step(const oracle_dec_cfg *c, const oracle_dec_weights *w, co
   float *o = (float *)malloc(sizeof(float) * B * D);
   float *h2 = (float *)malloc(sizeof(float) * B * D);
   for (int64_t b = 0; b < B; ++b) memcpy(h + b * D, w->tok_emb + (int64_t)tokens[b] * D, sizeof(float) * D);
-  /* cache append with eviction (streaming_mqa.rs:294-323, cache_ops.rs:64-117; sink_tokens = 0):
-   * one new row; when full, every row moves up by one (roll) and the new row goes last */
+  /* cache append with eviction (streaming_mqa.rs:294-323, cache_ops.rs:64-117), one new row: when
+   * the cache is full, num_evicted = 1 and avail = used - sink rows after the sink rows; with
+   * avail > 1 the rows [sink, used) roll left by one (row sink + i takes row sink + (i + 1) mod
+   * avail; the wrapped row is overwritten next), else (avail <= num_evicted) nothing moves; then
+   * local_end = used - 1 + 1 and the new row goes to local_end - 1 */
   int rc = ORACLE_OK;
   int64_t used = *cache_used;
   const int evict = used + 1 > cap;
-  const int64_t row = evict ? cap - 1 : used;
-  const int64_t nused = evict ? cap : used + 1;
+  const int64_t avail = used > sink ? used - sink : 0;
+  const int roll = evict && avail > 1;
+  const int64_t nused = evict ? used : used + 1;
+  const int64_t row = nused - 1;
+  /* the active window of every layer (streaming_mqa.rs:332-339): Full = all nused rows,
+   * Window(w) = the last sink + min(w, nused - sink) rows; a windowed layer with fewer than sink
+   * rows has no valid window (the reference's shapes disagree there) */
+  for (int64_t l = 0; l < c->n_layers && sink > 0; ++l) {
+    int64_t lw = 0;
+    if (c->window_policy == 1) lw = c->window;
+    if (c->window_policy == 2) lw = ((l % 2 == 0) == (c->full_on_even != 0)) ? 0 : c->window;
+    if (caller_window > 0) lw = lw == 0 ? caller_window : (caller_window < lw ? caller_window : lw);
+    if (lw > 0 && nused < sink) return ORACLE_INVALID;
+  }
   for (int64_t l = 0; l < c->n_layers; ++l) {
     rmsnorm_rows(h, B, D, w->norm_attn + l * D, c->rms_eps, xn);
     oracle_linear(xn, B, D, w->wq + l * qd * D, w->bq + l * qd, qd, q);
@@ -239,20 +255,20 @@ int oracle_decoder_step(const oracle_dec_cfg *c, const oracle_dec_weights *w, co
     const int64_t lstride = B * cap * kd;
     for (int64_t b = 0; b < B; ++b) {
       float *ck = cache_k + l * lstride + b * cap * kd, *cv = cache_v + l * lstride + b * cap * kd;
-      if (evict) {
-        memmove(ck, ck + kd, sizeof(float) * (size_t)((cap - 1) * kd));
-        memmove(cv, cv + kd, sizeof(float) * (size_t)((cap - 1) * kd));
+      if (roll) {  /* rows sink+1 .. used-1 move to sink .. used-2 (row used-1 is rewritten below) */
+        memmove(ck + sink * kd, ck + (sink + 1) * kd, sizeof(float) * (size_t)((avail - 1) * kd));
+        memmove(cv + sink * kd, cv + (sink + 1) * kd, sizeof(float) * (size_t)((avail - 1) * kd));
       }
       memcpy(ck + row * kd, kk + b * kd, sizeof(float) * kd);
       memcpy(cv + row * kd, vv + b * kd, sizeof(float) * kd);
     }
     /* window_for(l) (src/cache/mod.rs:15-33) combined with the caller's (combine_windows, 0 = Full);
-     * Full = every cached row, Window(w) = the last min(w, rows) rows */
+     * Full = every cached row, Window(w) = the last sink + min(w, rows - sink) rows */
     int64_t lw = 0;
     if (c->window_policy == 1) lw = c->window;
     if (c->window_policy == 2) lw = ((l % 2 == 0) == (c->full_on_even != 0)) ? 0 : c->window;
     if (caller_window > 0) lw = lw == 0 ? caller_window : (caller_window < lw ? caller_window : lw);
-    const int64_t active = lw > 0 ? (lw < nused ? lw : nused) : nused;
+    const int64_t active = lw > 0 ? sink + (lw < nused - sink ? lw : nused - sink) : nused;
     const int64_t start = nused - active;
     for (int64_t b = 0; b < B; ++b) {
       const float *ck = cache_k + l * lstride + b * cap * kd + start * kd;

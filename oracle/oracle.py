@@ -31,7 +31,7 @@ class _DecCfg(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("vocab", "d_model", "n_layers", "n_heads", "kv_heads", "head_dim",
                                               "batch", "cache_len", "window_policy", "window", "full_on_even",
                                               "rope_head_stride")] + \
-               [("rms_eps", ctypes.c_float), ("scale_dk", ctypes.c_float)]
+               [("rms_eps", ctypes.c_float), ("scale_dk", ctypes.c_float), ("sink_tokens", ctypes.c_int64)]
 
 
 class _DecWeights(ctypes.Structure):
@@ -314,7 +314,7 @@ class DecoderOracle:
                                _p(self.table, _f32p))
         self._cc = _DecCfg(cfg.vocab_size, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.kv_heads, cfg.head_dim, batch,
                            cfg.cache_len, cfg.window_policy_code, cfg.window, int(cfg.full_on_even),
-                           cfg.rope_head_stride, cfg.rms_eps, cfg.scale_dk)
+                           cfg.rope_head_stride, cfg.rms_eps, cfg.scale_dk, cfg.sink_tokens)
 
     def load(self, k, v) -> None:
         """Cache rows for positions 0 .. len-1 (k, v [L, B, len, kvH, dk])."""

@@ -204,9 +204,9 @@ def test_gptoss_struct_layouts_match_header():
 #include <stdio.h>
 #include "burnext_gptoss.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu\n", sizeof(burnext_gptoss_config), offsetof(burnext_gptoss_config, kv_bf16),
+  printf("%zu %zu %zu %zu %zu %zu\n", sizeof(burnext_gptoss_config), offsetof(burnext_gptoss_config, kv_bf16),
          offsetof(burnext_gptoss_config, rms_eps), offsetof(burnext_gptoss_config, scale_dk),
-         sizeof(burnext_gptoss_weights));
+         offsetof(burnext_gptoss_config, sink_tokens), sizeof(burnext_gptoss_weights));
   printf("%zu %zu\n", offsetof(burnext_gptoss_weights, sinks), offsetof(burnext_gptoss_weights, lm_head));
   return 0;
 }
@@ -218,7 +218,8 @@ int main(void) {
     assert r.returncode == 0, r.stderr
     vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     assert vals == [ctypes.sizeof(N.GptOssConfigC), N.GptOssConfigC.kv_bf16.offset, N.GptOssConfigC.rms_eps.offset,
-                    N.GptOssConfigC.scale_dk.offset, ctypes.sizeof(N.GptOssWeightsC), N.GptOssWeightsC.sinks.offset,
+                    N.GptOssConfigC.scale_dk.offset, N.GptOssConfigC.sink_tokens.offset,
+                    ctypes.sizeof(N.GptOssWeightsC), N.GptOssWeightsC.sinks.offset,
                     N.GptOssWeightsC.lm_head.offset]
 
 
@@ -252,6 +253,7 @@ def _gweights():
     (dict(window=0), N.BURNEXT_INVALID_ARG, "window"),
     (dict(window_policy=3), N.BURNEXT_INVALID_ARG, "window_policy"),
     (dict(scale_dk=0.0), N.BURNEXT_INVALID_ARG, "scale_dk"),
+    (dict(sink_tokens=32), N.BURNEXT_INVALID_ARG, "sink_tokens"),
     (dict(rope_theta=1.0), N.BURNEXT_INVALID_ARG, "rope_theta"),
     # YaRN thresholds: beta <= alpha makes low >= high (the reference asserts)
     (dict(rope_ntk_alpha=32.0, rope_ntk_beta=1.0), N.BURNEXT_INVALID_ARG, "YaRN"),

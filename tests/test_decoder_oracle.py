@@ -201,9 +201,11 @@ def _f64_model(oracle, data, batch):
             for b in range(batch):
                 rows = cache[l][b]
                 rows.append((rope(k[b].reshape(kvH, dk), pos), v[b].reshape(kvH, dk)))
-                if len(rows) > cfg.cache_len:
-                    rows.pop(0)
-                act = rows[-lw:] if lw else rows
+                S = cfg.sink_tokens
+                if len(rows) > cfg.cache_len:  # the oldest row after the sink rows leaves
+                    rows.pop(min(S, cfg.cache_len - 1))
+                n = len(rows)
+                act = rows[n - (S + min(lw, n - S)):] if lw else rows
                 qb = rope(q[b].reshape(nH, dk), pos)
                 for hh in range(nH):
                     sc = np.array([r[0][hh // g] @ qb[hh] for r in act]) / math.sqrt(cfg.scale_dk)
@@ -218,12 +220,23 @@ def _f64_model(oracle, data, batch):
         logits = _rms64(h, W["norm_final"], cfg.rms_eps) @ W["lm_head"].T
         return logits, hid
 
+    def load(k, v):  # cache rows [L, B, len, kvH, dk] for positions 0 .. len-1
+        for l in range(cfg.n_layers):
+            for b in range(batch):
+                cache[l][b][:] = [(k[l, b, r].astype(np.float64), v[l, b, r].astype(np.float64))
+                                  for r in range(k.shape[2])]
+
+    step.load = load
     return step
 
 
 @pytest.mark.parametrize("kw,window", [(dict(), 0), (dict(window_policy="fixed", window=4), 0),
                                        (dict(window_policy="full", rope_head_stride=0), 2),
-                                       (dict(rope_scaling_factor=1.0, full_on_even=False), 0)])
+                                       (dict(rope_scaling_factor=1.0, full_on_even=False), 0),
+                                       # sink rows kept through eviction; windows widened by them
+                                       (dict(sink_tokens=1), 0), (dict(sink_tokens=2, window=2), 0),
+                                       (dict(sink_tokens=2, window_policy="full"), 2),
+                                       (dict(sink_tokens=5), 0)])  # cache_len - 1: nothing rolls
 def test_decoder_step_vs_f64(oracle, kw, window):
     D = dec()
     cfg = tiny_cfg(**kw)
@@ -232,7 +245,13 @@ def test_decoder_step_vs_f64(oracle, kw, window):
     orc = oracle.DecoderOracle(data, B)
     ref = _f64_model(oracle, data, B)
     rng = np.random.default_rng(0)
-    for pos in range(10):  # cache_len 6: positions 6.. evict
+    S = cfg.sink_tokens
+    if S:  # a windowed layer needs the sink rows in the cache: load them (what a prefill leaves)
+        shape = (cfg.n_layers, B, S, cfg.kv_heads, cfg.head_dim)
+        k, v = rng.standard_normal(shape).astype(np.float32), rng.standard_normal(shape).astype(np.float32)
+        orc.load(k, v)
+        ref.load(k, v)
+    for pos in range(S, S + 10):  # cache_len 6: positions 6.. evict
         tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
         nxt, lg, hid = orc.step(tok, pos, window)
         lg64, hid64 = ref(tok, pos, window)
@@ -243,6 +262,36 @@ def test_decoder_step_vs_f64(oracle, kw, window):
             if top2[b, 1] - top2[b, 0] > 1e-4 * np.abs(lg64).max():
                 assert nxt[b] == int(np.argmax(lg64[b])), (pos, b)
     assert orc.used == cfg.cache_len
+
+
+def test_sink_rows_survive_eviction(oracle):
+    """With sink_tokens S the first S cache rows are the first S positions' rows after any number of
+    evictions (src/attention/cache_ops.rs:64-117), and the other rows are the latest positions in
+    order; without sinks the cache is the latest cache_len positions."""
+    D = dec()
+    for S in (0, 2, 5):
+        cfg = tiny_cfg(sink_tokens=S, window_policy="full")
+        data = D.make_decoder(cfg, seed=4, moe_dtype="f32")
+        orc = oracle.DecoderOracle(data, 1)
+        rows = {}
+        for pos in range(15):
+            orc.step(np.array([pos % cfg.vocab_size], np.int32), pos)
+            rows[pos] = orc.k[0, 0, min(pos, cfg.cache_len - 1)].copy()  # the row a step appends
+        cap = cfg.cache_len
+        expect = list(range(S)) + list(range(15 - (cap - S), 15))
+        for r, p in enumerate(expect):
+            assert np.array_equal(orc.k[0, 0, r], rows[p]), (S, r, p)
+
+
+def test_window_with_too_few_sink_rows_is_refused(oracle):
+    """A windowed layer over fewer cache rows than sink_tokens has no window in the reference (its
+    gathered rows and the window length disagree): the oracle refuses the step."""
+    D = dec()
+    cfg = tiny_cfg(sink_tokens=3)
+    data = D.make_decoder(cfg, seed=4, moe_dtype="f32")
+    orc = oracle.DecoderOracle(data, 1)
+    with pytest.raises(AssertionError):
+        orc.step(np.array([1], np.int32), 0)
 
 
 def test_window_covering_cache_equals_full(oracle):

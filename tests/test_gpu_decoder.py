@@ -65,6 +65,9 @@ CASES = {
     "combine_norm_4parts": dict(ffn_hidden=512),
     "combine_norm_unsplit": dict(ffn_hidden=96),
     "wide_d_unfused": dict(d_model=4160, n_layers=2),
+    # an output projection of 32 K-parts (512 rows x 4096 inputs: few row tiles, so 4 K-groups per
+    # part), more than the router that forms the residual row takes: the separate residual add
+    "wo_32_parts": dict(d_model=512, n_heads=32, head_dim=128, kv_heads=8, n_layers=2),
 }
 
 
@@ -87,6 +90,44 @@ def test_decode_steps_match_oracle(D, oracle, case):
         o_nxt, o_lg, o_hid = orc.step(tok, pos, caller)
         torch.cuda.synchronize()
         _check_step(oracle, TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, (case, pos))
+        tok = o_nxt
+    dev.close()
+
+
+@pytest.mark.parametrize("kw,caller", [
+    (dict(sink_tokens=4), 0),                                       # every-other 8-row windows
+    (dict(sink_tokens=3, window_policy="fixed", window=5), 0),
+    (dict(sink_tokens=2, window_policy="full", cache_len=300, max_seq_len=700), 0),  # two key chunks
+    (dict(sink_tokens=39, window_policy="full"), 6),                # one non-sink row: nothing rolls
+])
+def test_decode_sink_tokens(D, oracle, kw, caller):
+    """GptOssConfig.sink_tokens: the cache keeps the first positions' rows through eviction and
+    windows span the last sink + min(w, rows - sink) rows (src/attention/cache_ops.rs:64-117,
+    src/attention/streaming_mqa.rs:332-339).  The sink rows are loaded first (a windowed layer needs
+    them), then teacher-forced steps past several evictions."""
+    cfg = _cfg(D, **kw)
+    data = D.make_decoder(cfg, seed=14, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B, S = 3, cfg.sink_tokens
+    print(f"[decoder] sink_tokens cfg={cfg}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    from burnext_amd import _native as N
+    if cfg.window_policy != "full" or caller:
+        with pytest.raises(N.BurnextError, match="sink_tokens"):  # no sink rows yet
+            dev.decode(torch.zeros(B, dtype=torch.int32, device="cuda"), 0, window=caller)
+    orc = oracle.DecoderOracle(data, B)
+    rng = np.random.default_rng(8)
+    shape = (cfg.n_layers, B, S, cfg.kv_heads, cfg.head_dim)
+    k = (rng.standard_normal(shape, dtype=np.float32) * 0.6).astype(np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    dev.cache_load(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    orc.load(k, v)
+    tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
+    steps = cfg.cache_len + 12 if cfg.cache_len < 100 else 2 * cfg.cache_len - 2 * S + 5
+    for pos in range(S, S + steps):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True, window=caller)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos, caller)
+        torch.cuda.synchronize()
+        _check_step(oracle, TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, (kw, pos))
         tok = o_nxt
     dev.close()
 
@@ -143,10 +184,21 @@ def test_decode_argument_errors(D):
     ws = dev.workspace(2)
     with pytest.raises(N.BurnextError, match="WORKSPACE_TOO_SMALL"):
         dev.decode(tok, 0, workspace=ws[:ws.numel() // 2])
+    # a batch row the cache holds no rows for is refused while the cache is not empty
+    dev.decode(tok[:1], 0)
+    with pytest.raises(N.BurnextError, match="batch rows the cache holds"):
+        dev.decode(tok, 1)
+    dev.reset()
     for p in range(8):
         dev.decode(tok, p)
     with pytest.raises(N.BurnextError, match="max_positions"):
         dev.decode(tok, 8)
+    dev.reset()
+    k = torch.zeros((2, 1, 3, cfg.kv_heads, cfg.head_dim), device="cuda")
+    dev.cache_load(k, k)  # 3 rows for batch row 0 only
+    with pytest.raises(N.BurnextError, match="batch rows the cache holds"):
+        dev.decode(tok, 3)
+    dev.decode(tok[:1], 3)
     torch.cuda.synchronize()
 
 
