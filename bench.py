@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder leg of the default run")
     ap.add_argument("--decoder-steps", type=int, default=50, help="timed decode steps of the decoder leg")
     ap.add_argument("--decoder-only", action="store_true", help="measure the full-decoder leg alone")
+    ap.add_argument("--fused-experts", action="store_true",
+                    help="forward with BURNEXT_FUSED_EXPERTS (the opt-in one-launch experts kernel of decode batches)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     return ap.parse_args()
@@ -117,6 +119,9 @@ def make_layers(data, copies, dev=0):
     return layers
 
 
+FORWARD_FLAGS = [3]  # BURNEXT_FORWARD_DEFAULT; | BURNEXT_FUSED_EXPERTS under --fused-experts
+
+
 def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     """Times `steps` layer forwards (after `warmup`) on resident inputs; returns the workload's
     figures: tokens/s, per-kernel execution times, the dominant kernel's roofline, routing."""
@@ -138,8 +143,10 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     counts = np.bincount(idx_np.ravel(), minlength=E)
     touched = int(np.count_nonzero(counts))
 
+    flags = FORWARD_FLAGS[0]
+
     def step(i):
-        layers[i % len(layers)].forward(x, out=y, workspace=ws)
+        layers[i % len(layers)].forward(x, out=y, workspace=ws, flags=flags)
 
     for i in range(warmup):
         step(i)
@@ -154,10 +161,12 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
 
     # per-kernel execution times over a second pass of the same steps.  A first recorded pass fills
     # each layer's pool of event pairs (read and discarded), so the measured pass creates no events
-    # between its launches.  Timed launches cost the host more than plain ones, so that pass is
-    # host-bound: its kernels start on an idle GPU.  The measured pass therefore queues its steps in
-    # chunks behind a bounded GPU sleep longer than the chunk's enqueue time, and its kernels run
-    # back to back as in the untimed pass.
+    # between its launches.  Timed launches cost the host more than plain ones; where that makes the
+    # pass host-bound (short decode steps), its kernels would start on an idle GPU, so the measured
+    # pass queues its steps in chunks behind a bounded GPU sleep longer than the chunk's enqueue
+    # time and its kernels run back to back as in the untimed pass.  (Where the host keeps ahead,
+    # the steps go out directly: queued behind a sleep, the prefill GEMMs measured 15% slower under
+    # the kernel tracer too.)
     for L in layers:
         L.profile_enable(True)
     t0 = time.perf_counter()
@@ -169,14 +178,21 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         L.profile_read()
     for L in layers:
         L.profile_enable(True)  # every pass read: its pairs return to the pool
-    rate = sleep_cycles_per_s()
-    chunk = 20
+    gated = host_s > ms_step * 1e-3
+    chunk = 20 if gated else steps
+    spans = []  # GPU time of each chunk's steps (after its sleep): the measured pass's own step
     for c0 in range(0, steps, chunk):
         n = min(chunk, steps - c0)
-        torch.cuda._sleep(int(2.0 * n * host_s * rate) + 10000)
+        if gated:
+            torch.cuda._sleep(int(2.0 * n * host_s * sleep_cycles_per_s()) + 10000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for i in range(c0, c0 + n):
             step(i)
+        e1.record()
+        spans.append((e0, e1))
     torch.cuda.synchronize()
+    prof_step_us = sum(a.elapsed_time(b) for a, b in spans) * 1e3 / steps
     kern = {}
     for L in layers:
         L.profile_enable(False)
@@ -185,12 +201,16 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
             a[0] += ms
             a[1] += cnt
     kavg_us = {k: (v[0] / v[1] * 1e3) for k, v in kern.items() if v[1]}
-    # every kernel of a step runs on one stream, one launch each: their durations cannot sum past the step
+    # every kernel of a step runs on one stream, one launch each: their exclusive intervals are
+    # disjoint, so their sum cannot pass the step of the pass they were measured in (whose event
+    # pairs cost a little over the untimed pass's step)
     ksum_us = sum(v[0] for v in kern.values()) * 1e3 / steps
     log(f"{name}: {ms_step * 1e3:.1f} us/step, kernels {', '.join(f'{k} {v:.1f}' for k, v in kavg_us.items())}, "
-        f"sum {ksum_us:.1f} (timed launches enqueue at {host_s * 1e6:.1f} us per step)")
-    if ksum_us > ms_step * 1e3:
-        log(f"{name}: WARNING kernel durations sum to {ksum_us:.1f} us, above the {ms_step * 1e3:.1f} us step")
+        f"sum {ksum_us:.1f} in a timed pass of {prof_step_us:.1f} us/step (its launches enqueue at "
+        f"{host_s * 1e6:.1f} us per step{', queued behind a GPU sleep' if gated else ''})")
+    if ksum_us > prof_step_us:
+        log(f"{name}: WARNING kernel durations sum to {ksum_us:.1f} us, above the {prof_step_us:.1f} us step "
+            f"of their pass")
 
     # algorithmic bytes / FLOPs per launch (realised routing; bf16 biases, router, activations)
     nk = T * K
@@ -201,6 +221,9 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         "down": touched * w2_bytes + nk * F * 4 + nk * D * 4,
         "router": E * D * 2 + E * 2 + T * D * 2 + T * D * 2 + T * E * 4,
         "combine": nk * D * 4 + touched * D * 2 + 2 * T * D * 2 + nk * 12,
+        # the fused decode experts: both projections' weights and biases, the token rows, one f32
+        # output row per slot (its per-slice partial rows are not algorithmic)
+        "experts": touched * (w1_bytes + w2_bytes + D * 2) + T * D * 2 + nk * D * 4,
     }
     kflops = {"gate_up": 2 * nk * 2 * F * D, "down": 2 * nk * D * F}
     layer_bytes = synth.decode_bytes(data, touched, T, 2)
@@ -241,6 +264,7 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         "layer_algorithmic_bytes": layer_bytes,
         "kernels_avg_us": {k: round(v, 2) for k, v in kavg_us.items()},
         "kernels_sum_us": round(ksum_us, 2),
+        "kernels_pass_us_per_step": round(prof_step_us, 2),
         "roofline": roof,
     }
     if prefill:
@@ -250,6 +274,8 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         out["config"]["router_bias"] = f"zipf s={ZIPF_S} gamma={synth.ZIPF_GAMMA_C3} (calibrated)"
         out["segment_histogram_by_zipf_rank"] = by_rank.tolist()
         out["segment_ideal_by_zipf_rank"] = [int(round(v)) for v in synth.zipf_ideal_counts(E, ZIPF_S, T, K)]
+    if flags & 4:
+        out["config"]["experts"] = "fused (BURNEXT_FUSED_EXPERTS)"
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline(data, x_np, cpu_seconds)
     return out
@@ -440,6 +466,8 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path (one MI355X per run); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.fused_experts:
+        FORWARD_FLAGS[0] = 3 | 4
     import torch
 
     torch.cuda.set_device(0)
@@ -479,7 +507,7 @@ def main():
                 r = measure(name, use, bdata, args.steps, args.warmup, False, 0)
                 sweep[name.split("_")[1]] = {k: r[k] for k in ("value", "unit", "ms_per_step", "layer_hbm_frac",
                                                                 "layer_fp4_mfma_util", "kernels_avg_us",
-                                                                "kernels_sum_us", "roofline", "config") if k in r}
+                                                                "kernels_sum_us", "kernels_pass_us_per_step", "roofline", "config") if k in r}
             out["sweep_120b"] = sweep
             for L in layers:
                 L.close()

@@ -13,7 +13,7 @@ PKG = pathlib.Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libburnext_moe.so"
-SOURCES = ["kernels.hip", "gemm.hip", "layer.hip", "decoder.hip"]
+SOURCES = ["kernels.hip", "gemm.hip", "fused.hip", "layer.hip", "decoder.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops off: hipcc forms packed fp32 ops from plain float code on its own; they are
 # kept out of every kernel here.  The host pass warns that it does not know the feature.

@@ -176,6 +176,40 @@ struct GemmArgs {
   float alpha, limit;
 };
 
+// The experts of a decode-sized batch in one launch (moe_fused_kernel): one workgroup per
+// (active expert, feature slice) item, at most one item per CU.  The slice count per expert is
+// set on the device from the number of active experts na: nsl = clamp(G / na, 1, min(nb2,
+// nsl_cap)) for a grid of G workgroups, slice s = the 32-feature blocks [s nb2 / nsl,
+// (s + 1) nb2 / nsl).  Phase 1 computes the slice's SwiGLU features for the expert's tokens (its
+// interleaved W1 rows over all of D, bias, clamped SwiGLU; token passes of mt_max rows) into
+// LDS; phase 2 multiplies W2's matching K range (every output row) with them and writes, per
+// slot, the partial output row of slice s (b2 with slice 0).  No workgroup waits for another
+// (split-K over F); combine_slices_kernel adds the slices in order.
+struct FusedArgs {
+  const uint8_t *w1b, *w1s, *w2b, *w2s;  // tiled MXFP4 codes and scales (as GemvArgs)
+  uint64_t w1b_es, w1s_es, w2b_es, w2s_es;
+  const float *b1, *b2;  // [E, w1 rows_p] interleaved order, [E, w2 rows_p]
+  uint32_t b1_es, b2_es;
+  uint32_t nrt1, nb1;    // W1 row tiles (2F rows), K blocks of 32 (D)
+  uint32_t kt1;          // true K of W1 (D)
+  uint32_t nrt2, nb2;    // W2 row tiles (D rows), K blocks (F)
+  uint32_t D;            // output rows
+  uint32_t nsl_cap;      // most slices per expert (the partial-row buffer's size)
+  uint32_t sb_max;       // widest slice in blocks the LDS is sized for
+  uint32_t mt_max;       // tokens per phase-1 pass
+  const int32_t *num_active, *exrec, *perm;
+  uint32_t topk;
+  const void *xn;        // B rows of phase 1: [n, 32 * nb1] x dtype (normalised tokens)
+  float *out;            // partial slot rows [nsl][n * topk][out_stride]
+  uint64_t slice_stride; // elements between slices
+  uint32_t out_stride;
+  float alpha, limit;
+};
+constexpr uint32_t kFusedKgPerStep = 6;   // K-groups per wave per step of the fused kernel
+constexpr uint32_t kFusedWaves = 16;      // waves per workgroup (one workgroup per CU)
+constexpr uint64_t kFusedPartBytes = 8ull << 20;  // budget of the partial slot rows
+constexpr uint32_t kFusedBiasRegs = 4;     // bias values per thread held in registers over the staging
+
 struct CombineArgs {
   const void *x;
   void *y;
@@ -191,6 +225,10 @@ struct CombineArgs {
   const float *ngamma;
   float *nout;
   float neps;
+  // combine_slices_kernel: the fused kernel's slice count, from num_active as that kernel sets it
+  // (nparts = clamp(slice_grid / na, 1, slice_cap))
+  const int32_t *num_active;
+  uint32_t slice_grid, slice_cap;
 };
 
 // act[r, f] = SwiGLU(sum_h part_h[r, 2f], sum_h part_h[r, 2f + 1]) (h ascending) for the
@@ -260,6 +298,23 @@ hipError_t launch_topk(const TopkArgs &a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, bool x_bf16, hipStream_t s);
+// Fused decode experts: launch geometry chosen by the host (fused_geometry in fused.hip) from the
+// batch size and the most experts it can activate (max_active); the slicing itself is set on the
+// device from the realised count.
+struct FusedGeom {
+  uint32_t grid;     // workgroups (the CUs)
+  uint32_t nsl_cap;  // most slices per expert
+  uint32_t sb_max;   // widest slice in 32-feature blocks
+  uint32_t mt;       // tokens per phase-1 pass
+  size_t lds;
+};
+bool fused_geometry(uint32_t nb1, uint32_t nb2, uint32_t nrt2, uint32_t Dp, uint32_t num_cus, uint32_t max_active,
+                    uint32_t topk, uint64_t n, int nt, FusedGeom &g);
+hipError_t launch_fused(const FusedArgs &a, const FusedGeom &g, int nt, bool x_bf16, hipStream_t s);
+// combine over the slices of the fused kernel: y = x + sum_p w_p * (sum_s part[s][t k + p]),
+// parts part_stride apart, their count as the fused kernel set it (CombineArgs.num_active)
+hipError_t launch_combine_slices(const CombineArgs &a, bool x_bf16, hipStream_t s);
+hipError_t configure_fused_kernels();
 hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s);
 hipError_t configure_gemm_kernels();

@@ -365,6 +365,24 @@ uint64_t max_split_tokens(const burnext_moe_layer &L, uint64_t n) {
   return ms;
 }
 
+// The experts of a decode-sized batch in one launch (moe_fused_kernel, opt-in by
+// BURNEXT_FUSED_EXPERTS): batches of at most kSmallRouteMaxTokens tokens with top-k <= 8 whose
+// geometry fits, except where the decoder fuses the next RmsNorm into the combine (post_norm).
+// Sets g when it applies.
+bool use_fused(const burnext_moe_layer &L, uint64_t n, int nt, bool post_norm, FusedGeom &g) {
+  if (post_norm || n == 0 || n > kSmallRouteMaxTokens || L.K > 8u) return false;
+  return fused_geometry(L.w1.nb, L.w2.nb, L.w2.nrt, L.Dp, (uint32_t)L.num_cus,
+                        (uint32_t)std::min<uint64_t>(L.E, n * L.K), L.K, n, nt, g);
+}
+
+// Partial slot rows the fused kernel may write for a batch of m tokens (its most slices x m k),
+// 0 when it does not apply (the slice cap does not depend on the activation terms).
+uint64_t fused_rows(const burnext_moe_layer &L, uint64_t m) {
+  FusedGeom g{};
+  if (!use_fused(L, m, 1, false, g) && !use_fused(L, m, 2, false, g)) return 0;
+  return (uint64_t)g.nsl_cap * m * L.K;
+}
+
 // Workspace regions for n tokens.  Every region is sized for the largest need of any batch of
 // m <= n tokens, so burnext_moe_workspace_size(n) is non-decreasing in n and one workspace sized
 // for the largest batch serves every smaller one: the K-part buffers of decode-sized batches
@@ -404,8 +422,11 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
     w.aq[3] = take(nk * qscale_bytes(L.w2));
   }
   // decode-sized batches split the down projection's K range in parts (kDownSplitFew when gate_up
-  // is split too, else kDownSplit): a partial-sum buffer each, sized for the largest m <= n
-  const uint64_t yrows = std::max({nk, ns * L.K * kDownSplit, ms * L.K * kDownSplitFew});
+  // is split too, else kDownSplit), or (the fused kernel) in feature slices: a partial-sum buffer
+  // each, sized for the largest m <= n
+  uint64_t frows = 0;
+  for (uint64_t m = 1; m <= ns; ++m) frows = std::max(frows, fused_rows(L, m));
+  const uint64_t yrows = std::max({nk, ns * L.K * kDownSplit, ms * L.K * kDownSplitFew, frows});
   w.ypart = take(yrows * L.Dp * 4);
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
   if (ms) w.upart = take((uint64_t)kGateUpSplit * ms * L.K * L.w1.rows_p * 4);
@@ -514,7 +535,9 @@ struct ProfScope final : LaunchTimer {
   }
 };
 
-enum KernelId { kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5, kKSwiglu = 6 };
+enum KernelId {
+  kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5, kKSwiglu = 6, kKExperts = 7
+};
 
 burnext_status check_launch(hipError_t e, const char *what) {
   if (e != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
@@ -690,7 +713,7 @@ struct PostNorm {
 
 burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, uint64_t n, uint32_t flags,
                        const WsPtrs &p, hipStream_t s, uint32_t nparts = 1, bool part_bf16 = false,
-                       const PostNorm *pn = nullptr) {
+                       const PostNorm *pn = nullptr, const FusedGeom *slices = nullptr) {
   CombineArgs c{};
   c.x = x;
   c.y = y;
@@ -709,12 +732,57 @@ burnext_status combine(burnext_moe_layer *L, const void *x, void *y, bool xb, ui
     c.nout = pn->out;
     c.neps = pn->eps;
   }
+  if (slices) {  // the fused kernel's slices: their count follows num_active on the device
+    c.num_active = p.num_active;
+    c.slice_grid = slices->grid;
+    c.slice_cap = std::min(L->w2.nb, slices->nsl_cap);
+  }
   burnext_status st;
   {
     ProfScope ps(L, s, kKCombine);
-    st = check_launch(launch_combine(c, xb, s), "combine launch");
+    st = slices ? check_launch(launch_combine_slices(c, xb, s), "combine launch")  // the fused kernel's slices
+                : check_launch(launch_combine(c, xb, s), "combine launch");
   }
   return st == BURNEXT_OK ? ok() : st;
+}
+
+// The fused decode experts (use_fused): one launch over (active expert, slice) items.
+burnext_status run_fused(burnext_moe_layer *L, uint64_t n, int nt, bool xb, const FusedGeom &fg, const WsPtrs &p,
+                         hipStream_t s) {
+  FusedArgs a{};
+  a.w1b = L->w1.blocks;
+  a.w1s = L->w1.scales;
+  a.w2b = L->w2.blocks;
+  a.w2s = L->w2.scales;
+  a.w1b_es = L->w1.blocks_per_expert;
+  a.w1s_es = L->w1.scales_per_expert;
+  a.w2b_es = L->w2.blocks_per_expert;
+  a.w2s_es = L->w2.scales_per_expert;
+  a.b1 = L->b1;
+  a.b2 = L->b2;
+  a.b1_es = L->w1.rows_p;
+  a.b2_es = L->w2.rows_p;
+  a.nrt1 = L->w1.nrt;
+  a.nb1 = L->w1.nb;
+  a.kt1 = L->w1.cols;
+  a.nrt2 = L->w2.nrt;
+  a.nb2 = L->w2.nb;
+  a.D = L->D;
+  a.nsl_cap = fg.nsl_cap;
+  a.sb_max = fg.sb_max;
+  a.mt_max = fg.mt;
+  a.num_active = p.num_active;
+  a.exrec = p.exrec;
+  a.perm = p.perm;
+  a.topk = L->K;
+  a.xn = p.xn;
+  a.out = p.ypart;
+  a.out_stride = L->Dp;
+  a.slice_stride = n * L->K * L->Dp;
+  a.alpha = L->alpha;
+  a.limit = L->limit;
+  ProfScope ps(L, s, kKExperts);
+  return check_launch(launch_fused(a, fg, nt, xb, s), "fused experts launch");
 }
 
 // Grouped-GEMM path (use_gemm_path): router (+ the two-term rows of xn), top-k,
@@ -827,7 +895,8 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   if (pa && (x != pa->xout || x_dtype != BURNEXT_F32 || !moe_front_fusable(L, n, pa->nparts)))
     return fail(BURNEXT_INVALID_ARG, "formed input rows need f32 rows, x == xout and a decode-sized batch");
   if (x_dtype != BURNEXT_F32 && x_dtype != BURNEXT_BF16) return fail(BURNEXT_INVALID_ARG, "bad x_dtype");
-  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)) return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
+  if (flags & ~(BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL | BURNEXT_FUSED_EXPERTS))
+    return fail(BURNEXT_INVALID_ARG, "unknown flag bits");
   if (n > kMaxTokens) return fail(BURNEXT_UNSUPPORTED, "n_tokens above 4194304 is not supported");
   if (n == 0) return ok();
   if (!x || !y) return fail(BURNEXT_INVALID_ARG, "x or y is null");
@@ -872,6 +941,13 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
       st = run_dispatch(L, n, p.topk_idx, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec, p.dcnt, s);
   }
   if (st != BURNEXT_OK) return st;
+
+  FusedGeom fg{};
+  if ((flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg)) {
+    st = run_fused(L, n, nt, xb, fg, p, s);
+    if (st != BURNEXT_OK) return st;
+    return combine(L, x, y, xb, n, flags, p, s, 1, false, nullptr, &fg);
+  }
 
   auto gemv = [&](bool gate_up) -> burnext_status {
     const GemvCfg &cf = gate_up ? cfg_up : cfg_dn;
@@ -1039,6 +1115,7 @@ burnext_status burnext_moe_layer_create(const burnext_moe_config *cfg, const bur
     std::call_once(once, [] {
       cfg_err = configure_kernels();
       if (cfg_err == hipSuccess) cfg_err = configure_gemm_kernels();
+      if (cfg_err == hipSuccess) cfg_err = configure_fused_kernels();
     });
     if (cfg_err != hipSuccess) return fail(BURNEXT_DEVICE_ERROR, std::string("kernel configuration failed: ") + hipGetErrorString(cfg_err));
   }

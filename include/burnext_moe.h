@@ -89,6 +89,12 @@ typedef struct burnext_moe_layer *burnext_moe_layer_t;
 #define BURNEXT_APPLY_RMSNORM 1u /* route on RmsNorm(x) (src/moe/mod.rs:109) */
 #define BURNEXT_ADD_RESIDUAL 2u  /* y = x + MoE(...) (src/moe/mod.rs:411)   */
 #define BURNEXT_FORWARD_DEFAULT (BURNEXT_APPLY_RMSNORM | BURNEXT_ADD_RESIDUAL)
+/* Forward only, opt-in, no counterpart in the reference: batches of at most 16 tokens with
+ * top-k <= 8 run gate_up, SwiGLU and down in one launch split over feature slices (each
+ * workgroup one slice of one active expert), then a combine that sums the slices in order.  Same
+ * results to the forward's tolerance; on MI355X it measured slower than the default two expert
+ * GEMVs at every decode shape tried, so the default path does not take it. */
+#define BURNEXT_FUSED_EXPERTS 4u
 
 /* Uploads one layer to `device` and repacks W1/W2 into the kernels' tiled layout.
  * Host inputs: w1 [E, 2F, ...] per w1_desc, w2 [E, D, ...] per w2_desc, b1 [E, 2F] (same row
@@ -165,9 +171,11 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
  * pairs are pooled per process: an enable call made when every layer's records have been read
  * returns them to the pool, so a later recorded pass creates no events between its launches.
  * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine, 6 SwiGLU of the gate_up
- * K-parts (batches of at most 16 tokens run top-k and dispatch as one kernel, recorded under id 1;
- * id 2 then records nothing; id 6 records only decode batches that touch few experts). */
-#define BURNEXT_NUM_KERNELS 7
+ * K-parts, 7 the fused experts (batches of at most 16 tokens run top-k and dispatch as one kernel,
+ * recorded under id 1; id 2 then records nothing; such batches run gate_up, SwiGLU and down as one
+ * kernel, id 7, except inside the decoder step, whose MoE combine also writes the next norm: there
+ * ids 3, 4 and, for batches that touch few experts, 6 record them). */
+#define BURNEXT_NUM_KERNELS 8
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t layer, int enable);
 burnext_status burnext_moe_profile_read(burnext_moe_layer_t layer, double *ms_total, uint64_t *launches,
                                         int n_kernels);

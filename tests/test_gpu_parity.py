@@ -527,6 +527,35 @@ def test_forward_gate_up_k_split(M, oracle, D, F, E, K, n, dtype):
     assert err <= (TOL_F32 if dtype == "f32" else TOL_BF16)
 
 
+@pytest.mark.parametrize("D,F,E,K,n,dtype", [
+    (2880, 2880, 32, 4, 1, "bf16"),   # narrow slices, W1 K split between two waves
+    (2880, 2880, 32, 4, 3, "bf16"),   # 12 active-expert slots: still narrow
+    (2880, 2880, 32, 4, 4, "bf16"),   # 16 slots: wide slices
+    (2880, 2880, 32, 4, 16, "bf16"),  # largest decode batch; segments above 8 tokens take a second pass
+    (2880, 2880, 32, 4, 8, "f32"),    # two activation terms, 4 tokens per pass
+    (512, 384, 4, 2, 16, "bf16"),     # 4 experts for 16 tokens: two passes of 8
+    (512, 384, 4, 2, 13, "f32"),      # up to four passes of 4
+    (256, 100, 8, 3, 6, "bf16"),      # F = 100: a partial block, one slice of 4 blocks
+    (320, 1000, 16, 8, 5, "f32"),     # top-8 (combine lanes in groups of 8), F = 1000 (tail slice)
+    (256, 256, 16, 10, 4, "bf16"),    # top-10: beyond the fused path (the expert GEMVs)
+])
+def test_forward_fused_decode(M, oracle, D, F, E, K, n, dtype):
+    """Decode-sized batches with BURNEXT_FUSED_EXPERTS: the fused experts kernel (one launch for
+    gate_up, SwiGLU and down, split over feature slices) and the combine over the slices, against
+    the oracle."""
+    from burnext_amd import _native as N, synth
+    print(f"fused decode case D={D} F={F} E={E} K={K} n={n} {dtype}", flush=True)
+    L = _make(synth, D, F, E, K, seed=17, dtype=dtype, with_gamma=True)
+    x = synth.make_tokens(n, D, seed=18, dtype=dtype)
+    y, y_ref = _forward_case(M, oracle, L, x, dtype, flags=N.FORWARD_DEFAULT | N.FUSED_EXPERTS)
+    err = oracle.max_abs_rel(y, y_ref)
+    moe_err = oracle.max_abs_rel(y - x, y_ref - x)
+    print(f"  max-abs-rel {err:.3e} (moe part {moe_err:.3e})")
+    assert np.isfinite(y).all()
+    tol = TOL_F32 if dtype == "f32" else TOL_BF16
+    assert err <= tol and moe_err <= (tol if dtype == "bf16" else 10 * tol)
+
+
 def test_forward_deterministic(M):
     from burnext_amd import synth
     L = _make(synth, 2880, 2880, 32, 4, seed=2, dtype="bf16")
