@@ -348,35 +348,44 @@ def measure_decoder(steps, warmup, with_cpu, kv_bf16_leg=True):
                               f"uniform routing; cache rows attended per step summed over layers: {rows}"}
     log(f"decoder: {ms:.3f} ms/step, {out['value']} tokens/s, step {out['step_hbm_gbs']} GB/s")
     if kv_bf16_leg:
-        # the same decoder with bf16 cache rows (half the attention bytes; parity bar 2e-2 instead of
-        # the f32 cache's 5e-4): a second model object on the same MoE layers
-        cfg16 = dataclasses.replace(cfg, kv_bf16=True)
-        data16 = dataclasses.replace(data, cfg=cfg16)
-        dev.close()
-        dev = DEC.GptOssDecoder(data16, max_batch=B, moe_layers=dev.moe_layers)
-        k = torch.randn(shape, generator=g, device="cuda:0") * 0.6
-        v = torch.randn(shape, generator=g, device="cuda:0")
-        dev.cache_load(k, v)
-        torch.cuda.synchronize()
-        del k, v
-        ws = dev.workspace(B)
-        pos = pre
-        for _ in range(warmup):
-            tok = dev.decode(tok, pos, workspace=ws)
-            pos += 1
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(steps):
-            tok = dev.decode(tok, pos, workspace=ws)
-            pos += 1
-        end.record()
-        torch.cuda.synchronize()
-        ms16 = start.elapsed_time(end) / steps
-        step16 = step_b - (rows * B * kd * 4 * 2 + L * B * kd * 4 * 2) / 2
-        out["kv_bf16"] = {"value": round(B / (ms16 * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms16, 4),
-                          "step_hbm_frac": round(step16 / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                          "note": "same decoder with bf16 cache rows (the reference keeps f32)"}
-        log(f"decoder (bf16 cache): {ms16:.3f} ms/step, {out['kv_bf16']['value']} tokens/s")
+        # options beyond the reference, on second model objects over the same MoE layers: bf16 cache
+        # rows (half the attention bytes), the expert projections on bf16-rounded rows (one MFMA
+        # term), and both; parity bar 2e-2 for each instead of the f32 decoder's 5e-4
+        kv_b_all = rows * B * kd * 4 * 2 + L * B * kd * 4 * 2
+
+        def leg(key, note, **changes):
+            nonlocal dev, tok
+            cfgx = dataclasses.replace(cfg, **changes)
+            datax = dataclasses.replace(data, cfg=cfgx)
+            moe_layers = dev.moe_layers
+            dev.close()
+            dev = DEC.GptOssDecoder(datax, max_batch=B, moe_layers=moe_layers)
+            k = torch.randn(shape, generator=g, device="cuda:0") * 0.6
+            v = torch.randn(shape, generator=g, device="cuda:0")
+            dev.cache_load(k, v)
+            torch.cuda.synchronize()
+            del k, v
+            wsx = dev.workspace(B)
+            p = pre
+            for _ in range(warmup):
+                tok = dev.decode(tok, p, workspace=wsx)
+                p += 1
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(steps):
+                tok = dev.decode(tok, p, workspace=wsx)
+                p += 1
+            end.record()
+            torch.cuda.synchronize()
+            msx = start.elapsed_time(end) / steps
+            stepx = step_b - (kv_b_all / 2 if changes.get("kv_bf16") else 0)
+            out[key] = {"value": round(B / (msx * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(msx, 4),
+                        "step_hbm_frac": round(stepx / (msx * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "note": note}
+            log(f"decoder ({note}): {msx:.3f} ms/step, {out[key]['value']} tokens/s")
+
+        leg("kv_bf16", "bf16 cache rows (the reference keeps f32)", kv_bf16=True)
+        leg("experts_bf16", "expert projections on bf16-rounded rows (the reference's are f32)", experts_bf16=True)
+        leg("kv_bf16_experts_bf16", "bf16 cache rows and bf16 expert rows", kv_bf16=True, experts_bf16=True)
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_decoder(data, B, pre)
     dev.close()

@@ -65,7 +65,7 @@ class GptOssConfigC(ctypes.Structure):
                                                "rope_head_stride", "max_positions", "kv_bf16")] + \
                [(n, ctypes.c_float) for n in ("rms_eps", "rope_theta", "rope_scaling_factor", "rope_initial_context",
                                               "rope_ntk_alpha", "rope_ntk_beta", "scale_dk")] + \
-               [("sink_tokens", ctypes.c_uint32)]
+               [("sink_tokens", ctypes.c_uint32), ("experts_bf16", ctypes.c_uint32)]
 
 
 class GptOssWeightsC(ctypes.Structure):

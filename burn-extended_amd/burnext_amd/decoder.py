@@ -37,8 +37,9 @@ class GptOssConfig:
     reference: ``rope_theta`` (the reference
     takes Burn's default base 10000; GPT-OSS uses 150000), ``rope_head_stride`` (1 = the
     reference's head-indexed RoPE positions, 0 = one position per token), ``scale_dk`` (scores
-    divided by sqrt(scale_dk); 1 = pre-scaled q/k as the reference's GPT-OSS layers) and
-    ``kv_bf16`` (bf16 cache rows instead of the reference's f32)."""
+    divided by sqrt(scale_dk); 1 = pre-scaled q/k as the reference's GPT-OSS layers),
+    ``kv_bf16`` (bf16 cache rows instead of the reference's f32) and ``experts_bf16`` (the expert
+    projections on the normalised rows rounded to bf16 instead of f32)."""
     vocab_size: int = 201088
     d_model: int = 2880
     n_layers: int = 24
@@ -67,6 +68,7 @@ class GptOssConfig:
     rms_eps: float = 1e-5
     kv_bf16: bool = False
     sink_tokens: int = 0  # rows of the first positions the cache keeps through eviction (< cache_len)
+    experts_bf16: bool = False  # expert projections on bf16-rounded rows (one MFMA term; not in the reference)
 
     @property
     def window_policy_code(self) -> int:
@@ -88,7 +90,7 @@ class GptOssConfig:
                                int(self.rope_head_stride), self.max_seq_len, int(self.kv_bf16), self.rms_eps,
                                self.rope_theta, self.rope_scaling_factor if yarn else 1.0,
                                self.rope_initial_context, self.rope_ntk_alpha, self.rope_ntk_beta, self.scale_dk,
-                               self.sink_tokens)
+                               self.sink_tokens, int(self.experts_bf16))
 
 
 GPT_OSS_20B = GptOssConfig()

@@ -42,7 +42,8 @@ void moe_layer_shape(const burnext_moe_layer *L, uint32_t *d_model, int *device)
 burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                                      uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
                                      const float *gamma, float eps, float *xn, bool *norm_done, const float *part,
-                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid);
+                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid,
+                                     bool experts_bf16);
 bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n, uint32_t nparts);
 }  // namespace burnext
 
@@ -1055,8 +1056,8 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
     return set_error(BURNEXT_UNSUPPORTED, "head_dim must be a multiple of 8 and at most 128");
   if (c.max_batch > kMaxBatch) return set_error(BURNEXT_UNSUPPORTED, "max_batch above 16 is not supported");
   if (c.d_model % 4) return set_error(BURNEXT_UNSUPPORTED, "d_model must be a multiple of 4");
-  if (c.rope_head_stride > 1 || c.kv_bf16 > 1 || c.full_on_even > 1)
-    return set_error(BURNEXT_INVALID_ARG, "rope_head_stride, kv_bf16 and full_on_even must be 0 or 1");
+  if (c.rope_head_stride > 1 || c.kv_bf16 > 1 || c.full_on_even > 1 || c.experts_bf16 > 1)
+    return set_error(BURNEXT_INVALID_ARG, "rope_head_stride, kv_bf16, full_on_even and experts_bf16 must be 0 or 1");
   if (c.window_policy > 2) return set_error(BURNEXT_INVALID_ARG, "window_policy must be 0 (Full), 1 (Fixed) or 2 (EveryOther)");
   if (c.window_policy != 0 && c.window == 0) return set_error(BURNEXT_INVALID_ARG, "window must be positive");
   if (c.sink_tokens >= c.cache_len) return set_error(BURNEXT_INVALID_ARG, "sink_tokens must be below cache_len");
@@ -1370,7 +1371,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
       // its router also forms the residual hid2 = hid + (sum of the output projection's parts + bo)
       st = moe_forward_post_norm(M->moe[l], hid2, BURNEXT_F32, hid, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
                                  stream, next_gamma, c.rms_eps, xn, &normed, part, (uint64_t)B * D, M->wo[l].parts,
-                                 bo, hid);
+                                 bo, hid, c.experts_bf16 != 0);
       if (st != BURNEXT_OK) return st;
     } else {
       OPostArgs oa{part, (uint64_t)B * D, M->wo[l].parts, D, bo, hid};
@@ -1378,7 +1379,8 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
                      "o post launch");
       if (st != BURNEXT_OK) return st;
       st = moe_forward_post_norm(M->moe[l], hid, BURNEXT_F32, hid2, B, BURNEXT_FORWARD_DEFAULT, moe_ws, w.moe_bytes,
-                                 stream, next_gamma, c.rms_eps, xn, &normed, nullptr, 0, 0, nullptr, nullptr);
+                                 stream, next_gamma, c.rms_eps, xn, &normed, nullptr, 0, 0, nullptr, nullptr,
+                                 c.experts_bf16 != 0);
       if (st != BURNEXT_OK) return st;
       std::swap(hid, hid2);
     }

@@ -251,7 +251,10 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
         }
         v[j] = u;
       }
-      store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
+      if (a.xn_bf16)
+        store8((uint16_t *)a.xn + (size_t)(t0 + tt) * a.Dp + c0, v);
+      else
+        store8(xn + (size_t)(t0 + tt) * a.Dp + c0, v);
     }
   }
   if (a.xq.hi) {
@@ -477,7 +480,12 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
         for (int j = 0; j < 8; ++j) u[j] = a.apply_norm ? (xv[t][i][j] * ir) * g[j] : xv[t][i][j];
         const size_t row = t0 + (uint32_t)t;
         const bool tv = (uint32_t)t < nt;
-        if (a.xn && tv && c0 < a.Dp) store8((XT *)a.xn + row * a.Dp + c0, u);
+        if (a.xn && tv && c0 < a.Dp) {
+          if (a.xn_bf16)
+            store8((uint16_t *)a.xn + row * a.Dp + c0, u);
+          else
+            store8((XT *)a.xn + row * a.Dp + c0, u);
+        }
         if (a.xq.hi && 512u * i < a.xq.kq) {  // wave-uniform
           float amax = 0.0f;
 #pragma unroll
@@ -1091,7 +1099,7 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
 // c = 512 i + 8 l + j, fmaf over i then j, xor butterfly) -- no LDS, no barrier.
 // logit = dot / r + b with r = sqrt(sum(x^2) / D + eps) (r = 1 without RmsNorm).  Workgroup 0
 // writes r; the normalised rows xn_t = x_t * (1/r_t) * gamma (x_t without RmsNorm) in the x
-// dtype, zero padded to Dp, for the expert GEMV are written chunk by chunk, chunk i (columns
+// dtype (bf16 with xn_bf16), zero padded to Dp, for the expert GEMV are written chunk by chunk, chunk i (columns
 // 512 i ..) by workgroup i mod E, so no workgroup carries all of them.  Results equal
 // router_kernel bit for bit.
 // ---------------------------------------------------------------------------------------------
@@ -1149,8 +1157,12 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
   }
   if (!a.xn) return;
   const float ir0 = 1.0f / r0, ir1 = 1.0f / r1;
-  XT *xn0 = (XT *)a.xn + (size_t)t0 * a.Dp;
-  XT *xn1 = (XT *)a.xn + (size_t)t1 * a.Dp;
+  auto put = [&](uint32_t t, uint32_t c0, const float (&v)[8]) {
+    if (a.xn_bf16)
+      store8((uint16_t *)a.xn + (size_t)t * a.Dp + c0, v);
+    else
+      store8((XT *)a.xn + (size_t)t * a.Dp + c0, v);
+  };
 #pragma unroll
   for (int i = 0; i < RC; ++i) {
     const uint32_t c0 = 512u * i + 8u * lane;
@@ -1171,14 +1183,14 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) x0[j] = x1[j] = 0.0f;
     }
-    store8(xn0 + c0, x0);
-    if (has1) store8(xn1 + c0, x1);
+    put(t0, c0, x0);
+    if (has1) put(t1, c0, x1);
   }
   // rows beyond RC chunks of padding (Dp > 512 * RC cannot happen: Dp <= D + 31 <= 512 * RC + 31)
   for (uint32_t c0 = 512u * RC + 8u * lane; xn_wg && c0 < a.Dp; c0 += 512u) {
     const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    store8(xn0 + c0, z);
-    if (has1) store8(xn1 + c0, z);
+    put(t0, c0, z);
+    if (has1) put(t1, c0, z);
   }
 }
 
@@ -1192,7 +1204,8 @@ __global__ __launch_bounds__(512) void router_small_kernel(FrontArgs a) {
 //   2. wave w forms the logit of expert 8 g + w exactly as router_small_kernel does for (e, t):
 //      lane l owns chunks 512 i + 8 l + j, fmaf over i then j for the dot and the sum of squares,
 //      xor butterfly, logit = dot / r + b with r = sqrt(sum / D + eps);
-//   3. xn_t = x (1/r) gamma (zero padded to Dp) chunk by chunk, chunk c by workgroup c mod G.
+//   3. xn_t = x (1/r) gamma (zero padded to Dp; f32, or bf16 with xn_bf16) chunk by chunk, chunk
+//      c by workgroup c mod G.
 // Logits, r and xn take router_small_kernel's arithmetic on x = xout.  f32 rows, n <= 16,
 // D % 8 == 0, D <= 512 * kFrontChunks, nparts <= kFrontMaxParts, 16-byte aligned rows.
 // ---------------------------------------------------------------------------------------------
@@ -1284,7 +1297,10 @@ __global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) u[j] = 0.0f;
     }
-    store8((float *)f.xn + (size_t)t * f.Dp + 8u * c, u);
+    if (f.xn_bf16)
+      store8((uint16_t *)f.xn + (size_t)t * f.Dp + 8u * c, u);
+    else
+      store8((float *)f.xn + (size_t)t * f.Dp + 8u * c, u);
   }
 }
 

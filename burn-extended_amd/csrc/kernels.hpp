@@ -47,12 +47,14 @@ struct RouterArgs {
   const float *rb;    // router bias [E]
   float *logits;      // [n, E]
   float *rms;         // [n] (written when apply_norm), nullable
-  void *xn;           // [n, Dp] normalised rows in the x dtype (expert group 0 writes), nullable
+  void *xn;           // [n, Dp] normalised rows in the x dtype (bf16 with xn_bf16; expert group 0
+                      // writes), nullable
   QRows xq;           // the same rows in the GEMM's two-term form (expert group 0 writes when xq.hi)
   const float *gamma; // [D]
   uint32_t n, D, Dpad, Dp, E, tb, epw;
   float eps;
   int apply_norm;
+  int xn_bf16;        // xn rows rounded to bf16 (nearest even) whatever the x dtype
 };
 
 // Top-k + softmax per token (one wave per token) from logits [n, E].
@@ -128,12 +130,13 @@ struct FrontArgs {
   const void *rw;      // router weight [E, D], gamma-folded when apply_norm
   const float *rb;     // [E]
   const float *gamma;  // [D]
-  void *xn;            // [n, Dp] x dtype, or null
+  void *xn;            // [n, Dp] x dtype (bf16 with xn_bf16), or null
   float *logits;       // [n, E]
   float *rms;          // [n] or null
   uint32_t n, D, Dp, E;
   float eps;
   int apply_norm;
+  int xn_bf16;         // xn rows rounded to bf16 (nearest even) whatever the x dtype
 };
 constexpr int kFrontChunks = 6;  // router_small_kernel: D <= 512 * kFrontChunks
 

@@ -547,9 +547,10 @@ burnext_status check_launch(hipError_t e, const char *what) {
 // Router logits (and r per token when normalising) into the workspace: router_rows_kernel for
 // batches of kRouterRowsMinTokens tokens or more whose rows fit its registers, router_kernel else.
 burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
-                          float *logits, void *xn, hipStream_t s, const QRows *xq = nullptr) {
+                          float *logits, void *xn, hipStream_t s, const QRows *xq = nullptr, bool xn_bf16 = false) {
   RouterArgs ra{};
   ra.xn = xn;
+  ra.xn_bf16 = xn_bf16 ? 1 : 0;
   if (xq) ra.xq = *xq;
   ra.gamma = L->gamma;
   ra.Dp = L->Dp;
@@ -639,8 +640,9 @@ bool router_small_ok(const burnext_moe_layer &L, uint64_t n, const void *x, bool
 }
 
 burnext_status run_router_small(burnext_moe_layer *L, const void *x, bool x_bf16, uint64_t n, bool norm, float *rms,
-                                float *logits, void *xn, hipStream_t s) {
+                                float *logits, void *xn, bool xn_bf16, hipStream_t s) {
   FrontArgs a{};
+  a.xn_bf16 = xn_bf16 ? 1 : 0;
   a.x = x;
   a.rw = norm ? L->router_wg : L->router_w;
   const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
@@ -676,9 +678,10 @@ bool front_ok(const burnext_moe_layer &L, uint64_t n) {
 }
 
 burnext_status run_router_front(burnext_moe_layer *L, const PreAdd &pa, uint64_t n, bool norm, float *rms,
-                                float *logits, void *xn, hipStream_t s) {
+                                float *logits, void *xn, bool xn_bf16, hipStream_t s) {
   PreFrontArgs a{};
   FrontArgs &f = a.f;
+  f.xn_bf16 = xn_bf16 ? 1 : 0;
   f.x = pa.xout;
   f.rw = norm ? L->router_wg : L->router_w;
   const bool w_bf16 = norm ? L->router_wg_bf16 : L->router_bf16;
@@ -889,7 +892,7 @@ bool moe_front_fusable(const burnext_moe_layer *L, uint64_t n, uint32_t nparts);
 // it did (otherwise the caller normalises y itself).
 burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                             uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream, const PostNorm *pn,
-                            bool *norm_done, const PreAdd *pa = nullptr) {
+                            bool *norm_done, const PreAdd *pa = nullptr, bool experts_bf16 = false) {
   if (norm_done) *norm_done = false;
   if (!L) return fail(BURNEXT_INVALID_ARG, "layer is null");
   if (pa && (x != pa->xout || x_dtype != BURNEXT_F32 || !moe_front_fusable(L, n, pa->nparts)))
@@ -920,8 +923,12 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
     if (st != BURNEXT_OK) return st;
     return combine(L, x, y, xb, n, flags, p, s, 1, true);  // bf16 slot rows from the down GEMM
   }
-  // f32 activations: two bf16 terms (hi + bf16 of the residual, ~2^-17 relative per value)
-  const int nt = xb ? 1 : 2;
+  // f32 activations: two bf16 terms (hi + bf16 of the residual, ~2^-17 relative per value); with
+  // experts_bf16 the router writes the normalised rows rounded to bf16 once and every expert
+  // projection takes one term (the down projection rounds the SwiGLU rows as it stages them)
+  const bool small_router = !pa && router_small_ok(*L, n, x, norm);
+  const bool xnb = xb || experts_bf16;
+  const int nt = xnb ? 1 : 2;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
@@ -930,9 +937,9 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
   const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
                         : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
-  st = pa                               ? run_router_front(L, *pa, n, norm, p.rms, p.logits, p.xn, s)
-       : router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, s)
-                                         : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s);
+  st = pa             ? run_router_front(L, *pa, n, norm, p.rms, p.logits, p.xn, xnb, s)
+       : small_router ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, xnb && !xb, s)
+                      : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s, nullptr, xnb && !xb);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
     st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
   } else if (st == BURNEXT_OK) {
@@ -944,7 +951,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
 
   FusedGeom fg{};
   if ((flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg)) {
-    st = run_fused(L, n, nt, xb, fg, p, s);
+    st = run_fused(L, n, nt, xnb, fg, p, s);
     if (st != BURNEXT_OK) return st;
     return combine(L, x, y, xb, n, flags, p, s, 1, false, nullptr, &fg);
   }
@@ -990,7 +997,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
       g.out_half = n * L->K * L->w1.rows_p;
     }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
-    return check_launch(launch_gemv(g, nt, gate_up, xb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
+    return check_launch(launch_gemv(g, nt, gate_up, xnb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
@@ -1027,11 +1034,12 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
 burnext_status moe_forward_post_norm(burnext_moe_layer *L, const void *x, burnext_dtype x_dtype, void *y, uint64_t n,
                                      uint32_t flags, void *workspace, uint64_t ws_bytes, void *stream,
                                      const float *gamma, float eps, float *xn, bool *norm_done, const float *part,
-                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid) {
+                                     uint64_t part_stride, uint32_t nparts, const float *bias, const float *resid,
+                                     bool experts_bf16) {
   const PostNorm pn{gamma, eps, xn};
   const PreAdd pa{part, part_stride, nparts, bias, resid, (float *)x};
   return forward_impl(L, x, x_dtype, y, n, flags, workspace, ws_bytes, stream, gamma && xn ? &pn : nullptr,
-                      norm_done, part ? &pa : nullptr);
+                      norm_done, part ? &pa : nullptr, experts_bf16);
 }
 
 // nparts: the K-part partial sums of the output projection the router adds (router_front_kernel
@@ -1240,7 +1248,7 @@ burnext_status burnext_moe_route(burnext_moe_layer_t L, const void *x, burnext_d
   float *lg = logits ? logits : p.logits;
   const bool xb = x_dtype == BURNEXT_BF16, norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
   // the forward's routing kernels for this batch size
-  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, lg, nullptr, s)
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, lg, nullptr, false, s)
                                   : run_router(L, x, xb, n, norm, p.rms, lg, nullptr, s);
   if (st == BURNEXT_OK)
     st = n <= kSmallRouteMaxTokens ? run_small_route(L, n, p, lg, topk_idx, topk_w, s)
@@ -1287,7 +1295,7 @@ burnext_status burnext_moe_route_dispatch(burnext_moe_layer_t L, const void *x, 
   p.seg_off = seg_offsets;
   p.perm = perm;
   const bool xb = x_dtype == BURNEXT_BF16, norm = (flags & BURNEXT_APPLY_RMSNORM) != 0;
-  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, nullptr, s)
+  st = router_small_ok(*L, n, x, norm) ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, nullptr, false, s)
                                   : run_router(L, x, xb, n, norm, p.rms, p.logits, nullptr, s);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
     st = run_small_route(L, n, p, p.logits, topk_idx, topk_w, s);

@@ -55,6 +55,10 @@ typedef struct burnext_gptoss_config {
                               sink_tokens + min(w, rows - sink_tokens) cache rows
                               (src/attention/streaming_mqa.rs:332-339); a windowed layer needs at least
                               sink_tokens cache rows (BURNEXT_INVALID_ARG before any launch otherwise) */
+  uint32_t experts_bf16;   /* 0: the MoE layers' expert projections take the normalised f32 rows (the
+                              reference's element, two bf16 MFMA terms); 1: those rows rounded to bf16
+                              once (one term; routing, residuals and norms stay f32).  No counterpart
+                              in the reference; results within 2e-2 of it */
 } burnext_gptoss_config;
 
 /* Dense weights (host, bf16 bit patterns, row-major [out, in] as Burn Linear's transposed weight;

@@ -16,7 +16,9 @@
 typedef struct {
   int64_t d, f, e, k;
   float alpha, limit, eps;
+  int64_t bf16_rows;
 } oracle_cfg;
+float oracle_round_bf16(float v);
 
 float oracle_fp4_value(int nib);
 float oracle_e8m0_scale(int s);
@@ -52,6 +54,7 @@ typedef struct {
   int64_t window_policy, window, full_on_even, rope_head_stride;
   float rms_eps, scale_dk;
   int64_t sink_tokens;
+  int64_t experts_bf16;
 } oracle_dec_cfg;
 typedef struct {
   const float *tok_emb, *norm_attn, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo, *sinks, *norm_final, *lm_head,
@@ -110,6 +113,7 @@ static layer_t make_layer(int64_t D, int64_t F, int64_t E, int64_t K, int ue8) {
   L.c.alpha = 1.702f;
   L.c.limit = 7.0f;
   L.c.eps = 1e-5f;
+  L.c.bf16_rows = (D + F) & 1;  /* ragged shapes also take the bf16-row products */
   const int64_t bpr1 = (D + 1) / 2, gpr1 = (D + 31) / 32, bpr2 = (F + 1) / 2, gpr2 = (F + 31) / 32;
   L.w1b = bbuf(E * 2 * F * bpr1, 0, 255);
   L.w1s = bbuf(E * 2 * F * gpr1, 119 + ue8, 123 + ue8);
@@ -231,6 +235,7 @@ static void decoder_cases(void) {
     c.rms_eps = 1e-5f;
     c.scale_dk = 1.0f;
     c.sink_tokens = q[13];
+    c.experts_bf16 = ci & 1;
     const int64_t V = c.vocab, D = c.d_model, L = c.n_layers, qd = c.n_heads * c.head_dim,
                   kd = c.kv_heads * c.head_dim, B = c.batch, steps = c.cache_len + 3;
     const int64_t npos = steps + c.n_heads;

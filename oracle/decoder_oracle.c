@@ -52,6 +52,7 @@
 typedef struct {
   int64_t d, f, e, k;
   float alpha, limit, eps;
+  int64_t bf16_rows;
 } oracle_cfg;
 
 int oracle_moe_forward(const float *x, int64_t n, const oracle_cfg *cfg, const uint8_t *w1b, const uint8_t *w1s,
@@ -174,6 +175,7 @@ typedef struct {
   float rms_eps;
   float scale_dk;           /* 1 with pre-scaled q/k (GPT-OSS) */
   int64_t sink_tokens;      /* StreamingMqaCache::sink_tokens (src/attention/streaming_mqa.rs:143) */
+  int64_t experts_bf16;     /* the device option: every MoE layer with cfg.bf16_rows = 1 */
 } oracle_dec_cfg;
 
 /* Weights as f32 (the device's bf16 values), per layer l at offset l * (layer size). */
@@ -279,7 +281,9 @@ int oracle_decoder_step(const oracle_dec_cfg *c, const oracle_dec_weights *w, co
     oracle_linear(ctx, B, qd, w->wo + l * D * qd, w->bo + l * D, D, o);
     for (int64_t i = 0; i < B * D; ++i) h[i] = h[i] + o[i];
     const oracle_moe_layer *m = moe + l;
-    rc = oracle_moe_forward(h, B, &m->cfg, m->w1b, m->w1s, m->w2b, m->w2s, m->ue8_offset, m->b1, m->b2,
+    oracle_cfg mc = m->cfg;
+    mc.bf16_rows = c->experts_bf16 ? 1 : 0;
+    rc = oracle_moe_forward(h, B, &mc, m->w1b, m->w1s, m->w2b, m->w2s, m->ue8_offset, m->b1, m->b2,
                                 m->router_w, m->router_b, m->gamma, m->layout, 1, 1, h2, NULL, NULL);
     if (rc != ORACLE_OK) break;
     memcpy(h, h2, sizeof(float) * B * D);

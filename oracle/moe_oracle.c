@@ -37,6 +37,10 @@
  *     module (third-party implementation of the same layer), zero-weight residual
  *     invariant (tests/moe_basic_tests.rs:31-33), gate/up layout permutation invariance,
  *     hand-computed one-hot closed forms.
+ *   oracle_round_bf16: brute-force nearest bf16 value (ties to the even significand) over
+ *     random, boundary and tie inputs.
+ *   oracle_moe_forward with bf16_rows: the same forward on rows and SwiGLU outputs rounded by
+ *     oracle_round_bf16 beforehand (bit-exact), and the default forward within the bf16 bar.
  *   oracle_moe_forward_reference: agrees with oracle_moe_forward (halves layout) where
  *     the reference's b2-per-f-tile quirk is inactive (F <= 256), and differs by exactly
  *     (ceil(F/256)-1) * sum_p w_p*b2 when it is active.
@@ -243,7 +247,23 @@ float oracle_swiglu(float g, float l, float alpha, float limit) {
 typedef struct {
   int64_t d, f, e, k;
   float alpha, limit, eps;
+  int64_t bf16_rows; /* 1: the expert products take the normalised rows and the SwiGLU outputs
+                        rounded to bf16 (the device's one-term option; no counterpart in the
+                        reference, which multiplies f32 rows) */
 } oracle_cfg;
+
+/* Nearest bf16 value of v (ties to the even significand; NaN stays NaN): f32 bits + 0x7FFF + the
+ * lowest kept bit, truncated to the top 16 bits. */
+float oracle_round_bf16(float v) {
+  uint32_t u;
+  memcpy(&u, &v, sizeof u);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u)
+    u = (u | 0x00400000u) & 0xFFFF0000u;
+  else
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  memcpy(&v, &u, sizeof v);
+  return v;
+}
 
 /* W1 source row that holds the gate (lin = 0) or linear (lin = 1) half of feature f.
  * layout 0 = halves ([0,F) gate, [F,2F) linear: src/quant/gpu.rs:112-113 / src/moe/mod.rs:336-337),
@@ -306,6 +326,8 @@ int oracle_moe_forward(const float *x, int64_t n, const oracle_cfg *cfg, const u
     oracle_rmsnorm(x, n, D, gamma, cfg->eps, xn);
   else
     memcpy(xn, x, sizeof(float) * (size_t)(n * D));
+  if (cfg->bf16_rows)  /* xn feeds only the expert products: routing reads x */
+    for (int64_t i = 0; i < n * D; ++i) xn[i] = oracle_round_bf16(xn[i]);
   oracle_route_logits(x, n, D, gamma, cfg->eps, apply_rmsnorm, router_w, router_b, E, lg);
   oracle_topk_softmax(lg, n, E, K, idx, wt);
   for (int64_t e = 0; e < E; ++e) {
@@ -332,7 +354,8 @@ int oracle_moe_forward(const float *x, int64_t n, const oracle_cfg *cfg, const u
         }
         sg = sg + b1[e * 2 * F + rg];
         sl = sl + b1[e * 2 * F + rl];
-        act[f] = oracle_swiglu(sg, sl, cfg->alpha, cfg->limit);
+        const float a = oracle_swiglu(sg, sl, cfg->alpha, cfg->limit);
+        act[f] = cfg->bf16_rows ? oracle_round_bf16(a) : a;
       }
       const float wp = wt[i];
       float *so = slot + i * D;

@@ -24,14 +24,16 @@ _i64 = ctypes.c_int64
 
 class _Cfg(ctypes.Structure):
     _fields_ = [("d", ctypes.c_int64), ("f", ctypes.c_int64), ("e", ctypes.c_int64), ("k", ctypes.c_int64),
-                ("alpha", ctypes.c_float), ("limit", ctypes.c_float), ("eps", ctypes.c_float)]
+                ("alpha", ctypes.c_float), ("limit", ctypes.c_float), ("eps", ctypes.c_float),
+                ("bf16_rows", ctypes.c_int64)]
 
 
 class _DecCfg(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("vocab", "d_model", "n_layers", "n_heads", "kv_heads", "head_dim",
                                               "batch", "cache_len", "window_policy", "window", "full_on_even",
                                               "rope_head_stride")] + \
-               [("rms_eps", ctypes.c_float), ("scale_dk", ctypes.c_float), ("sink_tokens", ctypes.c_int64)]
+               [("rms_eps", ctypes.c_float), ("scale_dk", ctypes.c_float), ("sink_tokens", ctypes.c_int64),
+                ("experts_bf16", ctypes.c_int64)]
 
 
 class _DecWeights(ctypes.Structure):
@@ -69,6 +71,8 @@ def lib():
         L.oracle_dispatch.argtypes = [_i32p, _i64, _i64, _i64, _i32p, _i32p, _i32p]
         L.oracle_swiglu.restype = ctypes.c_float
         L.oracle_swiglu.argtypes = [ctypes.c_float] * 4
+        L.oracle_round_bf16.restype = ctypes.c_float
+        L.oracle_round_bf16.argtypes = [ctypes.c_float]
         fwd = [_f32p, _i64, ctypes.POINTER(_Cfg), _u8p, _u8p, _u8p, _u8p, ctypes.c_int, _f32p, _f32p, _f32p,
                _f32p, _f32p]
         L.oracle_moe_forward.argtypes = fwd + [ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _f32p]
@@ -193,12 +197,14 @@ def _layer_args(layer):
     return cfg, arrs
 
 
-def moe_forward(layer, x, apply_rmsnorm=True, add_residual=True, layout=None):
-    """The build's layer semantics (see oracle_moe_forward).  Returns (y, idx, w)."""
+def moe_forward(layer, x, apply_rmsnorm=True, add_residual=True, layout=None, bf16_rows=False):
+    """The build's layer semantics (see oracle_moe_forward).  Returns (y, idx, w).  bf16_rows:
+    the expert products on rows and SwiGLU outputs rounded to bf16 (the device's one-term option)."""
     x = _c(x, np.float32)
     n, d = x.shape
     assert d == layer.d_model
     cfg, a = _layer_args(layer)
+    cfg.bf16_rows = int(bf16_rows)
     kk = min(max(layer.experts_per_token, 1), layer.num_experts)
     lay = {"halves": 0, "interleaved": 1}[layout or layer.gate_up_layout]
     y = np.empty_like(x)
@@ -281,9 +287,10 @@ def sink_attention(q, k, v, n_kv_heads, sinks=None, scale_dk=1.0) -> np.ndarray:
 class DecoderOracle:
     """CPU decoder state (f32 weights and cache) driven step by step by oracle_decoder_step.
 
-    ``data`` is a burnext_amd.decoder.DecoderData; the cache is [L][B][cache_len][kvH][dk] f32."""
+    ``data`` is a burnext_amd.decoder.DecoderData; the cache is [L][B][cache_len][kvH][dk] f32.
+    ``experts_bf16`` (default: the config's) models the device's bf16 expert rows."""
 
-    def __init__(self, data, batch: int):
+    def __init__(self, data, batch: int, experts_bf16=None):
         cfg = data.cfg
         self.cfg, self.batch = cfg, batch
         self.w = {k: np.ascontiguousarray(data.f32(k)) for k in
@@ -314,7 +321,8 @@ class DecoderOracle:
                                _p(self.table, _f32p))
         self._cc = _DecCfg(cfg.vocab_size, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.kv_heads, cfg.head_dim, batch,
                            cfg.cache_len, cfg.window_policy_code, cfg.window, int(cfg.full_on_even),
-                           cfg.rope_head_stride, cfg.rms_eps, cfg.scale_dk, cfg.sink_tokens)
+                           cfg.rope_head_stride, cfg.rms_eps, cfg.scale_dk, cfg.sink_tokens,
+                           int(cfg.experts_bf16 if experts_bf16 is None else experts_bf16))
 
     def load(self, k, v) -> None:
         """Cache rows for positions 0 .. len-1 (k, v [L, B, len, kvH, dk])."""

@@ -204,9 +204,10 @@ def test_gptoss_struct_layouts_match_header():
 #include <stdio.h>
 #include "burnext_gptoss.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu\n", sizeof(burnext_gptoss_config), offsetof(burnext_gptoss_config, kv_bf16),
+  printf("%zu %zu %zu %zu %zu %zu %zu\n", sizeof(burnext_gptoss_config), offsetof(burnext_gptoss_config, kv_bf16),
          offsetof(burnext_gptoss_config, rms_eps), offsetof(burnext_gptoss_config, scale_dk),
-         offsetof(burnext_gptoss_config, sink_tokens), sizeof(burnext_gptoss_weights));
+         offsetof(burnext_gptoss_config, sink_tokens), offsetof(burnext_gptoss_config, experts_bf16),
+         sizeof(burnext_gptoss_weights));
   printf("%zu %zu\n", offsetof(burnext_gptoss_weights, sinks), offsetof(burnext_gptoss_weights, lm_head));
   return 0;
 }
@@ -219,7 +220,7 @@ int main(void) {
     vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     assert vals == [ctypes.sizeof(N.GptOssConfigC), N.GptOssConfigC.kv_bf16.offset, N.GptOssConfigC.rms_eps.offset,
                     N.GptOssConfigC.scale_dk.offset, N.GptOssConfigC.sink_tokens.offset,
-                    ctypes.sizeof(N.GptOssWeightsC), N.GptOssWeightsC.sinks.offset,
+                    N.GptOssConfigC.experts_bf16.offset, ctypes.sizeof(N.GptOssWeightsC), N.GptOssWeightsC.sinks.offset,
                     N.GptOssWeightsC.lm_head.offset]
 
 
@@ -249,6 +250,7 @@ def _gweights():
     (dict(vocab_size=0), N.BURNEXT_INVALID_ARG, "zero dimension"),
     (dict(cache_len=0), N.BURNEXT_INVALID_ARG, "zero dimension"),
     (dict(kv_bf16=2), N.BURNEXT_INVALID_ARG, "kv_bf16"),
+    (dict(experts_bf16=2), N.BURNEXT_INVALID_ARG, "experts_bf16"),
     (dict(rope_head_stride=3), N.BURNEXT_INVALID_ARG, "rope_head_stride"),
     (dict(window=0), N.BURNEXT_INVALID_ARG, "window"),
     (dict(window_policy=3), N.BURNEXT_INVALID_ARG, "window_policy"),

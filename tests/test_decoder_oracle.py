@@ -215,7 +215,8 @@ def _f64_model(oracle, data, batch):
                     wts = (e / e.sum())[: len(act)]
                     ctx[b, hh * dk:(hh + 1) * dk] = sum(wt * r[1][hh // g] for wt, r in zip(wts, act))
             h = h + ctx @ W["wo"][l].T + W["bo"][l]
-            h = oracle.moe_forward(data.moe[l], h.astype(np.float32))[0].astype(np.float64)
+            h = oracle.moe_forward(data.moe[l], h.astype(np.float32),
+                                   bf16_rows=cfg.experts_bf16)[0].astype(np.float64)
         hid = h
         logits = _rms64(h, W["norm_final"], cfg.rms_eps) @ W["lm_head"].T
         return logits, hid
@@ -236,7 +237,8 @@ def _f64_model(oracle, data, batch):
                                        # sink rows kept through eviction; windows widened by them
                                        (dict(sink_tokens=1), 0), (dict(sink_tokens=2, window=2), 0),
                                        (dict(sink_tokens=2, window_policy="full"), 2),
-                                       (dict(sink_tokens=5), 0)])  # cache_len - 1: nothing rolls
+                                       (dict(sink_tokens=5), 0),  # cache_len - 1: nothing rolls
+                                       (dict(experts_bf16=True), 0)])  # the MoE layers on bf16 rows
 def test_decoder_step_vs_f64(oracle, kw, window):
     D = dec()
     cfg = tiny_cfg(**kw)

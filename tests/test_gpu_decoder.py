@@ -17,6 +17,10 @@ pytestmark = pytest.mark.gpu
 
 TOL_F32 = 5e-4
 TOL_BF16 = 2e-2
+# experts_bf16 against the oracle that rounds the same rows: the device's f32 rows and SwiGLU
+# outputs differ from the oracle's in the last bits (summation order), so now and then one value
+# rounds to the other bf16 neighbour; one such value moves a row by up to a few 1e-3
+TOL_EXPERTS_BF16 = 5e-3
 
 
 @pytest.fixture(scope="module")
@@ -146,6 +150,46 @@ def test_decode_bf16_cache(D, oracle):
         tok = o_nxt
 
 
+@pytest.mark.parametrize("case", ["every_other", "wo_32_parts", "wide_d_unfused", "groups16"])
+def test_decode_experts_bf16(D, oracle, case):
+    """experts_bf16 (the expert projections on bf16-rounded rows) against the oracle that rounds the
+    same rows (its bf16_rows mode), four steps.  The cases take the router that also forms the
+    residual row, the separate residual add with the decode router, and (d_model 4160) the
+    general router.  (Over many steps a value rounded to the other bf16 neighbour can move a
+    later layer's expert choice: the single-layer test below runs the whole eviction range.)"""
+    cfg = _cfg(D, experts_bf16=True, **CASES[case])
+    data = D.make_decoder(cfg, seed=14, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B = 3
+    print(f"[decoder] experts_bf16 {case}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    orc = oracle.DecoderOracle(data, B)
+    tok = np.array([3, 100, 7], np.int32)
+    for pos in range(4):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        _check_step(oracle, TOL_EXPERTS_BF16, nxt, lg, hid, o_nxt, o_lg, o_hid, (case, pos))
+        tok = o_nxt
+    dev.close()
+
+
+def test_decode_experts_bf16_vs_f32(D, oracle):
+    """experts_bf16 against the f32 decoder oracle (the reference's arithmetic) within the bf16 bar,
+    one layer over the whole eviction range (its cache rows come from the embeddings alone, so
+    they stay equal to the oracle's)."""
+    cfg = _cfg(D, experts_bf16=True, n_layers=1)
+    data = D.make_decoder(cfg, seed=15, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    B = 4
+    dev = D.GptOssDecoder(data, max_batch=B)
+    orc = oracle.DecoderOracle(data, B, experts_bf16=False)
+    tok = np.array([3, 100, 7, 250], np.int32)
+    for pos in range(cfg.cache_len + 3):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        _check_step(oracle, TOL_BF16, nxt, lg, hid, o_nxt, o_lg, o_hid, pos)
+        tok = o_nxt
+    dev.close()
+
+
 def test_greedy_generation_and_null_outputs(D, oracle):
     """Free-running greedy generation equals the oracle's token for token; the step without
     logits / hidden outputs returns the same tokens; batch rows are independent."""
@@ -236,19 +280,19 @@ def test_decode_c5_full_size(D, oracle):
     dev.close()
 
 
-@pytest.mark.parametrize("kv_bf16", [False, True])
-def test_decode_20b_shapes_full_cache(D, oracle, kv_bf16):
+@pytest.mark.parametrize("kv_bf16,experts_bf16", [(False, False), (True, False), (False, True)])
+def test_decode_20b_shapes_full_cache(D, oracle, kv_bf16, experts_bf16):
     """GPT-OSS-20B layer shapes (d_model 2880, 64 q / 8 kv heads of 64, 32 experts top-4, 128-row
     window on the odd layer) with an 8192-row cache loaded to 8190 rows: three steps fill it and
     evict the oldest row."""
-    cfg = D.GptOssConfig(vocab_size=50001, n_layers=2, kv_bf16=kv_bf16, max_seq_len=16384)
+    cfg = D.GptOssConfig(vocab_size=50001, n_layers=2, kv_bf16=kv_bf16, experts_bf16=experts_bf16, max_seq_len=16384)
     data = D.make_decoder(cfg, seed=21, sinks_std=0.8, norm_std=0.1)
     B, pre = 8, cfg.cache_len - 2
     rng = np.random.default_rng(5)
     shape = (cfg.n_layers, B, pre, cfg.kv_heads, cfg.head_dim)
     k = (rng.standard_normal(shape, dtype=np.float32) * 0.6).astype(np.float32)
     v = rng.standard_normal(shape, dtype=np.float32).astype(np.float32)
-    print(f"[decoder] 20b shapes kv_bf16={kv_bf16}", flush=True)
+    print(f"[decoder] 20b shapes kv_bf16={kv_bf16} experts_bf16={experts_bf16}", flush=True)
     dev = D.GptOssDecoder(data, max_batch=B)
     dev.cache_load(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
     orc = oracle.DecoderOracle(data, B)
@@ -259,7 +303,8 @@ def test_decode_20b_shapes_full_cache(D, oracle, kv_bf16):
         orc.load(k, v)
     del k, v
     tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
-    tol = TOL_BF16 if kv_bf16 else TOL_F32
+    # the oracle rounds the expert rows as experts_bf16 does
+    tol = TOL_BF16 if kv_bf16 else TOL_EXPERTS_BF16 if experts_bf16 else TOL_F32
     for pos in range(pre, pre + 3):
         nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
         o_nxt, o_lg, o_hid = orc.step(tok, pos)

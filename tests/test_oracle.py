@@ -241,13 +241,17 @@ def dequant_np(blocks, scales, cols, ue8=0):
     return vals * np.repeat(np.ldexp(1.0, s), 32, axis=-1)[..., :cols]
 
 
-def layer_f64(L, x, idx, w, layout, norm=True, residual=True):
-    """float64 brute force of the layer for given routing (matmul-based, not the oracle's loops)."""
+def layer_f64(L, x, idx, w, layout, norm=True, residual=True, round_rows=None, round_act=None):
+    """float64 brute force of the layer for given routing (matmul-based, not the oracle's loops).
+    round_rows(xn) / round_act(act): applied to the normalised rows / SwiGLU outputs (the rows
+    are then the given f32 ones, round_rows receives None) before the expert products."""
     D, F = L.d_model, L.ffn_hidden
     x64 = x.astype(np.float64)
     xn = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + L.rms_eps) if norm else x64
     if L.gamma_f32 is not None and norm:
         xn = xn * L.gamma_f32
+    if round_rows is not None:
+        xn = round_rows(xn).astype(np.float64)
     W1 = dequant_np(L.w1_blocks, L.w1_scales, D, L.ue8_offset)
     W2 = dequant_np(L.w2_blocks, L.w2_scales, F, L.ue8_offset)
     if layout == "interleaved":
@@ -261,6 +265,8 @@ def layer_f64(L, x, idx, w, layout, norm=True, residual=True):
             h = W1[e] @ xn[t] + L.b1_f32[e]
             g, l = np.minimum(h[gi], L.swiglu_limit), np.clip(h[li], -L.swiglu_limit, L.swiglu_limit)
             act = g / (1 + np.exp(-L.swiglu_alpha * g)) * (l + 1)
+            if round_act is not None:
+                act = round_act(act).astype(np.float64)
             y[t] += w[t, p] * (W2[e] @ act + L.b2_f32[e])
     return y
 
@@ -284,6 +290,68 @@ def test_forward_vs_f64_20b_shape(oracle):
     ref = layer_f64(L, x, idx, w.astype(np.float64), "interleaved")
     assert oracle.max_abs_rel(y, ref) < 1e-5
     assert oracle.max_abs_rel(y - x, ref - x) < 1e-4
+
+
+def _nearest_bf16_bits(v):
+    """bf16 bits nearest to the float32 v by search over its two bf16 neighbours (the magnitude
+    truncated to 8 significand bits and the next one up), exact rational distances, ties to the
+    even significand; the largest finite bf16 steps up to infinity (at 2^128)."""
+    bits = int(np.float32(v).view(np.uint32))
+    lo = bits & 0xFFFF0000
+    hi = lo + 0x10000
+
+    def val(b):
+        f = np.uint32(b).view(np.float32)
+        return Fraction(2) ** 128 * (1 if f > 0 else -1) if np.isinf(f) else Fraction(float(f))
+
+    x = Fraction(float(np.float32(v)))
+    dl, dh = abs(x - val(lo)), abs(x - val(hi))
+    return lo >> 16 if dl < dh or (dl == dh and (lo >> 16) % 2 == 0) else hi >> 16
+
+
+def test_round_bf16_brute_force(oracle):
+    """oracle_round_bf16 (the rounding of the bf16 expert rows) against the nearest-value search on
+    random magnitudes of every exponent, exact ties (even and odd significands), the largest finite
+    values (one rounds to infinity), subnormals, zeros and infinities; NaN stays NaN."""
+    rng = np.random.default_rng(0)
+    vals = list(rng.integers(0, 1 << 32, 4000, dtype=np.uint64).astype(np.uint32))
+    for hi16 in (0x3F80, 0x3F81, 0xBF80, 0xBF81, 0x7F7E, 0x7F7F, 0x0000, 0x0001, 0x8001):
+        for lo16 in (0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF):
+            vals.append(np.uint32((hi16 << 16) | lo16))
+    L = oracle.lib()
+    for b in vals:
+        f = np.uint32(b).view(np.float32)
+        got = int(np.float32(L.oracle_round_bf16(float(f))).view(np.uint32))
+        if np.isnan(f):
+            assert np.isnan(np.uint32(got).view(np.float32))
+            continue
+        if np.isinf(f):
+            assert got == int(b)
+            continue
+        assert got & 0xFFFF == 0 and got >> 16 == _nearest_bf16_bits(f), hex(int(b))
+
+
+def test_forward_bf16_rows_vs_f64(oracle):
+    """bf16_rows: the forward whose expert products take the normalised rows and the SwiGLU
+    outputs rounded to bf16 equals the float64 brute force with those two roundings (the rows as
+    oracle_rmsnorm forms them in f32); leaving out either rounding moves the brute force by more
+    than a hundred times the bar, so each is pinned."""
+    S = synth()
+    L = S.make_layer(256, 192, 8, 2, seed=3, dtype="f32", with_gamma=True)
+    x = S.make_tokens(6, 256, seed=4, dtype="f32")
+    y, idx, w = oracle.moe_forward(L, x, add_residual=False, bf16_rows=True)
+    xn32 = oracle.rmsnorm(x, L.gamma_f32, L.rms_eps)
+    rnd = lambda a: S.round_bf16(np.asarray(a, np.float32))  # noqa: E731
+    rows = lambda _xn: rnd(xn32)  # noqa: E731
+    w64 = w.astype(np.float64)
+    ref = layer_f64(L, x, idx, w64, "interleaved", residual=False, round_rows=rows, round_act=rnd)
+    assert oracle.max_abs_rel(y, ref) < 1e-6
+    no_rows = layer_f64(L, x, idx, w64, "interleaved", residual=False, round_act=rnd)
+    no_act = layer_f64(L, x, idx, w64, "interleaved", residual=False, round_rows=rows)
+    assert oracle.max_abs_rel(y, no_rows) > 1e-4 and oracle.max_abs_rel(y, no_act) > 1e-4
+    y32, idx32, _ = oracle.moe_forward(L, x, add_residual=False)
+    assert np.array_equal(idx, idx32)  # routing reads the unrounded rows
+    assert oracle.max_abs_rel(y, y32) < 2e-2
 
 
 def test_forward_matches_hf_gpt_oss_experts(oracle):
