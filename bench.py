@@ -228,16 +228,9 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     kflops = {"gate_up": 2 * nk * 2 * F * D, "down": 2 * nk * D * F}
     layer_bytes = synth.decode_bytes(data, touched, T, 2)
     stage_us = dict(kavg_us)
-    gate_label = "gate_up"
-    if "swiglu" in stage_us:  # few-expert decode: the gate_up stage is the K-part GEMV + its SwiGLU kernel
-        stage_us["gate_up"] = stage_us["gate_up"] + stage_us.pop("swiglu")
-        gate_label = "gate_up+swiglu"
     dominant = max((k for k in stage_us if k in kbytes), key=stage_us.get)
-    label = gate_label if dominant == "gate_up" else dominant
+    label = dominant
     traffic = measured_traffic(name, dominant)
-    if traffic is not None and label == "gate_up+swiglu":
-        sw = measured_traffic(name, "swiglu")
-        traffic = traffic + sw if sw is not None else None
     prefill = T >= 1024
     if prefill:
         fl = kflops[dominant]

@@ -29,7 +29,7 @@ ADD_RESIDUAL = 2
 FORWARD_DEFAULT = APPLY_RMSNORM | ADD_RESIDUAL
 FUSED_EXPERTS = 4  # forward only, opt-in: one launch for the experts of a batch of <= 16 tokens
 NUM_KERNELS = 8
-KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine", "swiglu", "experts"]
+KERNEL_NAMES = ["router", "topk", "dispatch", "gate_up", "down", "combine", "reserved", "experts"]
 
 # Every symbol include/burnext_moe.h declares.
 EXPORTS = ["burnext_moe_layer_create", "burnext_moe_layer_destroy", "burnext_moe_workspace_size",

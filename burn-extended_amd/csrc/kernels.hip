@@ -480,12 +480,7 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
         for (int j = 0; j < 8; ++j) u[j] = a.apply_norm ? (xv[t][i][j] * ir) * g[j] : xv[t][i][j];
         const size_t row = t0 + (uint32_t)t;
         const bool tv = (uint32_t)t < nt;
-        if (a.xn && tv && c0 < a.Dp) {
-          if (a.xn_bf16)
-            store8((uint16_t *)a.xn + row * a.Dp + c0, u);
-          else
-            store8((XT *)a.xn + row * a.Dp + c0, u);
-        }
+        if (a.xn && tv && c0 < a.Dp) store8((XT *)a.xn + row * a.Dp + c0, u);
         if (a.xq.hi && 512u * i < a.xq.kq) {  // wave-uniform
           float amax = 0.0f;
 #pragma unroll
@@ -1362,6 +1357,9 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // gemv_share gives it (decode-sized batches) or a strided share (units part + wpe * i of slot
 // g / wpe, larger batches), wave w every 4th of them from its w-th.  A unit is a row tile or (down with
 // ksplit) one of ksplit fixed K-parts of a row tile (unit u: part u / nrt of row tile u mod nrt).
+// gate_up in kGateUpSplit K-parts: the workgroup's units are row tiles and wave w takes K-part w of
+// every one of them; at each tile's end the parts meet in LDS (one barrier), wave 0 sums them in
+// part order (b1 in part 0) and writes the SwiGLU rows.
 // Every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the
 // expert's routed tokens; one pass at decode sizes).  A workgroup learns num_active, its expert,
 // segment and first tokens from one round trip (num_active plus the record table).
@@ -1386,7 +1384,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t nrt = a.nrt;
   // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
   constexpr uint32_t nsplit = (uint32_t)SPLIT;  // a.ksplit, fixed at compile time
-  const uint32_t nunits = nrt * nsplit;
+  constexpr bool kInWg = GATE_UP && SPLIT > 1;    // K-parts of a row tile on the 4 waves of a workgroup
+  static_assert(!kInWg || SPLIT == 4, "one K-part per wave");
+  const uint32_t nunits = kInWg ? nrt : nrt * nsplit;
   // one round trip: num_active and the record table (the table is staged through the B area)
   const uint32_t na = (uint32_t)*a.num_active;
   {
@@ -1521,10 +1521,13 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   };
 
   // this wave's units: lo + us * i for i = wv, wv + 4, ... < ntw (first unit clamped into the
-  // expert for the start-up loads of a wave without units)
-  const uint32_t my_first = lo + us * wv, tstride = 4u * us;
-  const uint32_t my_tiles = wv < ntw ? (ntw - wv + 3u) / 4u : 0u;
-  const uint32_t first_c = min(my_first, nunits - 1u);
+  // expert for the start-up loads of a wave without units); in-workgroup K-parts: K-part wv of
+  // row tiles lo + us * i, i < ntw (unit index rt + wv * nrt)
+  const uint32_t my_first = kInWg ? lo + wv * nrt : lo + us * wv, tstride = kInWg ? us : 4u * us;
+  const uint32_t my_tiles = kInWg ? ntw : (wv < ntw ? (ntw - wv + 3u) / 4u : 0u);
+  const uint32_t first_c = kInWg ? my_first : min(my_first, nunits - 1u);
+  float *red = (float *)(smem + gemv_red_offset(NT, mtm, a.nb, a.nrec));  // kInWg: [2][4][64][4]
+  uint32_t parity = 0;
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
   uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
   uint4 abuf[CJ];
@@ -1596,20 +1599,39 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     if (++st < nst) return true;
     st = 0;
     // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
-    if (bval) {
-      const uint32_t r0 = rt * 16u + 4u * q;
-      if constexpr (GATE_UP && SPLIT > 1) {
-        // raw pre-activation rows of K-part h (b1 in part 0), segment-order slot rows
-        const int pos = seg0 + (int)(m0 + i16);
-        float *o = a.out + h * a.out_half + (size_t)pos * a.out_stride + r0;
-        const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : bias4;
-        if (r0 + 3u < a.out_rows) {
-          *(float4 *)o = make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
-        } else {
-          for (uint32_t r = 0; r < 4u; ++r)
-            if (r0 + r < a.out_rows) o[r] = acc[r] + b4[r];
+    if constexpr (kInWg) {
+      // every wave (a workgroup's waves walk the same tiles): part h's rows, b1 in part 0
+      const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : bias4;
+      float *rp = red + (size_t)parity * (4u * 64u * 4u);
+      *(float4 *)(rp + (wv * 64u + lane) * 4u) = make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
+      __syncthreads();
+      if (wv == 0u && bval) {
+        float v[4];
+#pragma unroll
+        for (uint32_t r = 0; r < 4u; ++r) v[r] = 0.0f;
+#pragma unroll
+        for (uint32_t hh = 0; hh < 4u; ++hh) {
+          const float4 pp = *(const float4 *)(rp + (hh * 64u + lane) * 4u);
+          v[0] = v[0] + pp.x;
+          v[1] = v[1] + pp.y;
+          v[2] = v[2] + pp.z;
+          v[3] = v[3] + pp.w;
         }
-      } else if constexpr (GATE_UP) {
+        const int pos = seg0 + (int)(m0 + i16);
+        const uint32_t f0 = (rt * 16u + 4u * q) >> 1;
+        const float o0 = swiglu_clamp_f(v[0], v[1], a.alpha, a.limit);
+        const float o1 = swiglu_clamp_f(v[2], v[3], a.alpha, a.limit);
+        float *o = a.out + (size_t)pos * a.out_stride + f0;
+        if (f0 + 1u < a.out_rows) {
+          *(float2 *)o = make_float2(o0, o1);
+        } else if (f0 < a.out_rows) {
+          o[0] = o0;
+        }
+      }
+      parity ^= 1u;  // the next tile's parts go to the other half (wave 0 may still read this one)
+    } else if (bval) {
+      const uint32_t r0 = rt * 16u + 4u * q;
+      if constexpr (GATE_UP) {
         const int pos = seg0 + (int)(m0 + i16);
         const uint32_t f0 = r0 >> 1;
         const float o0 = swiglu_clamp_f(acc[0] + bias4[0], acc[1] + bias4[1], a.alpha, a.limit);
@@ -2022,7 +2044,7 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   const uint64_t nunits = (uint64_t)a.nrt * (a.ksplit > 1u ? a.ksplit : 1u);
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid), block(kGemvThreads);
-  const size_t lds = gemv_total_lds_bytes(nt, a.mt_max, a.nb, a.nrec);
+  const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
   const bool split = !gate_up && a.ksplit > 1u;
@@ -2060,32 +2082,6 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   } else {
     return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-// SwiGLU of the summed gate_up K-parts (interleaved rows: 2f gate, 2f + 1 linear), one output
-// per thread.
-__global__ __launch_bounds__(256) void swiglu_parts_kernel(SwigluPartsArgs a) {
-  const uint32_t r = blockIdx.y, f = blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= a.F) return;
-  const float *p = a.parts + (size_t)r * a.rows_p + 2u * f;
-  float2 v[kGateUpSplit];  // every part requested before the first is summed
-#pragma unroll
-  for (uint32_t h = 0; h < kGateUpSplit; ++h) v[h] = *(const float2 *)(p + h * a.part_stride);
-  float g = 0.0f, l = 0.0f;
-#pragma unroll
-  for (uint32_t h = 0; h < kGateUpSplit; ++h) {
-    g = g + v[h].x;
-    l = l + v[h].y;
-  }
-  a.act[(size_t)r * a.act_stride + f] = swiglu_clamp_f(g, l, a.alpha, a.limit);
-}
-
-hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s) {
-  if (a.rows == 0 || a.F == 0 || 2u * a.F > a.rows_p || (a.rows_p & 1u) || (a.part_stride & 1u) ||
-      a.nparts != kGateUpSplit)
-    return hipErrorInvalidValue;
-  (void)launch_kernel(swiglu_parts_kernel, dim3((a.F + 255u) / 256u, a.rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

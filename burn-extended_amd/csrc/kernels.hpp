@@ -54,7 +54,7 @@ struct RouterArgs {
   uint32_t n, D, Dpad, Dp, E, tb, epw;
   float eps;
   int apply_norm;
-  int xn_bf16;        // xn rows rounded to bf16 (nearest even) whatever the x dtype
+  int xn_bf16;        // xn rows rounded to bf16 (nearest even) whatever the x dtype (router_kernel)
 };
 
 // Top-k + softmax per token (one wave per token) from logits [n, E].
@@ -104,10 +104,10 @@ struct GemvArgs {
   float *out;             // gate_up: act [n*k, Fp] (segment order); down: token-major slots [n*k, Dp]
   uint32_t out_stride;
   float alpha, limit;
-  // every row tile's K range split into ksplit (0 or 1: none) fixed parts, separate work units;
-  // part h's partial sums go to out + h * out_half (bias in part 0).  down: slot rows, combine
-  // adds the parts; gate_up: raw pre-activation rows [n*k, out_stride] of the out_rows W1 rows,
-  // finished by swiglu_parts_kernel
+  // every row tile's K range split into ksplit (0 or 1: none) fixed parts.  down: separate work
+  // units, part h's partial sums go to out + h * out_half (bias in part 0), the combine adds the
+  // parts; gate_up (kGateUpSplit parts): wave h of a workgroup takes part h of each of its row
+  // tiles, the workgroup sums the parts in order (bias in part 0) and writes the SwiGLU rows
   uint32_t ksplit;
   uint64_t out_half;
 };
@@ -234,16 +234,6 @@ struct CombineArgs {
   uint32_t slice_grid, slice_cap;
 };
 
-// act[r, f] = SwiGLU(sum_h part_h[r, 2f], sum_h part_h[r, 2f + 1]) (h ascending) for the
-// gate_up K-parts of a decode-sized batch.
-struct SwigluPartsArgs {
-  const float *parts;  // [nparts][rows, rows_p]
-  uint64_t part_stride;
-  float *act;          // [rows, act_stride]
-  uint32_t nparts, rows, F, rows_p, act_stride;
-  float alpha, limit;
-};
-
 struct DequantArgs {
   const uint8_t *blocks, *scales;
   void *out;
@@ -265,6 +255,15 @@ __host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint
 __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
   return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
+// gate_up in K-parts (kGateUpSplit waves of a workgroup per row tile): the parts' tile results
+// meet in LDS after the other regions, [tile parity][wave][lane] x 4 floats
+constexpr size_t kGemvRedBytes = 2u * 4u * 64u * 16u;
+__host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec) + 15u) & ~(size_t)15u;
+}
+__host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red) {
+  return red ? gemv_red_offset(nt, mt_max, nb, nrec) + kGemvRedBytes : gemv_total_lds_bytes(nt, mt_max, nb, nrec);
+}
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
 constexpr uint32_t kRouterThreads = 256;
@@ -283,7 +282,7 @@ constexpr uint32_t kGemvThreads = 256;
 constexpr uint32_t kRoundWeight[2][4] = {{20, 10, 4, 2}, {20, 16, 11, 8}};
 constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert GEMV (decode-sized batches; 3, 4 and 6 measured slower)
 // K-parts per gate_up row tile when a batch touches so few experts that whole row tiles leave most
-// waves idle (gate_up then writes partial pre-activations, swiglu_parts_kernel finishes them)
+// waves idle (one part per wave of a workgroup, summed in LDS before the SwiGLU epilogue)
 constexpr uint32_t kGateUpSplit = 4;
 constexpr uint32_t kDownSplitFew = 4;  // K-parts per down row tile for the same batches
 constexpr uint32_t kMaxTopK = 32;
@@ -318,7 +317,6 @@ hipError_t launch_fused(const FusedArgs &a, const FusedGeom &g, int nt, bool x_b
 // parts part_stride apart, their count as the fused kernel set it (CombineArgs.num_active)
 hipError_t launch_combine_slices(const CombineArgs &a, bool x_bf16, hipStream_t s);
 hipError_t configure_fused_kernels();
-hipError_t launch_swiglu_parts(const SwigluPartsArgs &a, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs &a, bool gate_up, uint32_t grid, hipStream_t s);
 hipError_t configure_gemm_kernels();
 size_t gemm_lds_bytes();

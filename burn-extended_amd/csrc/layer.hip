@@ -294,6 +294,8 @@ struct GemvCfg {
   uint32_t mt, grid, nrec;
 };
 
+bool gate_up_split(const burnext_moe_layer &L, uint64_t n);
+
 GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   const TiledMx &t = gate_up ? L.w1 : L.w2;
   GemvCfg c{};
@@ -315,16 +317,17 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
     }
   mt = (uint32_t)std::min<uint64_t>(mt, n);
   c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
-  const size_t lds = gemv_total_lds_bytes(nt, c.mt, t.nb, c.nrec);
+  const size_t lds = gemv_launch_lds_bytes(nt, c.mt, t.nb, c.nrec, gate_up && gate_up_split(L, n));
   const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, (160 * 1024) / std::max<size_t>(lds, 1)));
   c.grid = (uint32_t)std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L.num_cus * per_cu, max_active * t.nrt));
   return c;
 }
 
 // Decode-sized batches that touch so few experts that their gate_up row tiles are fewer than 8 per
-// CU (2/3 of a tile per wave) split every tile's K range in kGateUpSplit parts: a wave then streams
-// 6 instead of 23 K-groups at D = 2880 (120B T = 1: 4 experts, 1440 row tiles for 3072 waves).
-inline bool gate_up_split(const burnext_moe_layer &L, uint64_t n) {
+// CU (2/3 of a tile per wave) split every tile's K range in kGateUpSplit parts, one per wave of a
+// workgroup: a wave then streams 6 instead of 23 K-groups at D = 2880 (120B T = 1: 4 experts, 1440
+// row tiles for 3072 waves), and the workgroup sums the parts before the SwiGLU.
+bool gate_up_split(const burnext_moe_layer &L, uint64_t n) {
   return n <= kSmallRouteMaxTokens && std::min<uint64_t>(L.E, n * L.K) * L.w1.nrt < 8ull * (uint64_t)L.num_cus &&
          (L.w1.nb + 3u) / 4u >= kGateUpSplit;
 }
@@ -333,7 +336,6 @@ inline bool gate_up_split(const burnext_moe_layer &L, uint64_t n) {
 struct WsLayout {
   uint64_t rms, logits, topk_idx, topk_w, meta, exrec, perm, pos_of, xn, act, ypart, dcnt, total;
   uint64_t tile_off, xq[4], aq[4];  // grouped-GEMM path: tile prefix, xq / act rows (hi lo shi slo)
-  uint64_t upart;                   // gate_up K-parts of a few-expert decode batch (gate_up_split)
   bool gemm;                        // the grouped-GEMM regions are present
 };
 
@@ -429,7 +431,6 @@ WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   const uint64_t yrows = std::max({nk, ns * L.K * kDownSplit, ms * L.K * kDownSplitFew, frows});
   w.ypart = take(yrows * L.Dp * 4);
   w.dcnt = take(((n + kDispatchChunk - 1) / kDispatchChunk) * (uint64_t)L.E * 4);
-  if (ms) w.upart = take((uint64_t)kGateUpSplit * ms * L.K * L.w1.rows_p * 4);
   w.total = off;
   return w;
 }
@@ -443,7 +444,6 @@ struct WsPtrs {
   int32_t *exrec;
   void *xn;
   float *act, *ypart;
-  float *upart;  // gate_up K-parts [kGateUpSplit][n*k, w1.rows_p] (gate_up_split)
   int32_t *tile_off;
   int32_t *dcnt;  // per-chunk expert counts of the multi-workgroup dispatch
   QRows xq, aq;
@@ -470,7 +470,6 @@ WsPtrs ws_ptrs(const burnext_moe_layer &L, const WsLayout &w, void *base) {
   p.pos_of = (int32_t *)(b + w.pos_of);
   p.act = (float *)(b + w.act);
   p.ypart = (float *)(b + w.ypart);
-  p.upart = w.upart ? (float *)(b + w.upart) : nullptr;
   p.dcnt = (int32_t *)(b + w.dcnt);
   return p;
 }
@@ -536,7 +535,7 @@ struct ProfScope final : LaunchTimer {
 };
 
 enum KernelId {
-  kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5, kKSwiglu = 6, kKExperts = 7
+  kKRouter = 0, kKTopk = 1, kKDispatch = 2, kKGateUp = 3, kKDown = 4, kKCombine = 5, kKExperts = 7  // 6: reserved
 };
 
 burnext_status check_launch(hipError_t e, const char *what) {
@@ -571,7 +570,7 @@ burnext_status run_router(burnext_moe_layer *L, const void *x, bool x_bf16, uint
   const bool vec = L->D % 8 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)ra.rw & 15u) == 0;
   const uint32_t lim = 512u * kFrontChunks;
   const bool rows = vec && n >= kRouterRowsMinTokens && L->D <= lim && (!xn || L->Dp <= lim) &&
-                    (!xq || !xq->hi || xq->kq <= lim);
+                    (!xq || !xq->hi || xq->kq <= lim) && !xn_bf16;  // (bf16 rows: router_kernel)
   ProfScope ps(L, s, kKRouter);
   // 4 tokens per wave (32 per workgroup) once that still gives every CU a workgroup: half the LDS
   // reads per token (measured: 120B T = 8192 206 -> 171 us; slower while the grid is short of the CUs)
@@ -933,7 +932,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
   // evenly over the waves; measured slower from 64 tokens on)
-  const bool up_split = gate_up_split(*L, n) && p.upart;
+  const bool up_split = gate_up_split(*L, n);
   // (few touched experts: kDownSplitFew parts, as many as the workspace holds for those batches)
   const uint32_t ksplit = (up_split && (L->w2.nb + 3u) / 4u >= kDownSplitFew) ? kDownSplitFew
                         : (n <= kSmallRouteMaxTokens && (L->w2.nb + 3u) / 4u >= kDownSplit) ? kDownSplit : 1u;
@@ -989,34 +988,12 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
       g.ksplit = ksplit;
       g.out_half = n * L->K * L->Dp;
     }
-    if (gate_up && up_split) {  // raw pre-activation K-parts, finished by swiglu_parts_kernel
-      g.ksplit = kGateUpSplit;
-      g.out = p.upart;
-      g.out_stride = L->w1.rows_p;
-      g.out_rows = 2 * L->F;
-      g.out_half = n * L->K * L->w1.rows_p;
-    }
+    if (gate_up && up_split) g.ksplit = kGateUpSplit;  // K-parts on the waves of a workgroup, summed there
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xnb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
-  if (up_split) {
-    SwigluPartsArgs sa{};
-    sa.parts = p.upart;
-    sa.part_stride = n * L->K * L->w1.rows_p;
-    sa.act = p.act;
-    sa.nparts = kGateUpSplit;
-    sa.rows = (uint32_t)(n * L->K);
-    sa.F = L->F;
-    sa.rows_p = L->w1.rows_p;
-    sa.act_stride = L->Fp;
-    sa.alpha = L->alpha;
-    sa.limit = L->limit;
-    ProfScope ps(L, s, kKSwiglu);
-    st = check_launch(launch_swiglu_parts(sa, s), "gate_up SwiGLU launch");
-    if (st != BURNEXT_OK) return st;
-  }
   st = gemv(false);
   if (st != BURNEXT_OK) return st;
 

@@ -170,11 +170,10 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
  * launch counts since the last read (it synchronises on the recorded events) and resets.  Event
  * pairs are pooled per process: an enable call made when every layer's records have been read
  * returns them to the pool, so a later recorded pass creates no events between its launches.
- * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up, 4 down, 5 combine, 6 SwiGLU of the gate_up
- * K-parts, 7 the fused experts (batches of at most 16 tokens run top-k and dispatch as one kernel,
- * recorded under id 1; id 2 then records nothing; such batches run gate_up, SwiGLU and down as one
- * kernel, id 7, except inside the decoder step, whose MoE combine also writes the next norm: there
- * ids 3, 4 and, for batches that touch few experts, 6 record them). */
+ * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up (with its SwiGLU), 4 down, 5 combine,
+ * 6 reserved (records nothing), 7 the fused experts of BURNEXT_FUSED_EXPERTS (gate_up, SwiGLU and
+ * down as one kernel; ids 3 and 4 then record nothing).  Batches of at most 16 tokens run top-k
+ * and dispatch as one kernel, recorded under id 1; id 2 then records nothing. */
 #define BURNEXT_NUM_KERNELS 8
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t layer, int enable);
 burnext_status burnext_moe_profile_read(burnext_moe_layer_t layer, double *ms_total, uint64_t *launches,
