@@ -269,8 +269,9 @@ struct AttnArgs {
   float *part;           // [B][kvH][nchunk][groups][dk + 2]
   uint32_t nH, kvH, dk, cap_p, nchunk;
   // the active window's keys i < nkeys: the sink rows first (i < nsk: slot sk_lo + i, holding
-  // position sk_lo + i), then the recent positions p_lo + (i - nsk) at their ring slots
-  uint32_t nkeys, nsk, sk_lo, p_lo, sink, ring;  // ring = cache_len - sink
+  // position sk_lo + i), then the recent positions p_lo + (i - nsk) at their ring slots;
+  // p_mod = (p_lo - sink) mod ring (the recent keys are at most ring)
+  uint32_t nkeys, nsk, sk_lo, p_mod, sink, ring;  // ring = cache_len - sink
   float inv_scale;       // 1 / sqrt(scale_dk)
 };
 
@@ -279,7 +280,8 @@ struct AttnArgs {
 // rows the reference's evict-and-roll keeps (src/attention/cache_ops.rs:64-117), without moving
 // any row (sink = 0: slot p mod cache_len).
 __device__ __forceinline__ uint32_t key_slot(const AttnArgs &a, uint32_t i) {
-  return i < a.nsk ? a.sk_lo + i : a.sink + (a.p_lo - a.sink + (i - a.nsk)) % a.ring;
+  const uint32_t r = a.p_mod + (i - a.nsk);  // < 2 ring: p_mod < ring, i - nsk < ring
+  return i < a.nsk ? a.sk_lo + i : a.sink + (r >= a.ring ? r - a.ring : r);
 }
 
 template <typename KV, uint32_t G>
@@ -441,10 +443,43 @@ __device__ __forceinline__ void raw_vals(const RawQ<uint16_t> &r, float (&v)[4])
 // (key lane kq, dim quad dq) slot of the value phase needs, before waiting for any of them.  Keys
 // past the window and quads past head_dim read a valid slot and are not used.  Same arithmetic
 // order as attn_chunk_kernel.
+// G consecutive floats of LDS (16-byte aligned for G >= 4, 8-byte for G = 2) in the widest
+// accesses that fit.
+template <uint32_t G>
+__device__ __forceinline__ void lds_store_g(float *p, const float (&v)[G]) {
+  if constexpr (G >= 4) {
+#pragma unroll
+    for (uint32_t j = 0; j < G; j += 4u) *(float4 *)(p + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  } else if constexpr (G == 2) {
+    *(float2 *)p = make_float2(v[0], v[1]);
+  } else {
+    p[0] = v[0];
+  }
+}
+template <uint32_t G>
+__device__ __forceinline__ void lds_load_g(const float *p, float (&v)[G]) {
+  if constexpr (G >= 4) {
+#pragma unroll
+    for (uint32_t j = 0; j < G; j += 4u) {
+      const float4 x = *(const float4 *)(p + j);
+      v[j] = x.x;
+      v[j + 1] = x.y;
+      v[j + 2] = x.z;
+      v[j + 3] = x.w;
+    }
+  } else if constexpr (G == 2) {
+    const float2 x = *(const float2 *)p;
+    v[0] = x.x;
+    v[1] = x.y;
+  } else {
+    v[0] = p[0];
+  }
+}
+
 template <typename KV, uint32_t G>
 __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
   __shared__ __align__(16) float q_l[G * 64];
-  __shared__ float e_l[kAttnChunk * G];
+  __shared__ __align__(16) float e_l[kAttnChunk * G];
   __shared__ float m_l[4 * G], l_l[4 * G];
   __shared__ __align__(16) float acc_l[4 * G * 16 * 4];  // [wave][j][dq][4]
   const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
@@ -489,47 +524,70 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
       }
     }
   }
+  // wave maxima and sums of the G heads: lane-0 reductions, the G chains interleaved
+  float red[G];
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) {
     s[j] = valid ? s[j] * a.inv_scale : -INFINITY;
-    const float mw = wave_max(s[j]);
-    if (lane == 0) m_l[w * G + j] = mw;
+    red[j] = s[j];
+  }
+  wave_max_to_lane0_n<(int)G>(red);
+  if (lane == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j) m_l[w * G + j] = red[j];
   }
   __syncthreads();
+  float e[G];
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) {
     const float m = fmaxf(fmaxf(m_l[j], m_l[G + j]), fmaxf(m_l[2u * G + j], m_l[3u * G + j]));
-    const float e = valid ? expf(s[j] - m) : 0.0f;
-    e_l[t * G + j] = e;
-    const float lw = wave_sum_butterfly(e);
-    if (lane == 0) l_l[w * G + j] = lw;
+    e[j] = valid ? expf(s[j] - m) : 0.0f;
+    red[j] = e[j];
+  }
+  lds_store_g<G>(e_l + t * G, e);
+  wave_sum_to_lane0_n<(int)G>(red);
+  if (lane == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j) l_l[w * G + j] = red[j];
   }
   __syncthreads();
   float acc[G][4];
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+  // no branch: keys past the window have e = 0 and their (clamped) value quads are zeroed, so
+  // they add +0; quads past head_dim are never written out
 #pragma unroll
   for (uint32_t i = 0; i < 16u; ++i) {
     const uint32_t key = kq + 16u * i;
-    if (dq < nq && key < nkeys) {
-      float v4[4];
-      raw_vals(vr[i], v4);
+    float v4[4], ek[G];
+    raw_vals(vr[i], v4);
 #pragma unroll
-      for (uint32_t j = 0; j < G; ++j) {
-        const float e = e_l[key * G + j];
-        acc[j][0] = fmaf(e, v4[0], acc[j][0]);
-        acc[j][1] = fmaf(e, v4[1], acc[j][1]);
-        acc[j][2] = fmaf(e, v4[2], acc[j][2]);
-        acc[j][3] = fmaf(e, v4[3], acc[j][3]);
-      }
+    for (int u = 0; u < 4; ++u) v4[u] = key < nkeys ? v4[u] : 0.0f;
+    lds_load_g<G>(e_l + key * G, ek);
+#pragma unroll
+    for (uint32_t j = 0; j < G; ++j) {
+      acc[j][0] = fmaf(ek[j], v4[0], acc[j][0]);
+      acc[j][1] = fmaf(ek[j], v4[1], acc[j][1]);
+      acc[j][2] = fmaf(ek[j], v4[2], acc[j][2]);
+      acc[j][3] = fmaf(ek[j], v4[3], acc[j][3]);
+    }
+  }
+  // the 4 key lanes of the wave (lanes dq, dq + 16, dq + 32, dq + 48): lane dq gets
+  // (a[dq] + a[dq + 16]) + (a[dq + 32] + a[dq + 48]) by permlane swaps
+#pragma unroll
+  for (uint32_t j = 0; j < G; ++j) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[j][u]), __float_as_uint(acc[j][u]), false, false);
+      acc[j][u] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
   }
 #pragma unroll
   for (uint32_t j = 0; j < G; ++j) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 16, 64);
-      acc[j][u] = acc[j][u] + __shfl_xor(acc[j][u], 32, 64);
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j][u]), __float_as_uint(acc[j][u]), false, false);
+      acc[j][u] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
   }
   if (lane < 16u) {
@@ -1347,7 +1405,8 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     aa.nsk = wstart < nsink_rows ? nsink_rows - wstart : 0u;
     aa.sk_lo = wstart;
     const uint32_t nrec = used - std::max(wstart, S < used ? S : used);
-    aa.p_lo = pos + 1 - nrec;
+    const uint32_t p_lo = pos + 1 - nrec;  // first recent position (>= S when nrec > 0)
+    aa.p_mod = nrec ? (p_lo - S) % ring : 0u;
     aa.nkeys = aa.nsk + nrec;
     aa.sink = S;
     aa.ring = ring;

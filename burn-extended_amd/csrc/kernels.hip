@@ -104,34 +104,6 @@ __device__ __forceinline__ void wave_sum_butterfly_n(float (&v)[N]) {
   }
 }
 
-// The same sums as wave_sum_butterfly_n, valid in lane 0 only: the xor-32 and xor-16 levels by
-// permlane swaps, xor 8 by a row rotation (exact), and the xor-4/2/1 levels by a row rotation and
-// quad permutations that pair lane l < 4 with l ^ 4, l ^ 2, l ^ 1 -- every addition lane 0's
-// chain depends on adds the same two values as the butterfly's.
-template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int N>
-__device__ __forceinline__ void wave_sum_to_lane0_n(float (&v)[N]) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
-    v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
-    v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x128>(v[i]);  // row_ror:8
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x124>(v[i]);  // row_ror:4
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0x4E>(v[i]);   // quad_perm [2,3,0,1]
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<0xB1>(v[i]);   // quad_perm [1,0,3,2]
-}
 
 template <typename XT, typename WT, bool VEC>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
@@ -1310,7 +1282,9 @@ __global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
 // scale) and B = the same 8 K positions of token j = lane & 15 from LDS.  The K positions of a
 // step differ per lane group but are identical between A and B, so the product sums every
 // (row, token, k) exactly once.  Output: lane holds C[rows 4q..4q+3][token j].
-// f32 activations are split into NT bf16 terms (NT MFMAs per step).
+// f32 activations are split into NT bf16 terms: NT MFMAs per step, or (NT = 2 and at most 8 rows
+// per token pass) one MFMA whose columns hold both terms -- column c reads B row c, term 1 of token
+// j sits at row mt_max + j -- and the two columns of a token are summed once per tile.
 // ---------------------------------------------------------------------------------------------
 
 // a / b for a < 2^20 and b <= 2^12 given rb = 1.0f / b: the rounding error of (a + 0.5) * rb
@@ -1370,8 +1344,9 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // refills: loads complete in order, so waiting for those never waits for the prefetch.
 // At start-up the B operand's staging loads are issued before the first weight loads for the same
 // reason.  No branch surrounds a weight load.
-template <int NT, bool GATE_UP, typename XT, int SPLIT>
+template <int NT, bool GATE_UP, typename XT, int SPLIT, bool PK>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3))) void expert_gemv_kernel(GemvArgs a) {
+  static_assert(!PK || NT == 2, "packed columns hold two terms");
   static_assert(SPLIT >= 1 && (GATE_UP ? (SPLIT == 1 || SPLIT == (int)kGateUpSplit) : (SPLIT <= (int)kDownSplit || SPLIT == (int)kDownSplitFew)),
                 "K-parts of the units");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1538,6 +1513,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   // next step as soon as its MFMAs have consumed it (so CJ - 1 K-groups stay in flight from one
   // register buffer); at the end of a tile, the epilogue.  Returns false when the wave's steps
   // are done.
+  // PK: both activation terms in the columns of one MFMA (launched with 2 mt_max <= 16; columns
+  // 2 mt_max .. 15 unused)
   auto do_step = [&]() -> bool {
     if (g >= total) return false;
     const uint32_t u = my_first + tstride * ti, rt = unit_rt(u), h = unit_h(u);
@@ -1555,7 +1532,10 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const uint8_t *nwt = last ? (const uint8_t *)(a.bias + (size_t)e * a.bias_estride) : wexp + (size_t)nrt_ * a.nb * 256u;
     const uint8_t *nsp = sexp + (size_t)nrt_ * a.nb * 16u;
     const bool bval = i16 < mt;
-    const uint16_t *brow = bs + (size_t)min(i16, mtm - 1u) * ldk;  // rows >= mt: zeroed at use
+    // B row of this lane's column: token i16, or (packed) term i16 / mt_max of token i16 % mt_max
+    const uint32_t pcol = i16 < mtm ? i16 : i16 - mtm;
+    const bool bcol = PK ? (i16 < 2u * mtm && pcol < mt) : bval;
+    const uint16_t *brow = bs + (size_t)(PK ? min(i16, 2u * mtm - 1u) : min(i16, mtm - 1u)) * ldk;  // zeroed at use
     // few-expert batches (gate_up in K-parts: one or two tokens per expert) read B only in the lanes
     // of present tokens, an exec-masked read (120B T = 1 gate_up 17.7 -> 14.3 us); with more tokens
     // per expert the branches cost more than the skipped reads (20B T = 8 gate_up 37.8 -> 39.2 us)
@@ -1564,7 +1544,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     for (uint32_t j = 0; j < CJ; ++j) {
       const uint32_t kg = kg_of(h, st, j);
       const bool ok = lane_ok(h, kg);
-      const bool bok = bval && ok;
+      const bool bok = bcol && ok;
       const float sc = ok ? e8m0_to_f32((sbuf[j] >> sshift) & 0xFFu) : 1.0f;
       const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
       const uint32_t wd[4] = {abuf[j].x, abuf[j].y, abuf[j].z, abuf[j].w};
@@ -1572,7 +1552,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       for (int s = 0; s < 4; ++s) {
         const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
 #pragma unroll
-        for (int term = 0; term < NT; ++term) {
+        for (int term = 0; term < (PK ? 1 : NT); ++term) {
           const uint16_t *bp = brow + (size_t)term * mtm * ldk + kb + 8u * s;
           u32x4_t raw = {0u, 0u, 0u, 0u};
           if constexpr (kMaskB) {
@@ -1598,6 +1578,10 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     ++g;
     if (++st < nst) return true;
     st = 0;
+    if constexpr (PK) {  // token j's term-1 column (j + mt_max) onto its term-0 column
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] + __shfl(acc[r], (int)(lane + mtm), 64);
+    }
     // epilogue: lane holds rows 4q..4q+3 of tile rt for token column i16
     if constexpr (kInWg) {
       // every wave (a workgroup's waves walk the same tiles): part h's rows, b1 in part 0
@@ -1902,20 +1886,27 @@ hipError_t configure_kernels() {
   BX_ATTR((router_rows_kernel<uint16_t, uint16_t, 2>));
   BX_ATTR((router_rows_kernel<uint16_t, uint16_t, 4>));
   BX_ATTR(dispatch_kernel);
-  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1>));
-  BX_ATTR((expert_gemv_kernel<1, true, float, 1>));
-  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<1, true, float, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<1, false, float, 1>));
-  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit>));
-  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplitFew>));
-  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, 1>));
-  BX_ATTR((expert_gemv_kernel<2, true, float, 1>));
-  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<2, true, float, kGateUpSplit>));
-  BX_ATTR((expert_gemv_kernel<2, false, float, 1>));
-  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplit>));
-  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplitFew>));
+  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, 1, false>));
+  BX_ATTR((expert_gemv_kernel<1, true, float, 1, false>));
+  BX_ATTR((expert_gemv_kernel<1, true, uint16_t, kGateUpSplit, false>));
+  BX_ATTR((expert_gemv_kernel<1, true, float, kGateUpSplit, false>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, 1, false>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplit, false>));
+  BX_ATTR((expert_gemv_kernel<1, false, float, kDownSplitFew, false>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, 1, false>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, 1, false>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, kGateUpSplit, false>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, kGateUpSplit, false>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, 1, false>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplit, false>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplitFew, false>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, 1, true>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, 1, true>));
+  BX_ATTR((expert_gemv_kernel<2, true, uint16_t, kGateUpSplit, true>));
+  BX_ATTR((expert_gemv_kernel<2, true, float, kGateUpSplit, true>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, 1, true>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplit, true>));
+  BX_ATTR((expert_gemv_kernel<2, false, float, kDownSplitFew, true>));
 #undef BX_ATTR
   return err;
 }
@@ -2040,48 +2031,42 @@ hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int NT, bool PK>
+static void launch_gemv_t(const GemvArgs &a, bool gate_up, bool x_bf16, dim3 g, size_t lds, hipStream_t s) {
+  const dim3 block(kGemvThreads);
+  const bool split = !gate_up && a.ksplit > 1u;
+  const bool usplit = gate_up && a.ksplit > 1u;
+  if (split && a.ksplit == kDownSplitFew)
+    (void)launch_kernel(expert_gemv_kernel<NT, false, float, kDownSplitFew, PK>, g, block, lds, s, a);
+  else if (split)
+    (void)launch_kernel(expert_gemv_kernel<NT, false, float, kDownSplit, PK>, g, block, lds, s, a);
+  else if (!gate_up)
+    (void)launch_kernel(expert_gemv_kernel<NT, false, float, 1, PK>, g, block, lds, s, a);
+  else if (usplit && x_bf16)
+    (void)launch_kernel(expert_gemv_kernel<NT, true, uint16_t, kGateUpSplit, PK>, g, block, lds, s, a);
+  else if (usplit)
+    (void)launch_kernel(expert_gemv_kernel<NT, true, float, kGateUpSplit, PK>, g, block, lds, s, a);
+  else if (x_bf16)
+    (void)launch_kernel(expert_gemv_kernel<NT, true, uint16_t, 1, PK>, g, block, lds, s, a);
+  else
+    (void)launch_kernel(expert_gemv_kernel<NT, true, float, 1, PK>, g, block, lds, s, a);
+}
+
 hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uint32_t grid, hipStream_t s) {
   const uint64_t nunits = (uint64_t)a.nrt * (a.ksplit > 1u ? a.ksplit : 1u);
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
-  const dim3 g(grid), block(kGemvThreads);
+  const dim3 g(grid);
   const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
-  const bool split = !gate_up && a.ksplit > 1u;
-  const bool usplit = gate_up && a.ksplit > 1u;
-  if (nt == 1) {
-    if (split && a.ksplit == kDownSplitFew)
-      (void)launch_kernel(expert_gemv_kernel<1, false, float, kDownSplitFew>, g, block, lds, s, a);
-    else if (split)
-      (void)launch_kernel(expert_gemv_kernel<1, false, float, kDownSplit>, g, block, lds, s, a);
-    else if (!gate_up)
-      (void)launch_kernel(expert_gemv_kernel<1, false, float, 1>, g, block, lds, s, a);
-    else if (usplit && x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<1, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
-    else if (usplit)
-      (void)launch_kernel(expert_gemv_kernel<1, true, float, kGateUpSplit>, g, block, lds, s, a);
-    else if (x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<1, true, uint16_t, 1>, g, block, lds, s, a);
-    else
-      (void)launch_kernel(expert_gemv_kernel<1, true, float, 1>, g, block, lds, s, a);
-  } else if (nt == 2) {
-    if (split && a.ksplit == kDownSplitFew)
-      (void)launch_kernel(expert_gemv_kernel<2, false, float, kDownSplitFew>, g, block, lds, s, a);
-    else if (split)
-      (void)launch_kernel(expert_gemv_kernel<2, false, float, kDownSplit>, g, block, lds, s, a);
-    else if (!gate_up)
-      (void)launch_kernel(expert_gemv_kernel<2, false, float, 1>, g, block, lds, s, a);
-    else if (usplit && x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<2, true, uint16_t, kGateUpSplit>, g, block, lds, s, a);
-    else if (usplit)
-      (void)launch_kernel(expert_gemv_kernel<2, true, float, kGateUpSplit>, g, block, lds, s, a);
-    else if (x_bf16)
-      (void)launch_kernel(expert_gemv_kernel<2, true, uint16_t, 1>, g, block, lds, s, a);
-    else
-      (void)launch_kernel(expert_gemv_kernel<2, true, float, 1>, g, block, lds, s, a);
-  } else {
+  if (nt == 1)
+    launch_gemv_t<1, false>(a, gate_up, x_bf16, g, lds, s);
+  else if (nt == 2 && 2u * a.mt_max <= 16u)  // both terms in one MFMA's columns
+    launch_gemv_t<2, true>(a, gate_up, x_bf16, g, lds, s);
+  else if (nt == 2)
+    launch_gemv_t<2, false>(a, gate_up, x_bf16, g, lds, s);
+  else
     return hipErrorInvalidValue;
-  }
   return hipGetLastError();
 }
 

@@ -61,6 +61,45 @@ __device__ __forceinline__ float wave_sum_butterfly(float p) {
   return p;
 }
 
+// Reductions of N values at once over the 64 lanes of a wave, valid in lane 0 only, without an LDS
+// round trip: the xor-32 and xor-16 levels by permlane swaps, xor 8 by a row rotation (exact), and
+// the xor-4/2/1 levels by a row rotation and quad permutations that pair lane l < 4 with l ^ 4,
+// l ^ 2, l ^ 1 -- every operation lane 0's chain depends on combines the same two values, in the
+// same operand order, as the butterfly's (so lane 0 ends with the butterfly's bits).  The N chains
+// are interleaved level by level.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int N, typename Op>
+__device__ __forceinline__ void wave_reduce_to_lane0_n(float (&v)[N], Op op) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+    v[i] = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+    v[i] = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x128>(v[i]));  // row_ror:8
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x124>(v[i]));  // row_ror:4
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x4E>(v[i]));   // quad_perm [2,3,0,1]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0xB1>(v[i]));   // quad_perm [1,0,3,2]
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_to_lane0_n(float (&v)[N]) {
+  wave_reduce_to_lane0_n(v, [](float a, float b) { return a + b; });
+}
+template <int N>
+__device__ __forceinline__ void wave_max_to_lane0_n(float (&v)[N]) {
+  wave_reduce_to_lane0_n(v, [](float a, float b) { return fmaxf(a, b); });
+}
+
 // Packed top-k key with the same strict total order as `beats`: a beats b iff key(a) > key(b)
 // (unsigned).  High word: order-preserving map of the float with NaN -> 0 (lowest) and -0 -> +0;
 // low word: ~index, so equal values rank the lower index first.
