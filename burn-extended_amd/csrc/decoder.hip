@@ -10,7 +10,8 @@
 //                       rolling cache at slot pos mod cache_len
 //     attn_chunk_kernel one query row per head against 256 cached keys per workgroup: chunk
 //                       maximum, exp, sums and the weighted value sum (flash-decoding split)
-//     attn_combine_kernel  chunks merged with the learned sink in the softmax denominator
+//     attn_combine_kernel  chunks merged with the learned sink in the softmax denominator (a layer
+//                       whose window is one chunk merges it in the attention launch itself)
 //     dense_gemv_kernel the output projection; o_post_kernel hidden += sum + bias (where the MoE
 //                       router cannot: router_front_kernel forms that row itself for decode batches)
 //     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels;
@@ -273,6 +274,10 @@ struct AttnArgs {
   // p_mod = (p_lo - sink) mod ring (the recent keys are at most ring)
   uint32_t nkeys, nsk, sk_lo, p_mod, sink, ring;  // ring = cache_len - sink
   float inv_scale;       // 1 / sqrt(scale_dk)
+  // one chunk (attn_chunk64_kernel only): the sink merge in the same launch, ctx written directly
+  // (null: the chunk partials go to part for attn_combine_kernel)
+  float *ctx;            // [B][nH * dk]
+  const float *sinks;    // [nH] or null
 };
 
 // Cache slot of key i of the active window.  The cache keeps the first `sink` positions in slots
@@ -596,6 +601,30 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
       *(float4 *)(acc_l + ((w * G + j) * 16u + dq) * 4u) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
   }
   __syncthreads();
+  if (a.ctx != nullptr) {
+    // the only chunk: attn_combine_kernel's arithmetic for one chunk -- M = max(sink, m),
+    // f = exp(m - M), 1 / L = 1 / (l f + exp(sink - M)), ctx = (acc f) (1 / L)
+    for (uint32_t i = t; i < G * 16u; i += blockDim.x) {
+      const uint32_t j = i >> 4, dd = i & 15u;
+      if (dd >= nq) continue;
+      float4 r = *(const float4 *)(acc_l + (j * 16u + dd) * 4u);
+#pragma unroll
+      for (uint32_t w2 = 1; w2 < 4u; ++w2) {
+        const float4 v = *(const float4 *)(acc_l + ((w2 * G + j) * 16u + dd) * 4u);
+        r = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+      }
+      const float m = fmaxf(fmaxf(m_l[j], m_l[G + j]), fmaxf(m_l[2u * G + j], m_l[3u * G + j]));
+      const float l = (l_l[j] + l_l[G + j]) + (l_l[2u * G + j] + l_l[3u * G + j]);
+      const float sink = a.sinks ? a.sinks[g * G + j] : -INFINITY;
+      const float M = fmaxf(sink, m);
+      const float f = expf(m - M);
+      const float rinv = 1.0f / (__fmul_rn(l, f) + (a.sinks ? expf(sink - M) : 0.0f));
+      float *dst = a.ctx + (size_t)b * a.nH * dk + (size_t)(g * G + j) * dk + 4u * dd;
+      *(float4 *)dst = make_float4(__fmul_rn(r.x, f) * rinv, __fmul_rn(r.y, f) * rinv, __fmul_rn(r.z, f) * rinv,
+                                   __fmul_rn(r.w, f) * rinv);
+    }
+    return;
+  }
   float *out = a.part + (((size_t)b * a.kvH + g) * a.nchunk + c) * (size_t)G * (dk + 2u);
   for (uint32_t i = t; i < G * 16u; i += blockDim.x) {
     const uint32_t j = i >> 4, dd = i & 15u;
@@ -1021,8 +1050,14 @@ burnext_status dense_gemv(const DenseMat &m, const float *x, uint32_t B, float *
                    "dense GEMV launch");
 }
 
+// the shapes attn_chunk64_kernel serves (the only attention kernel that merges a single chunk itself)
+bool attn_direct_ok(uint32_t dk, uint32_t groups) {
+  return dk <= 64u && (groups == 1u || groups == 2u || groups == 4u || groups == 8u);
+}
+
 template <typename KV>
 hipError_t launch_attention_kv(uint32_t groups, dim3 grid, hipStream_t s, const AttnArgs &a) {
+  if (a.ctx != nullptr && !attn_direct_ok(a.dk, groups)) return hipErrorInvalidValue;
   if (a.dk <= 64u) {  // one memory round trip per chunk
     switch (groups) {
       case 1: return launch_kernel(attn_chunk64_kernel<KV, 1>, grid, dim3(256), 0, s, a);
@@ -1412,14 +1447,21 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     aa.ring = ring;
     aa.nchunk = (uint32_t)cdiv(aa.nkeys, kAttnChunk);
     aa.inv_scale = 1.0f / std::sqrt(c.scale_dk);
+    const float *sinks_l = M->sinks ? M->sinks + (size_t)l * c.n_heads : nullptr;
+    // a single chunk (windowed layers) merges the sink in the attention launch itself
+    const bool direct = aa.nchunk == 1 && attn_direct_ok(dk, M->groups);
+    if (direct) {
+      aa.ctx = ctx;
+      aa.sinks = sinks_l;
+    }
     const dim3 agrid(aa.nchunk, c.kv_heads, B);
     st = hip_check(launch_attention(c.kv_bf16 != 0, M->groups, agrid, s, aa), "attention launch");
     if (st != BURNEXT_OK) return st;
-    CombineAttnArgs ca{attn, M->sinks ? M->sinks + (size_t)l * c.n_heads : nullptr, ctx, c.n_heads, c.kv_heads, dk,
-                       aa.nchunk};
-    st = hip_check(launch_kernel(attn_combine_kernel, dim3(c.kv_heads, B), dim3(256),
-                                 (size_t)(aa.nchunk + 1) * M->groups * 4, s, ca),
-                   "attention combine launch");
+    CombineAttnArgs ca{attn, sinks_l, ctx, c.n_heads, c.kv_heads, dk, aa.nchunk};
+    if (!direct)
+      st = hip_check(launch_kernel(attn_combine_kernel, dim3(c.kv_heads, B), dim3(256),
+                                   (size_t)(aa.nchunk + 1) * M->groups * 4, s, ca),
+                     "attention combine launch");
     if (st == BURNEXT_OK) st = dense_gemv(M->wo[l], ctx, B, part, s);
     if (st != BURNEXT_OK) return st;
     // the MoE layer; its combine also writes the next norm of the new hidden rows (the next
