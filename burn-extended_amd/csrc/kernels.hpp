@@ -70,6 +70,18 @@ struct TopkArgs {
 // j-th segment entry, for j < min(M, kRecTokens).
 constexpr uint32_t kRecWords = 32;
 constexpr uint32_t kRecTokens = 14;
+constexpr uint32_t kMaxTopK = 32;
+constexpr uint32_t kMaxExperts = 256;
+constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: routing by one workgroup
+
+// Output pointers of the small-batch routing (top-k, softmax, dispatch, records); all null: none
+// written (the routing goes to LDS only).
+struct RouteOut {
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;
+};
 
 struct DispatchArgs {
   const int32_t *topk_idx;
@@ -110,6 +122,14 @@ struct GemvArgs {
   // tiles, the workgroup sums the parts in order (bias in part 0) and writes the SwiGLU rows
   uint32_t ksplit;
   uint64_t out_half;
+  // gate_up of a decode-sized batch with the routing in the same launch (route_lg not null): every
+  // workgroup computes the top-k and dispatch of the route_T tokens from their logits
+  // [route_T, route_E] into an LDS record table (up to kSmallRouteMaxTokens tokens per record);
+  // workgroup 0 also writes the routing outputs rout for the down projection and the combine
+  // (seg_off, active, num_active, perm and exrec above are then unused by this launch)
+  const float *route_lg;
+  uint32_t route_T, route_E;
+  RouteOut rout;
 };
 
 // Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,
@@ -247,22 +267,45 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
 }
-// B staging (which first holds the record table), the chosen record and the per-token row index.
-__host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
-  const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = 4u * (size_t)nrec * 32u;
+// Routing in the gate_up launch (route_E experts, route_wg_lds): the stage area first holds the
+// LDS record table [nrec][kRecWords], then the key words [kSmallRouteMaxTokens][route_E], the rank
+// bytes [route_E][kSmallRouteMaxTokens], the selected logits [kSmallRouteMaxTokens][kMaxTopK], the
+// counts [route_E], the scan totals [16] and the active count.
+__host__ __device__ inline size_t gemv_route_bytes(uint32_t nrec, uint32_t route_E) {
+  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)kSmallRouteMaxTokens * route_E +
+         (size_t)route_E * kSmallRouteMaxTokens + 4u * (size_t)kSmallRouteMaxTokens * kMaxTopK + 4u * (size_t)route_E +
+         4u * 16u + 16u;
+}
+// Routing in the gate_up launch (route_wg_lds) where it pays: at most 64 key comparisons per
+// thread.  Measured per workgroup, its prologue costs about 3 us at E = 32 (T = 8), against the
+// routing launch's 4.9 us, and 5.4 us at E = 128 (T = 1: 128 comparisons per thread), against
+// about 4.5 us.
+__host__ __device__ inline bool route_in_gate_up_ok(uint64_t T, uint32_t E, uint32_t K) {
+  return T >= 1 && T <= kSmallRouteMaxTokens && E <= kMaxExperts && K <= E && K <= kMaxTopK &&
+         (T * E + 255u) / 256u * E <= 64u;
+}
+// B staging (which first holds the record table, or with route_E > 0 the routing of the launch),
+// the chosen record and the per-token row index.
+__host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
+                                                   uint32_t route_E = 0) {
+  const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = route_E ? gemv_route_bytes(nrec, route_E) : 4u * (size_t)nrec * 32u;
   return b > t ? b : t;
 }
-__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
-  return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 4u * (size_t)mt_max + 16u;
+__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
+                                                       uint32_t route_E = 0) {
+  return gemv_stage_bytes(nt, mt_max, nb, nrec, route_E) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
 // gate_up in K-parts (kGateUpSplit waves of a workgroup per row tile): the parts' tile results
 // meet in LDS after the other regions, [tile parity][wave][lane] x 4 floats
 constexpr size_t kGemvRedBytes = 2u * 4u * 64u * 16u;
-__host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
-  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec) + 15u) & ~(size_t)15u;
+__host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
+                                                  uint32_t route_E = 0) {
+  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E) + 15u) & ~(size_t)15u;
 }
-__host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red) {
-  return red ? gemv_red_offset(nt, mt_max, nb, nrec) + kGemvRedBytes : gemv_total_lds_bytes(nt, mt_max, nb, nrec);
+__host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red,
+                                                        uint32_t route_E = 0) {
+  return red ? gemv_red_offset(nt, mt_max, nb, nrec, route_E) + kGemvRedBytes
+             : gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E);
 }
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
@@ -285,9 +328,6 @@ constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert G
 // waves idle (one part per wave of a workgroup, summed in LDS before the SwiGLU epilogue)
 constexpr uint32_t kGateUpSplit = 4;
 constexpr uint32_t kDownSplitFew = 4;  // K-parts per down row tile for the same batches
-constexpr uint32_t kMaxTopK = 32;
-constexpr uint32_t kMaxExperts = 256;
-constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
 // router_rows_kernel: D % 8 == 0 and D, Dp (with xn) and xq.kq (with xq) <= 512 * kFrontChunks,

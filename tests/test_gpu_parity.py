@@ -175,9 +175,10 @@ def test_route_small_ties_nan_signed_zero(M, oracle, E, K, n):
                                            (256, 2, 2, 16, "f32"), (200, 7, 3, 13, "f32"), (2880, 32, 4, 64, "bf16"),
                                            (2880, 128, 4, 1100, "bf16")])
 def test_route_dispatch_as_forward(M, oracle, D, E, K, n, dtype):
-    """Routing + dispatch exactly as the forward runs them (n <= 16: the fused one-workgroup kernel;
-    above: top-k then dispatch): indices, weights, segment offsets and the entry list against the
-    oracle's top-k and counting sort."""
+    """Routing + dispatch by the forward's routing kernels (n <= 16: the one-workgroup kernel, which
+    the forward runs where the routing does not go into its gate_up launch; above: top-k then
+    dispatch): indices, weights, segment offsets and the entry list against the oracle's top-k and
+    counting sort."""
     from burnext_amd import synth
     print(f"route+dispatch D={D} E={E} K={K} n={n} {dtype}", flush=True)
     L = _make(synth, D, 64, E, K, seed=21, dtype=dtype, with_gamma=True)
@@ -227,6 +228,32 @@ def _forward_case(M, oracle, L, x, dtype, flags=3, layout=None):
     assert np.array_equal(ridx.cpu().numpy(), idx_ref)
     layer.close()
     return _np(y), y_ref
+
+
+@pytest.mark.parametrize("E,K,n", [(32, 4, 8), (32, 4, 16), (64, 4, 1), (48, 5, 5), (7, 3, 13), (130, 6, 1),
+                                   (128, 4, 16)])
+def test_forward_routing_ties(M, oracle, E, K, n):
+    """Decode-sized forwards whose router logits are ties, a NaN, -0 and +0 (router weights zero,
+    biases chosen, so every token routes alike and a selected expert gets all n tokens): the first
+    five cases route inside the gate_up launch (every workgroup ranks the (token, expert) pairs
+    itself), the last two run the routing kernel.  A wrong selection, order or weight would change
+    y, which is checked against oracle.moe_forward (NaN lowest, -0 == +0, equal values by lower
+    index)."""
+    from burnext_amd import synth
+    print(f"forward routing ties E={E} K={K} n={n}", flush=True)
+    L = _make(synth, 64, 32, E, K, seed=23, dtype="f32")
+    L.router_w_f32[:] = 0.0
+    b = np.full(E, 0.5, np.float32)
+    for e_, v in ((E - 1, 2.0), (0, 1.0), (min(63, E - 1), 1.0), (min(64, E - 1), 1.0), (E // 2, 0.75),
+                  (E // 3, 0.75), (7 % E, -0.0), (8 % E, 0.0), ((E * 3) // 4, np.nan)):
+        b[e_] = v
+    L.router_b_f32[:] = b
+    x = synth.make_tokens(n, 64, seed=24, dtype="f32")
+    y, y_ref = _forward_case(M, oracle, L, x, "f32")
+    err = oracle.max_abs_rel(y, y_ref)
+    print(f"  max-abs-rel {err:.3e}")
+    assert np.isfinite(y).all()
+    assert err <= TOL_F32
 
 
 @pytest.mark.parametrize("layout", ["interleaved", "halves"])
@@ -514,8 +541,8 @@ def test_moe_basic_zero_weights_residual(M):
     (640, 640, 8, 2, 1, "bf16"),      # 5 K-groups: the last gate_up / down K-part is empty
 ])
 def test_forward_gate_up_k_split(M, oracle, D, F, E, K, n, dtype):
-    """Decode batches touching few experts: gate_up writes K-part pre-activations and a separate
-    kernel sums them (in order) and applies the clamped SwiGLU."""
+    """Decode batches touching few experts: the 4 waves of a gate_up workgroup take the 4 K-parts of
+    its row tiles, the workgroup sums them (in order) and applies the clamped SwiGLU."""
     from burnext_amd import synth
     L = _make(synth, D, F, E, K, seed=13, dtype=dtype, with_gamma=True)
     x = synth.make_tokens(n, D, seed=14, dtype=dtype)
