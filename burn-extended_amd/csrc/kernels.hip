@@ -1075,14 +1075,14 @@ __device__ __forceinline__ void route_small_dispatch(uint32_t T, uint32_t E, uin
 // pointers: not written); lrec receives the LDS record table with every token of a record
 // ([4 + j], j < M <= T).  Returns the number of active experts.  Every thread must call it.
 // LDS at lds (gemv_route_bytes past the table): key high words [T * E], rank bytes [E][16],
-// selected logits [16][kMaxTopK], counts [E], scan totals [16], active count.
+// selected logits [T][kMaxTopK], counts [E], scan totals [16], active count.
 __device__ __forceinline__ uint32_t route_wg_lds(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
                                                  unsigned char *lds, int32_t *lrec) {
   const uint32_t tid = threadIdx.x, nthr = blockDim.x, TE = T * E;
   uint32_t *kh = (uint32_t *)lds;
-  int8_t *rank = (int8_t *)(kh + kSmallRouteMaxTokens * E);
+  int8_t *rank = (int8_t *)(kh + T * E);
   float *selv = (float *)(rank + E * kSmallRouteMaxTokens);
-  int32_t *cnt_l = (int32_t *)(selv + kSmallRouteMaxTokens * kMaxTopK);
+  int32_t *cnt_l = (int32_t *)(selv + T * kMaxTopK);
   int32_t *tot_l = cnt_l + E;
   int32_t *na_l = tot_l + 16;
   for (uint32_t i = tid; i < TE; i += nthr) kh[i] = (uint32_t)(topk_key(lg[i], 0u) >> 32);
@@ -1476,7 +1476,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t mtm = a.mt_max;
   uint16_t *bs = (uint16_t *)smem;
   const bool lroute = GATE_UP && a.route_lg != nullptr;  // the routing in this launch
-  int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec, lroute ? a.route_E : 0u));  // [kRecWords]
+  int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec, lroute ? a.route_E : 0u,
+                                                       a.route_T));  // [kRecWords]
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
   const uint32_t nrt = a.nrt;
   // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
@@ -1484,6 +1485,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   constexpr bool kInWg = GATE_UP && SPLIT > 1;    // K-parts of a row tile on the 4 waves of a workgroup
   static_assert(!kInWg || SPLIT == 4, "one K-part per wave");
   const uint32_t nunits = kInWg ? nrt : nrt * nsplit;
+  const uint32_t k8n = Kp >> 3;
+  const float rk8n = 1.0f / (float)k8n;
+  unsigned char *tbl = smem;  // the record table (or the routing of the launch), in the B area
   // one round trip: num_active and the record table (the table is staged through the B area), or
   // the batch's logits, routed here into the same table
   uint32_t na = 0;
@@ -1491,13 +1495,13 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     if (lroute) {
       const RouteOut none{};
       na = route_wg_lds(a.route_lg, a.route_T, a.route_E, a.topk, blockIdx.x == 0 ? a.rout : none,
-                        smem + 4u * a.nrec * kRecWords, (int32_t *)smem);
+                        tbl + 4u * a.nrec * kRecWords, (int32_t *)tbl);
     }
   }
   if (!lroute) {
     na = (uint32_t)*a.num_active;
     const uint4 *src = (const uint4 *)a.exrec;
-    uint4 *dst = (uint4 *)smem;
+    uint4 *dst = (uint4 *)tbl;
     const uint32_t nv = a.nrec * (kRecWords / 4u);
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
@@ -1517,7 +1521,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     ntw = (nunits - lo + wpe - 1u) / wpe;
   }
   __syncthreads();
-  const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
+  const int32_t *rec0 = (const int32_t *)tbl + ai * kRecWords;  // valid until the first staging
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
   const int e = rec0[0];
   const int seg0 = rec0[1];
@@ -1564,7 +1568,6 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   // true K.  Rows: gate_up the routed tokens' xn rows, down the segment's act rows (both
   // [*, Kp] in XT).  `first_loads` runs once, after the first batch's global loads are issued.
   uint32_t mt = 0, m0 = 0;
-  const float rk8n = 1.0f / (float)(Kp >> 3);
   auto stage = [&](uint32_t pass_, auto &&first_loads) {
     m0 = pass_ * mtm;
     mt = min(mtm, (uint32_t)M - m0);
@@ -1586,7 +1589,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
     constexpr int SB = NT == 1 ? 3 : 2;
     const XT *src = (const XT *)a.brows;
-    const uint32_t k8n = Kp >> 3, nitm = mt * k8n;
+    const uint32_t nitm = mt * k8n;
     bool first = true;
     for (uint32_t base = threadIdx.x; base < nitm; base += SB * blockDim.x) {
       Chunk8<XT> cx[SB];
@@ -1632,7 +1635,8 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t my_first = kInWg ? lo + wv * nrt : lo + us * wv, tstride = kInWg ? us : 4u * us;
   const uint32_t my_tiles = kInWg ? ntw : (wv < ntw ? (ntw - wv + 3u) / 4u : 0u);
   const uint32_t first_c = kInWg ? my_first : min(my_first, nunits - 1u);
-  float *red = (float *)(smem + gemv_red_offset(NT, mtm, a.nb, a.nrec));  // kInWg: [2][4][64][4]
+  float *red = (float *)(smem + gemv_red_offset(NT, mtm, a.nb, a.nrec, lroute ? a.route_E : 0u,
+                                                a.route_T));  // kInWg: [2][4][64][4]
   uint32_t parity = 0;
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
   uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
@@ -2191,7 +2195,7 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
                      a.nrec < std::min(a.route_E, a.route_T * a.topk)))
     return hipErrorInvalidValue;
   const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u,
-                                           a.route_lg ? a.route_E : 0u);
+                                           a.route_lg ? a.route_E : 0u, a.route_T);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
   if (nt == 1)

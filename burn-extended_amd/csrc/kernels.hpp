@@ -267,14 +267,13 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
 }
-// Routing in the gate_up launch (route_E experts, route_wg_lds): the stage area first holds the
-// LDS record table [nrec][kRecWords], then the key words [kSmallRouteMaxTokens][route_E], the rank
-// bytes [route_E][kSmallRouteMaxTokens], the selected logits [kSmallRouteMaxTokens][kMaxTopK], the
-// counts [route_E], the scan totals [16] and the active count.
-__host__ __device__ inline size_t gemv_route_bytes(uint32_t nrec, uint32_t route_E) {
-  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)kSmallRouteMaxTokens * route_E +
-         (size_t)route_E * kSmallRouteMaxTokens + 4u * (size_t)kSmallRouteMaxTokens * kMaxTopK + 4u * (size_t)route_E +
-         4u * 16u + 16u;
+// Routing in the gate_up launch (route_E experts, route_T tokens, route_wg_lds): the LDS record
+// table [nrec][kRecWords], then the key words [route_T][route_E], the rank bytes
+// [route_E][kSmallRouteMaxTokens], the selected logits [route_T][kMaxTopK], the counts [route_E],
+// the scan totals [16] and the active count.
+__host__ __device__ inline size_t gemv_route_bytes(uint32_t nrec, uint32_t route_E, uint32_t route_T) {
+  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)route_T * route_E + (size_t)route_E * kSmallRouteMaxTokens +
+         4u * (size_t)route_T * kMaxTopK + 4u * (size_t)route_E + 4u * 16u + 16u;
 }
 // Routing in the gate_up launch (route_wg_lds) where it pays: at most 64 key comparisons per
 // thread.  Measured per workgroup, its prologue costs about 3 us at E = 32 (T = 8), against the
@@ -287,25 +286,27 @@ __host__ __device__ inline bool route_in_gate_up_ok(uint64_t T, uint32_t E, uint
 // B staging (which first holds the record table, or with route_E > 0 the routing of the launch),
 // the chosen record and the per-token row index.
 __host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                   uint32_t route_E = 0) {
-  const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = route_E ? gemv_route_bytes(nrec, route_E) : 4u * (size_t)nrec * 32u;
+                                                   uint32_t route_E = 0, uint32_t route_T = 0) {
+  const size_t b = gemv_lds_bytes(nt, mt_max, nb);
+  const size_t t = route_E ? gemv_route_bytes(nrec, route_E, route_T) : 4u * (size_t)nrec * kRecWords;
   return b > t ? b : t;
 }
 __host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                       uint32_t route_E = 0) {
-  return gemv_stage_bytes(nt, mt_max, nb, nrec, route_E) + 4u * 32u + 4u * (size_t)mt_max + 16u;
+                                                       uint32_t route_E = 0, uint32_t route_T = 0) {
+  return gemv_stage_bytes(nt, mt_max, nb, nrec, route_E, route_T) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
 // gate_up in K-parts (kGateUpSplit waves of a workgroup per row tile): the parts' tile results
 // meet in LDS after the other regions, [tile parity][wave][lane] x 4 floats
 constexpr size_t kGemvRedBytes = 2u * 4u * 64u * 16u;
+// (the kernel places red at the same offset: route_E / route_T as launched)
 __host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                  uint32_t route_E = 0) {
-  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E) + 15u) & ~(size_t)15u;
+                                                  uint32_t route_E = 0, uint32_t route_T = 0) {
+  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E, route_T) + 15u) & ~(size_t)15u;
 }
 __host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red,
-                                                        uint32_t route_E = 0) {
-  return red ? gemv_red_offset(nt, mt_max, nb, nrec, route_E) + kGemvRedBytes
-             : gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E);
+                                                        uint32_t route_E = 0, uint32_t route_T = 0) {
+  return red ? gemv_red_offset(nt, mt_max, nb, nrec, route_E, route_T) + kGemvRedBytes
+             : gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E, route_T);
 }
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 

@@ -317,7 +317,8 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up, b
     }
   mt = (uint32_t)std::min<uint64_t>(mt, n);
   c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
-  const size_t lds = gemv_launch_lds_bytes(nt, c.mt, t.nb, c.nrec, gate_up && gate_up_split(L, n), lroute ? L.E : 0u);
+  const size_t lds = gemv_launch_lds_bytes(nt, c.mt, t.nb, c.nrec, gate_up && gate_up_split(L, n), lroute ? L.E : 0u,
+                                           lroute ? (uint32_t)n : 0u);
   const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, (160 * 1024) / std::max<size_t>(lds, 1)));
   c.grid = (uint32_t)std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L.num_cus * per_cu, max_active * t.nrt));
   return c;
