@@ -96,10 +96,11 @@ __device__ __forceinline__ void kv_load8(const KV *p, float (&v)[8]) {
   }
 }
 
+// Maximum over the 64 lanes of a wave, in every lane (every lane active): lane 0's chain, broadcast.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  float r[1] = {v};
+  wave_max_to_lane0_n<1>(r);
+  return lane0_broadcast(r[0]);
 }
 
 // Cache layouts of one layer (cap_p = cache_len rounded up to 64 rows).

@@ -95,13 +95,12 @@ __device__ __forceinline__ uint32_t tpos_inv(uint32_t q) { return (q & ~511u) | 
 // ---------------------------------------------------------------------------------------------
 size_t router_lds_bytes(uint32_t tb, uint32_t Dpad) { return sizeof(float) * ((size_t)tb * Dpad + 8); }
 
+// N butterfly sums at once (wave_sum_butterfly's bits in every lane; every lane active)
 template <int N>
 __device__ __forceinline__ void wave_sum_butterfly_n(float (&v)[N]) {
+  wave_sum_to_lane0_n<N>(v);
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = v[i] + __shfl_xor(v[i], off, 64);
-  }
+  for (int i = 0; i < N; ++i) v[i] = lane0_broadcast(v[i]);
 }
 
 

@@ -53,13 +53,6 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t (&t)[NT]) {
   }
 }
 
-// Butterfly sum over the 64 lanes of a wave: after step `off` lane l holds p[l] + p[l ^ off].
-// IEEE addition is commutative, so all lanes finish with the same bits.
-__device__ __forceinline__ float wave_sum_butterfly(float p) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) p = p + __shfl_xor(p, off, 64);
-  return p;
-}
 
 // Reductions of N values at once over the 64 lanes of a wave, valid in lane 0 only, without an LDS
 // round trip: the xor-32 and xor-16 levels by permlane swaps, xor 8 by a row rotation (exact), and
@@ -98,6 +91,19 @@ __device__ __forceinline__ void wave_sum_to_lane0_n(float (&v)[N]) {
 template <int N>
 __device__ __forceinline__ void wave_max_to_lane0_n(float (&v)[N]) {
   wave_reduce_to_lane0_n(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ float lane0_broadcast(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+
+// Sum over the 64 lanes of a wave, in every lane, with the bits of the xor butterfly (after step
+// `off` = 32 .. 1 lane l holds p[l] + p[l ^ off]; IEEE addition is commutative, so every lane
+// finishes with lane 0's bits): lane 0's chain (wave_sum_to_lane0_n), broadcast from lane 0.
+// Every lane of the wave must be active.
+__device__ __forceinline__ float wave_sum_butterfly(float p) {
+  float v[1] = {p};
+  wave_sum_to_lane0_n<1>(v);
+  return lane0_broadcast(v[0]);
 }
 
 // Packed top-k key with the same strict total order as `beats`: a beats b iff key(a) > key(b)
