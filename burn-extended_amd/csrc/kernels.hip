@@ -1068,35 +1068,53 @@ __device__ __forceinline__ void route_small_dispatch(uint32_t T, uint32_t E, uin
 // with route_small_body's results.  Thread i takes the (token, expert) pairs (t, e) = (i / E,
 // i mod E), i += 256: the expert's rank among the token's E keys is the number of keys that beat
 // it (the topk_key order; keys are unique, so the ranks are a permutation and those below K are
-// route_small_body's selection, rank 0 first).  Thread e < E then counts expert e's tokens,
+// route_small_body's selection, rank 0 first); with fewer pairs than threads, S = 2, 4 or 8
+// adjacent lanes share a pair (lane s compares key quads s, s + S, ... read 16 bytes at a time; the
+// key rows are padded to whole quads with zero keys, which beat no real key) and add their counts
+// by DPP.  Thread e < E then counts expert e's tokens,
 // expert_prefix scans the counts and the active flags over the experts, and thread e writes
 // expert e's record and segment entries (earlier tokens first).  Global outputs o (null
 // pointers: not written); lrec receives the LDS record table with every token of a record
 // ([4 + j], j < M <= T).  Returns the number of active experts.  Every thread must call it.
-// LDS at lds (gemv_route_bytes past the table): key high words [T * E], rank bytes [E][16],
-// selected logits [T][kMaxTopK], counts [E], scan totals [16], active count.
+// LDS at lds (gemv_route_bytes past the table): key high words [T][E rounded up to 4], rank bytes
+// [E][16], selected logits [T][kMaxTopK], counts [E], scan totals [16], active count.
 __device__ __forceinline__ uint32_t route_wg_lds(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
                                                  unsigned char *lds, int32_t *lrec) {
-  const uint32_t tid = threadIdx.x, nthr = blockDim.x, TE = T * E;
+  const uint32_t tid = threadIdx.x, nthr = blockDim.x, TE = T * E, Ep = (E + 3u) & ~3u;
   uint32_t *kh = (uint32_t *)lds;
-  int8_t *rank = (int8_t *)(kh + T * E);
+  int8_t *rank = (int8_t *)(kh + T * Ep);
   float *selv = (float *)(rank + E * kSmallRouteMaxTokens);
   int32_t *cnt_l = (int32_t *)(selv + T * kMaxTopK);
   int32_t *tot_l = cnt_l + E;
   int32_t *na_l = tot_l + 16;
-  for (uint32_t i = tid; i < TE; i += nthr) kh[i] = (uint32_t)(topk_key(lg[i], 0u) >> 32);
+  const float rE = 1.0f / (float)E, rEp = 1.0f / (float)Ep, rK = 1.0f / (float)K;
+  for (uint32_t i = tid; i < T * Ep; i += nthr) {
+    const uint32_t t = div_small(i, rEp), e = i - t * Ep;
+    kh[i] = e < E ? (uint32_t)(topk_key(lg[t * E + e], 0u) >> 32) : 0u;
+  }
   __syncthreads();
-  const float rE = 1.0f / (float)E, rK = 1.0f / (float)K;
+  const uint32_t S = route_lanes_per_pair(TE), ls = tid & (S - 1u), per_round = nthr / S;
 #pragma unroll 1
-  for (uint32_t i = tid; i < TE; i += nthr) {
-    const uint32_t t = div_small(i, rE), e = i - t * E, h = kh[i];
-    const uint32_t *row = kh + t * E;
+  for (uint32_t i0 = 0; i0 < TE; i0 += per_round) {  // the same trip count in every lane
+    const uint32_t i = i0 + tid / S, ic = min(i, TE - 1u);
+    const uint32_t t = div_small(ic, rE), e = ic - t * E, h = kh[t * Ep + e];
+    const uint4 *row = (const uint4 *)(kh + t * Ep);
     uint32_t r = 0;  // keys above (h, ~e): a larger high word, or the same one at a lower index
-#pragma unroll 8
-    for (uint32_t e2 = 0; e2 < E; ++e2) {
-      const uint32_t h2 = row[e2];
-      r += (h2 > h || (h2 == h && e2 < e)) ? 1u : 0u;
+#pragma unroll 4
+    for (uint32_t qd = ls; qd < Ep / 4u; qd += S) {
+      const uint4 k4 = row[qd];
+      const uint32_t e2 = 4u * qd;
+      r += (k4.x > h || (k4.x == h && e2 < e)) ? 1u : 0u;
+      r += (k4.y > h || (k4.y == h && e2 + 1u < e)) ? 1u : 0u;
+      r += (k4.z > h || (k4.z == h && e2 + 2u < e)) ? 1u : 0u;
+      r += (k4.w > h || (k4.w == h && e2 + 3u < e)) ? 1u : 0u;
     }
+    // the S lanes of the pair (adjacent, every lane active): lane ^ 1, lane ^ 2, then the mirror
+    // in each 8 (after the first two steps the quads are uniform)
+    if (S >= 2u) r += dpp_u<0xB1>(r);   // quad_perm [1,0,3,2]
+    if (S >= 4u) r += dpp_u<0x4E>(r);   // quad_perm [2,3,0,1]
+    if (S >= 8u) r += dpp_u<0x141>(r);  // row_half_mirror
+    if (i >= TE || ls != 0u) continue;
     rank[e * kSmallRouteMaxTokens + t] = r < K ? (int8_t)r : (int8_t)-1;
     if (r < K) {
       selv[t * kMaxTopK + r] = lg[i];

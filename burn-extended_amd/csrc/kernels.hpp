@@ -272,16 +272,21 @@ __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32
 // [route_E][kSmallRouteMaxTokens], the selected logits [route_T][kMaxTopK], the counts [route_E],
 // the scan totals [16] and the active count.
 __host__ __device__ inline size_t gemv_route_bytes(uint32_t nrec, uint32_t route_E, uint32_t route_T) {
-  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)route_T * route_E + (size_t)route_E * kSmallRouteMaxTokens +
-         4u * (size_t)route_T * kMaxTopK + 4u * (size_t)route_E + 4u * 16u + 16u;
+  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)route_T * ((route_E + 3u) & ~3u) +
+         (size_t)route_E * kSmallRouteMaxTokens + 4u * (size_t)route_T * kMaxTopK + 4u * (size_t)route_E + 4u * 16u + 16u;
+}
+// Lanes per (token, expert) pair of route_wg_lds: 1, 2, 4 or 8, as many as 256 threads allow.
+__host__ __device__ inline uint32_t route_lanes_per_pair(uint64_t TE) {
+  uint32_t S = 1;
+  while (S < 8u && TE * S * 2u <= 256u) S *= 2u;
+  return S;
 }
 // Routing in the gate_up launch (route_wg_lds) where it pays: at most 64 key comparisons per
-// thread.  Measured per workgroup, its prologue costs about 3 us at E = 32 (T = 8), against the
-// routing launch's 4.9 us, and 5.4 us at E = 128 (T = 1: 128 comparisons per thread), against
-// about 4.5 us.
+// thread (16 quad reads).
 __host__ __device__ inline bool route_in_gate_up_ok(uint64_t T, uint32_t E, uint32_t K) {
-  return T >= 1 && T <= kSmallRouteMaxTokens && E <= kMaxExperts && K <= E && K <= kMaxTopK &&
-         (T * E + 255u) / 256u * E <= 64u;
+  if (T < 1 || T > kSmallRouteMaxTokens || E > kMaxExperts || K > E || K > kMaxTopK) return false;
+  const uint64_t TE = T * E, S = route_lanes_per_pair(TE), Ep = (E + 3u) & ~3u;
+  return (TE * S + 255u) / 256u * ((Ep / 4u + S - 1u) / S) * 4u <= 64u;
 }
 // B staging (which first holds the record table, or with route_E > 0 the routing of the launch),
 // the chosen record and the per-token row index.

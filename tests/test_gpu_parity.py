@@ -230,13 +230,13 @@ def _forward_case(M, oracle, L, x, dtype, flags=3, layout=None):
     return _np(y), y_ref
 
 
-@pytest.mark.parametrize("E,K,n", [(32, 4, 8), (32, 4, 16), (64, 4, 1), (48, 5, 5), (7, 3, 13), (130, 6, 1),
-                                   (128, 4, 16)])
+@pytest.mark.parametrize("E,K,n", [(32, 4, 8), (32, 4, 16), (64, 4, 1), (48, 5, 5), (7, 3, 13), (128, 4, 1),
+                                   (130, 6, 1), (128, 4, 16)])
 def test_forward_routing_ties(M, oracle, E, K, n):
     """Decode-sized forwards whose router logits are ties, a NaN, -0 and +0 (router weights zero,
     biases chosen, so every token routes alike and a selected expert gets all n tokens): the first
-    five cases route inside the gate_up launch (every workgroup ranks the (token, expert) pairs
-    itself), the last two run the routing kernel.  A wrong selection, order or weight would change
+    six cases route inside the gate_up launch (every workgroup ranks the (token, expert) pairs
+    itself, with 1, 2, 4 or 8 lanes per pair), the last two run the routing kernel.  A wrong selection, order or weight would change
     y, which is checked against oracle.moe_forward (NaN lowest, -0 == +0, equal values by lower
     index)."""
     from burnext_amd import synth
