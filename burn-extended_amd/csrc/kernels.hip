@@ -564,17 +564,11 @@ __device__ __forceinline__ uint32_t half_wave_incl_scan(uint32_t v) {
   return v + (row == 1u ? r0 : row == 3u ? r2 : 0u);
 }
 
-// a / b for a < 2^20 and b <= 2^12 given rb = 1.0f / b: the rounding error of (a + 0.5) * rb
-// (< 2^-22 relative) is far below the distance 0.5 / b of (a + 0.5) / b from an integer.
-__device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
-  return (uint32_t)(((float)a + 0.5f) * rb);
-}
-
 // Exclusive prefix sums over the experts e < E (E <= 256) of their entry counts c_e, of
 // [c_e > 0] and of ceil(c_e / kGemmTok), for thread e (threads 0 .. 255 of a workgroup of at least
 // 256): wave scans, then the totals of the waves below from LDS (tot_l: 12 ints).  Called by
 // every thread of the workgroup (two barriers); threads from 256 on get zeros.
-__device__ __forceinline__ void expert_prefix(const int32_t *cnt, uint32_t E, int32_t *tot_l, int32_t &off, int32_t &ra, int32_t &toff) {
+__device__ void expert_prefix(const int32_t *cnt, uint32_t E, int32_t *tot_l, int32_t &off, int32_t &ra, int32_t &toff) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const int32_t c = (tid < E && tid < kMaxExperts) ? cnt[tid] : 0;
   const uint32_t v0 = (uint32_t)c, v1 = c > 0 ? 1u : 0u, v2 = (uint32_t)((c + (int32_t)kGemmTok - 1) / (int32_t)kGemmTok);
@@ -899,22 +893,26 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 // Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
 
+// Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
+struct RouteOut {
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;
+};
+
 template <int J>
-__device__ __forceinline__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l, int32_t *lrec);
+__device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l);
 
 // Routing of T <= 16 tokens over E <= 64 * J experts from logits lg[t * E + e] (global or LDS) by
-// a workgroup of any number of waves (wave w takes tokens w, w + waves, ...).  Every wave of the
-// workgroup must call it (it has a barrier).  Global outputs o (null pointers: not written);
-// lrec (null: none) receives the record table in LDS with every token of a record
-// ([4 + j] token of segment entry j < M, M <= T), and na_l the active count (read it after a
-// barrier).
+// a workgroup of at least T waves.  Every wave of the workgroup must call it (it has a barrier).
 template <int J>
-__device__ __forceinline__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+__device__ void route_small_body(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
                                  int8_t (*rank_l)[kSmallRouteMaxTokens], float (*selv_l)[kMaxTopK],
-                                 int32_t *na_l, int32_t *lrec) {
-  const uint32_t lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
-  for (uint32_t t = threadIdx.x >> 6; t < T; t += nw) {
+                                 int32_t *na_l) {
+  const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
+  if (t < T) {
     float v[J];
     uint64_t key[J];
 #pragma unroll
@@ -955,17 +953,16 @@ __device__ __forceinline__ void route_small_body(const float *lg, uint32_t T, ui
       rank_l[e][t] = sel ? (int8_t)rank[j] : (int8_t)-1;
       if (sel) {
         selv_l[t][rank[j]] = v[j];
-        if (o.topk_idx) o.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
+        o.topk_idx[(size_t)t * K + rank[j]] = (int32_t)e;
       }
     }
-    if (!o.topk_w) continue;
     // this wave's selv_l writes complete (lgkmcnt(0) only: the global stores stay in flight)
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
     for (uint32_t p = lane; p < K; p += 64u) o.topk_w[(size_t)t * K + p] = softmax_weight(selv_l[t], K, p);
   }
   __syncthreads();
-  route_small_dispatch<J>(T, E, K, o, rank_l, na_l, lrec);
+  route_small_dispatch<J>(T, E, K, o, rank_l, na_l);
 }
 
 // Rank of token t in the 16 rank bytes rk (4 dwords) of one expert: -1 = not chosen.
@@ -976,13 +973,13 @@ __device__ __forceinline__ int rank_byte(const uint32_t (&rk)[4], uint32_t t) {
 // Dispatch part of route_small_body, run by every wave: each computes the per-expert counts and
 // scans (lane e reads the ranks of expert e in all tokens with one 16-byte LDS read,
 // rank_l[e][t]); wave 0 writes the per-expert outputs (segment offsets, active list, record
-// headers), wave w the segment entries of tokens w, w + waves, ... (the position of token t inside
-// expert e's segment is the number of earlier tokens that chose e).
+// headers), wave t < T the segment entries of token t (its position inside expert e's segment is
+// the number of earlier tokens that chose e).
 template <int J>
-__device__ __forceinline__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l, int32_t *lrec) {
+__device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
+                                     int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l) {
   static_assert(kSmallRouteMaxTokens == 16, "one 16-byte read per expert");
-  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint32_t lane = threadIdx.x & 63u, t = threadIdx.x >> 6;
   int cnt[J];
   uint32_t rk[J][4];
 #pragma unroll
@@ -1014,179 +1011,41 @@ __device__ __forceinline__ void route_small_dispatch(uint32_t T, uint32_t E, uin
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const uint32_t e = lane + 64u * j;
-    if (wv != 0 || e >= E) continue;
-    if (o.seg_off) o.seg_off[e] = off[j];
+    if (t != 0 || e >= E) continue;
+    o.seg_off[e] = off[j];
     if (cnt[j] > 0) {
-      if (o.active) o.active[ra[j]] = (int32_t)e;
-      if (o.exrec) {
-        int32_t *rec = o.exrec + ra[j] * kRecWords;
-        rec[0] = (int32_t)e;
-        rec[1] = off[j];
-        rec[2] = cnt[j];
-      }
-      if (lrec) {
-        int32_t *rec = lrec + ra[j] * kRecWords;
-        rec[0] = (int32_t)e;
-        rec[1] = off[j];
-        rec[2] = cnt[j];
-      }
+      o.active[ra[j]] = (int32_t)e;
+      int32_t *rec = o.exrec + ra[j] * kRecWords;
+      rec[0] = (int32_t)e;
+      rec[1] = off[j];
+      rec[2] = cnt[j];
     }
-    if ((int)e >= nact && o.active) o.active[e] = -1;
+    if ((int)e >= nact) o.active[e] = -1;
   }
-  if (wv == 0 && lane == 0) {
-    if (o.seg_off) o.seg_off[E] = total;
-    if (o.num_active) *o.num_active = nact;
+  if (t == 0 && lane == 0) {
+    o.seg_off[E] = total;
+    *o.num_active = nact;
     *na_l = nact;
   }
-  for (uint32_t t = wv; t < T; t += nw) {
+  if (t >= T) return;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t e = lane + 64u * j;
-      if (e >= E) continue;
-      const int r = rank_byte(rk[j], t);
-      if (r < 0) continue;
-      int seen = 0;  // earlier tokens that chose e
+  for (int j = 0; j < J; ++j) {
+    const uint32_t e = lane + 64u * j;
+    if (e >= E) continue;
+    const int r = rank_byte(rk[j], t);
+    if (r < 0) continue;
+    int seen = 0;  // earlier tokens that chose e
 #pragma unroll
-      for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) seen += (t2 < t && rank_byte(rk[j], t2) >= 0) ? 1 : 0;
-      const int pos = off[j] + seen;
-      const int32_t slot = (int32_t)(t * K + (uint32_t)r);
-      if (o.perm) {
-        o.perm[pos] = slot;
-        o.pos_of[slot] = pos;
-      }
-      if (o.exrec && seen < (int)kRecTokens) {
-        o.exrec[ra[j] * kRecWords + 4 + seen] = (int32_t)t;
-        o.exrec[ra[j] * kRecWords + 4 + kRecTokens + seen] = slot;
-      }
-      if (lrec) lrec[ra[j] * kRecWords + 4 + seen] = (int32_t)t;
+    for (uint32_t t2 = 0; t2 < kSmallRouteMaxTokens; ++t2) seen += (t2 < t && rank_byte(rk[j], t2) >= 0) ? 1 : 0;
+    const int pos = off[j] + seen;
+    const int32_t slot = (int32_t)(t * K + (uint32_t)r);
+    o.perm[pos] = slot;
+    o.pos_of[slot] = pos;
+    if (seen < (int)kRecTokens) {
+      o.exrec[ra[j] * kRecWords + 4 + seen] = (int32_t)t;
+      o.exrec[ra[j] * kRecWords + 4 + kRecTokens + seen] = slot;
     }
   }
-}
-
-// Routing of a decode-sized batch (T <= kSmallRouteMaxTokens tokens, E <= kMaxExperts experts,
-// K <= E) by one workgroup of 256 threads with compact loops: the prologue of the gate_up GEMV,
-// with route_small_body's results.  Thread i takes the (token, expert) pairs (t, e) = (i / E,
-// i mod E), i += 256: the expert's rank among the token's E keys is the number of keys that beat
-// it (the topk_key order; keys are unique, so the ranks are a permutation and those below K are
-// route_small_body's selection, rank 0 first); with fewer pairs than threads, S = 2, 4 or 8
-// adjacent lanes share a pair (lane s compares key quads s, s + S, ... read 16 bytes at a time; the
-// key rows are padded to whole quads with zero keys, which beat no real key) and add their counts
-// by DPP.  Thread e < E then counts expert e's tokens,
-// expert_prefix scans the counts and the active flags over the experts, and thread e writes
-// expert e's record and segment entries (earlier tokens first).  Global outputs o (null
-// pointers: not written); lrec receives the LDS record table with every token of a record
-// ([4 + j], j < M <= T).  Returns the number of active experts.  Every thread must call it.
-// LDS at lds (gemv_route_bytes past the table): key high words [T][E rounded up to 4], rank bytes
-// [E][16], selected logits [T][kMaxTopK], counts [E], scan totals [16], active count.
-__device__ __forceinline__ uint32_t route_wg_lds(const float *lg, uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
-                                                 unsigned char *lds, int32_t *lrec) {
-  const uint32_t tid = threadIdx.x, nthr = blockDim.x, TE = T * E, Ep = (E + 3u) & ~3u;
-  uint32_t *kh = (uint32_t *)lds;
-  int8_t *rank = (int8_t *)(kh + T * Ep);
-  float *selv = (float *)(rank + E * kSmallRouteMaxTokens);
-  int32_t *cnt_l = (int32_t *)(selv + T * kMaxTopK);
-  int32_t *tot_l = cnt_l + E;
-  int32_t *na_l = tot_l + 16;
-  const float rE = 1.0f / (float)E, rEp = 1.0f / (float)Ep, rK = 1.0f / (float)K;
-  for (uint32_t i = tid; i < T * Ep; i += nthr) {
-    const uint32_t t = div_small(i, rEp), e = i - t * Ep;
-    kh[i] = e < E ? (uint32_t)(topk_key(lg[t * E + e], 0u) >> 32) : 0u;
-  }
-  __syncthreads();
-  const uint32_t S = route_lanes_per_pair(TE), ls = tid & (S - 1u), per_round = nthr / S;
-#pragma unroll 1
-  for (uint32_t i0 = 0; i0 < TE; i0 += per_round) {  // the same trip count in every lane
-    const uint32_t i = i0 + tid / S, ic = min(i, TE - 1u);
-    const uint32_t t = div_small(ic, rE), e = ic - t * E, h = kh[t * Ep + e];
-    const uint4 *row = (const uint4 *)(kh + t * Ep);
-    uint32_t r = 0;  // keys above (h, ~e): a larger high word, or the same one at a lower index
-#pragma unroll 4
-    for (uint32_t qd = ls; qd < Ep / 4u; qd += S) {
-      const uint4 k4 = row[qd];
-      const uint32_t e2 = 4u * qd;
-      r += (k4.x > h || (k4.x == h && e2 < e)) ? 1u : 0u;
-      r += (k4.y > h || (k4.y == h && e2 + 1u < e)) ? 1u : 0u;
-      r += (k4.z > h || (k4.z == h && e2 + 2u < e)) ? 1u : 0u;
-      r += (k4.w > h || (k4.w == h && e2 + 3u < e)) ? 1u : 0u;
-    }
-    // the S lanes of the pair (adjacent, every lane active): lane ^ 1, lane ^ 2, then the mirror
-    // in each 8 (after the first two steps the quads are uniform)
-    if (S >= 2u) r += dpp_u<0xB1>(r);   // quad_perm [1,0,3,2]
-    if (S >= 4u) r += dpp_u<0x4E>(r);   // quad_perm [2,3,0,1]
-    if (S >= 8u) r += dpp_u<0x141>(r);  // row_half_mirror
-    if (i >= TE || ls != 0u) continue;
-    rank[e * kSmallRouteMaxTokens + t] = r < K ? (int8_t)r : (int8_t)-1;
-    if (r < K) {
-      selv[t * kMaxTopK + r] = lg[i];
-      if (o.topk_idx) o.topk_idx[(size_t)t * K + r] = (int32_t)e;
-    }
-  }
-  __syncthreads();
-  if (o.topk_w)
-    for (uint32_t i = tid; i < T * K; i += nthr) {
-      const uint32_t t = div_small(i, rK);
-      o.topk_w[i] = softmax_weight(selv + t * kMaxTopK, K, i - t * K);
-    }
-  uint32_t rk[4] = {0u, 0u, 0u, 0u};
-  int32_t c = 0;
-  if (tid < E) {
-    const uint4 v = *(const uint4 *)(rank + tid * kSmallRouteMaxTokens);
-    rk[0] = v.x;
-    rk[1] = v.y;
-    rk[2] = v.z;
-    rk[3] = v.w;
-#pragma unroll
-    for (uint32_t t = 0; t < kSmallRouteMaxTokens; ++t) c += (t < T && rank_byte(rk, t) >= 0) ? 1 : 0;
-    cnt_l[tid] = c;
-  }
-  int32_t off, ra, toff;
-  expert_prefix(cnt_l, E, tot_l, off, ra, toff);
-  if (tid < E) {
-    const uint32_t e = tid;
-    if (o.seg_off) o.seg_off[e] = off;
-    if (e + 1u == E) {
-      *na_l = ra + (c > 0 ? 1 : 0);
-      if (o.seg_off) o.seg_off[E] = off + c;
-      if (o.num_active) *o.num_active = ra + (c > 0 ? 1 : 0);
-    }
-    if (c > 0) {
-      if (o.active) o.active[ra] = (int32_t)e;
-      int32_t *lr = lrec + ra * kRecWords;
-      lr[0] = (int32_t)e;
-      lr[1] = off;
-      lr[2] = c;
-      if (o.exrec) {
-        int32_t *gr = o.exrec + ra * kRecWords;
-        gr[0] = (int32_t)e;
-        gr[1] = off;
-        gr[2] = c;
-      }
-      int seen = 0;
-#pragma unroll 1
-      for (uint32_t t = 0; t < T; ++t) {
-        const int r = rank_byte(rk, t);
-        if (r < 0) continue;
-        const int pos = off + seen;
-        const int32_t slot = (int32_t)(t * K + (uint32_t)r);
-        lr[4 + seen] = (int32_t)t;
-        if (o.perm) {
-          o.perm[pos] = slot;
-          o.pos_of[slot] = pos;
-        }
-        if (o.exrec && seen < (int)kRecTokens) {
-          o.exrec[ra * kRecWords + 4 + seen] = (int32_t)t;
-          o.exrec[ra * kRecWords + 4 + kRecTokens + seen] = slot;
-        }
-        ++seen;
-      }
-    }
-  }
-  __syncthreads();
-  const uint32_t nact = (uint32_t)*na_l;
-  if (o.active)
-    for (uint32_t e = tid; e < E; e += nthr)
-      if (e >= nact) o.active[e] = -1;
-  return nact;
 }
 
 template <int J>
@@ -1195,7 +1054,7 @@ __global__ __launch_bounds__(1024) void small_route_kernel(SmallRouteArgs a) {
   __shared__ float selv_l[kSmallRouteMaxTokens][kMaxTopK];
   __shared__ int32_t na_l;
   const RouteOut o{a.topk_idx, a.topk_w, a.seg_off, a.perm, a.pos_of, a.active, a.num_active, a.exrec};
-  route_small_body<J>(a.logits, a.n, a.E, a.K, o, rank_l, selv_l, &na_l, nullptr);
+  route_small_body<J>(a.logits, a.n, a.E, a.K, o, rank_l, selv_l, &na_l);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1427,6 +1286,11 @@ __global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
 // j sits at row mt_max + j -- and the two columns of a token are summed once per tile.
 // ---------------------------------------------------------------------------------------------
 
+// a / b for a < 2^20 and b <= 2^12 given rb = 1.0f / b: the rounding error of (a + 0.5) * rb
+// (< 2^-22 relative) is far below the distance 0.5 / b of (a + 0.5) / b from an integer.
+__device__ __forceinline__ uint32_t div_small(uint32_t a, float rb) {
+  return (uint32_t)(((float)a + 0.5f) * rb);
+}
 
 
 // Share of workgroup g of a grid of G among na active experts of nunits work units each: active
@@ -1471,10 +1335,7 @@ __device__ __forceinline__ bool gemv_share(uint32_t g, uint32_t G, uint32_t na, 
 // part order (b1 in part 0) and writes the SwiGLU rows.
 // Every workgroup stages its expert's B operand once per token pass (a pass = up to mt_max of the
 // expert's routed tokens; one pass at decode sizes).  A workgroup learns num_active, its expert,
-// segment and first tokens from one round trip (num_active plus the record table), or -- gate_up
-// of a decode-sized batch with route_lg -- routes the batch itself from its logits (one round trip
-// too; route_small_body into LDS, workgroup 0 also writing the routing outputs), which saves the
-// routing launch.
+// segment and first tokens from one round trip (num_active plus the record table).
 // Memory pipeline: waves stream their tiles in steps of kGemvKgPerWave K-groups held in one
 // register buffer; each K-group slot is refilled with the next step's K-group (also across tile
 // boundaries) right after its MFMAs, so kGemvKgPerWave - 1 K-groups stay in flight.  Everything
@@ -1492,9 +1353,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u;
   const uint32_t mtm = a.mt_max;
   uint16_t *bs = (uint16_t *)smem;
-  const bool lroute = GATE_UP && a.route_lg != nullptr;  // the routing in this launch
-  int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec, lroute ? a.route_E : 0u,
-                                                       a.route_T));  // [kRecWords]
+  int32_t *rec_l = (int32_t *)(smem + gemv_stage_bytes(NT, mtm, a.nb, a.nrec));  // [kRecWords]
   int32_t *tok_l = rec_l + kRecWords;                                             // [mtm]
   const uint32_t nrt = a.nrt;
   // work units: row tiles, or (down with ksplit) row tile u mod nrt, K-groups of part u / nrt
@@ -1502,23 +1361,11 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   constexpr bool kInWg = GATE_UP && SPLIT > 1;    // K-parts of a row tile on the 4 waves of a workgroup
   static_assert(!kInWg || SPLIT == 4, "one K-part per wave");
   const uint32_t nunits = kInWg ? nrt : nrt * nsplit;
-  const uint32_t k8n = Kp >> 3;
-  const float rk8n = 1.0f / (float)k8n;
-  unsigned char *tbl = smem;  // the record table (or the routing of the launch), in the B area
-  // one round trip: num_active and the record table (the table is staged through the B area), or
-  // the batch's logits, routed here into the same table
-  uint32_t na = 0;
-  if constexpr (GATE_UP) {
-    if (lroute) {
-      const RouteOut none{};
-      na = route_wg_lds(a.route_lg, a.route_T, a.route_E, a.topk, blockIdx.x == 0 ? a.rout : none,
-                        tbl + 4u * a.nrec * kRecWords, (int32_t *)tbl);
-    }
-  }
-  if (!lroute) {
-    na = (uint32_t)*a.num_active;
+  // one round trip: num_active and the record table (the table is staged through the B area)
+  const uint32_t na = (uint32_t)*a.num_active;
+  {
     const uint4 *src = (const uint4 *)a.exrec;
-    uint4 *dst = (uint4 *)tbl;
+    uint4 *dst = (uint4 *)smem;
     const uint32_t nv = a.nrec * (kRecWords / 4u);
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x) dst[i] = src[i];
   }
@@ -1538,7 +1385,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     ntw = (nunits - lo + wpe - 1u) / wpe;
   }
   __syncthreads();
-  const int32_t *rec0 = (const int32_t *)tbl + ai * kRecWords;  // valid until the first staging
+  const int32_t *rec0 = (const int32_t *)smem + ai * kRecWords;  // valid until the first staging
   if (threadIdx.x < kRecWords) rec_l[threadIdx.x] = rec0[threadIdx.x];
   const int e = rec0[0];
   const int seg0 = rec0[1];
@@ -1585,6 +1432,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   // true K.  Rows: gate_up the routed tokens' xn rows, down the segment's act rows (both
   // [*, Kp] in XT).  `first_loads` runs once, after the first batch's global loads are issued.
   uint32_t mt = 0, m0 = 0;
+  const float rk8n = 1.0f / (float)(Kp >> 3);
   auto stage = [&](uint32_t pass_, auto &&first_loads) {
     m0 = pass_ * mtm;
     mt = min(mtm, (uint32_t)M - m0);
@@ -1595,7 +1443,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
       const uint32_t jj = m0 + threadIdx.x;
       const int32_t *rec = pass_ == 0 ? rec0 : rec_l;
       int32_t v;
-      if (jj < (lroute ? kSmallRouteMaxTokens : kRecTokens)) {  // routed here: every token in the record
+      if (jj < kRecTokens) {
         v = rec[4 + (GATE_UP ? 0u : kRecTokens) + jj];
       } else {
         const int32_t slot = a.perm[seg0 + (int)jj];
@@ -1606,7 +1454,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
     __syncthreads();
     constexpr int SB = NT == 1 ? 3 : 2;
     const XT *src = (const XT *)a.brows;
-    const uint32_t nitm = mt * k8n;
+    const uint32_t k8n = Kp >> 3, nitm = mt * k8n;
     bool first = true;
     for (uint32_t base = threadIdx.x; base < nitm; base += SB * blockDim.x) {
       Chunk8<XT> cx[SB];
@@ -1652,8 +1500,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t my_first = kInWg ? lo + wv * nrt : lo + us * wv, tstride = kInWg ? us : 4u * us;
   const uint32_t my_tiles = kInWg ? ntw : (wv < ntw ? (ntw - wv + 3u) / 4u : 0u);
   const uint32_t first_c = kInWg ? my_first : min(my_first, nunits - 1u);
-  float *red = (float *)(smem + gemv_red_offset(NT, mtm, a.nb, a.nrec, lroute ? a.route_E : 0u,
-                                                a.route_T));  // kInWg: [2][4][64][4]
+  float *red = (float *)(smem + gemv_red_offset(NT, mtm, a.nb, a.nrec));  // kInWg: [2][4][64][4]
   uint32_t parity = 0;
   const uint32_t total = my_tiles * nst;  // steps of this wave per token pass
   uint32_t ti = 0, st = 0, g = 0;         // tile ordinal, step in tile, step count
@@ -2208,11 +2055,7 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   const uint64_t nunits = (uint64_t)a.nrt * (a.ksplit > 1u ? a.ksplit : 1u);
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid);
-  if (a.route_lg && (!gate_up || !route_in_gate_up_ok(a.route_T, a.route_E, a.topk) ||
-                     a.nrec < std::min(a.route_E, a.route_T * a.topk)))
-    return hipErrorInvalidValue;
-  const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u,
-                                           a.route_lg ? a.route_E : 0u, a.route_T);
+  const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;
   if (nt == 1)

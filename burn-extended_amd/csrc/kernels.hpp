@@ -70,18 +70,6 @@ struct TopkArgs {
 // j-th segment entry, for j < min(M, kRecTokens).
 constexpr uint32_t kRecWords = 32;
 constexpr uint32_t kRecTokens = 14;
-constexpr uint32_t kMaxTopK = 32;
-constexpr uint32_t kMaxExperts = 256;
-constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: routing by one workgroup
-
-// Output pointers of the small-batch routing (top-k, softmax, dispatch, records); all null: none
-// written (the routing goes to LDS only).
-struct RouteOut {
-  int32_t *topk_idx;
-  float *topk_w;
-  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
-  int32_t *exrec;
-};
 
 struct DispatchArgs {
   const int32_t *topk_idx;
@@ -122,14 +110,6 @@ struct GemvArgs {
   // tiles, the workgroup sums the parts in order (bias in part 0) and writes the SwiGLU rows
   uint32_t ksplit;
   uint64_t out_half;
-  // gate_up of a decode-sized batch with the routing in the same launch (route_lg not null): every
-  // workgroup computes the top-k and dispatch of the route_T tokens from their logits
-  // [route_T, route_E] into an LDS record table (up to kSmallRouteMaxTokens tokens per record);
-  // workgroup 0 also writes the routing outputs rout for the down projection and the combine
-  // (seg_off, active, num_active, perm and exrec above are then unused by this launch)
-  const float *route_lg;
-  uint32_t route_T, route_E;
-  RouteOut rout;
 };
 
 // Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,
@@ -267,51 +247,22 @@ size_t dispatch_lds_bytes(uint32_t E, uint32_t threads);
 __host__ __device__ inline size_t gemv_lds_bytes(int nt, uint32_t mt_max, uint32_t nb) {
   return sizeof(uint16_t) * (size_t)nt * mt_max * (32u * nb + 8u);
 }
-// Routing in the gate_up launch (route_E experts, route_T tokens, route_wg_lds): the LDS record
-// table [nrec][kRecWords], then the key words [route_T][route_E], the rank bytes
-// [route_E][kSmallRouteMaxTokens], the selected logits [route_T][kMaxTopK], the counts [route_E],
-// the scan totals [16] and the active count.
-__host__ __device__ inline size_t gemv_route_bytes(uint32_t nrec, uint32_t route_E, uint32_t route_T) {
-  return 4u * (size_t)nrec * kRecWords + 4u * (size_t)route_T * ((route_E + 3u) & ~3u) +
-         (size_t)route_E * kSmallRouteMaxTokens + 4u * (size_t)route_T * kMaxTopK + 4u * (size_t)route_E + 4u * 16u + 16u;
-}
-// Lanes per (token, expert) pair of route_wg_lds: 1, 2, 4 or 8, as many as 256 threads allow.
-__host__ __device__ inline uint32_t route_lanes_per_pair(uint64_t TE) {
-  uint32_t S = 1;
-  while (S < 8u && TE * S * 2u <= 256u) S *= 2u;
-  return S;
-}
-// Routing in the gate_up launch (route_wg_lds) where it pays: at most 64 key comparisons per
-// thread (16 quad reads).
-__host__ __device__ inline bool route_in_gate_up_ok(uint64_t T, uint32_t E, uint32_t K) {
-  if (T < 1 || T > kSmallRouteMaxTokens || E > kMaxExperts || K > E || K > kMaxTopK) return false;
-  const uint64_t TE = T * E, S = route_lanes_per_pair(TE), Ep = (E + 3u) & ~3u;
-  return (TE * S + 255u) / 256u * ((Ep / 4u + S - 1u) / S) * 4u <= 64u;
-}
-// B staging (which first holds the record table, or with route_E > 0 the routing of the launch),
-// the chosen record and the per-token row index.
-__host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                   uint32_t route_E = 0, uint32_t route_T = 0) {
-  const size_t b = gemv_lds_bytes(nt, mt_max, nb);
-  const size_t t = route_E ? gemv_route_bytes(nrec, route_E, route_T) : 4u * (size_t)nrec * kRecWords;
+// B staging (which first holds the record table), the chosen record and the per-token row index.
+__host__ __device__ inline size_t gemv_stage_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  const size_t b = gemv_lds_bytes(nt, mt_max, nb), t = 4u * (size_t)nrec * 32u;
   return b > t ? b : t;
 }
-__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                       uint32_t route_E = 0, uint32_t route_T = 0) {
-  return gemv_stage_bytes(nt, mt_max, nb, nrec, route_E, route_T) + 4u * 32u + 4u * (size_t)mt_max + 16u;
+__host__ __device__ inline size_t gemv_total_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  return gemv_stage_bytes(nt, mt_max, nb, nrec) + 4u * 32u + 4u * (size_t)mt_max + 16u;
 }
 // gate_up in K-parts (kGateUpSplit waves of a workgroup per row tile): the parts' tile results
 // meet in LDS after the other regions, [tile parity][wave][lane] x 4 floats
 constexpr size_t kGemvRedBytes = 2u * 4u * 64u * 16u;
-// (the kernel places red at the same offset: route_E / route_T as launched)
-__host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec,
-                                                  uint32_t route_E = 0, uint32_t route_T = 0) {
-  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E, route_T) + 15u) & ~(size_t)15u;
+__host__ __device__ inline size_t gemv_red_offset(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec) {
+  return (gemv_total_lds_bytes(nt, mt_max, nb, nrec) + 15u) & ~(size_t)15u;
 }
-__host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red,
-                                                        uint32_t route_E = 0, uint32_t route_T = 0) {
-  return red ? gemv_red_offset(nt, mt_max, nb, nrec, route_E, route_T) + kGemvRedBytes
-             : gemv_total_lds_bytes(nt, mt_max, nb, nrec, route_E, route_T);
+__host__ __device__ inline size_t gemv_launch_lds_bytes(int nt, uint32_t mt_max, uint32_t nb, uint32_t nrec, bool red) {
+  return red ? gemv_red_offset(nt, mt_max, nb, nrec) + kGemvRedBytes : gemv_total_lds_bytes(nt, mt_max, nb, nrec);
 }
 constexpr uint32_t kGemvKgPerWave = 6;  // K-groups per wave per step (6 KiB of weights in flight)
 
@@ -334,6 +285,9 @@ constexpr uint32_t kDownSplit = 2;  // K-parts per down row tile of the expert G
 // waves idle (one part per wave of a workgroup, summed in LDS before the SwiGLU epilogue)
 constexpr uint32_t kGateUpSplit = 4;
 constexpr uint32_t kDownSplitFew = 4;  // K-parts per down row tile for the same batches
+constexpr uint32_t kMaxTopK = 32;
+constexpr uint32_t kMaxExperts = 256;
+constexpr uint32_t kSmallRouteMaxTokens = 16;  // decode-sized batches: one-workgroup routing kernel
 
 hipError_t launch_router(const RouterArgs &a, bool x_bf16, bool w_bf16, bool vec, hipStream_t s);
 // router_rows_kernel: D % 8 == 0 and D, Dp (with xn) and xq.kq (with xq) <= 512 * kFrontChunks,

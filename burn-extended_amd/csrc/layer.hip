@@ -296,7 +296,7 @@ struct GemvCfg {
 
 bool gate_up_split(const burnext_moe_layer &L, uint64_t n);
 
-GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up, bool lroute) {
+GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up) {
   const TiledMx &t = gate_up ? L.w1 : L.w2;
   GemvCfg c{};
   const size_t per_tok = gemv_lds_bytes(nt, 1, t.nb);
@@ -317,8 +317,7 @@ GemvCfg gemv_cfg(const burnext_moe_layer &L, uint64_t n, int nt, bool gate_up, b
     }
   mt = (uint32_t)std::min<uint64_t>(mt, n);
   c.mt = (uint32_t)std::min<size_t>(mt, std::max<size_t>(1, (96 * 1024) / per_tok));
-  const size_t lds = gemv_launch_lds_bytes(nt, c.mt, t.nb, c.nrec, gate_up && gate_up_split(L, n), lroute ? L.E : 0u,
-                                           lroute ? (uint32_t)n : 0u);
+  const size_t lds = gemv_launch_lds_bytes(nt, c.mt, t.nb, c.nrec, gate_up && gate_up_split(L, n));
   const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, (160 * 1024) / std::max<size_t>(lds, 1)));
   c.grid = (uint32_t)std::max<uint64_t>(max_active, std::min<uint64_t>((uint64_t)L.num_cus * per_cu, max_active * t.nrt));
   return c;
@@ -929,13 +928,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   const bool small_router = !pa && router_small_ok(*L, n, x, norm);
   const bool xnb = xb || experts_bf16;
   const int nt = xnb ? 1 : 2;
-  FusedGeom fg{};
-  const bool fused_experts = (flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg);
-  // decode-sized batches with few (token, expert) pairs route inside the gate_up launch (every
-  // workgroup from the logits, no routing launch); the fused experts kernel reads the routing
-  // kernel's records
-  const bool lroute = !fused_experts && route_in_gate_up_ok(n, L->E, L->K);
-  const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true, lroute), cfg_dn = gemv_cfg(*L, n, nt, false, false);
+  const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
   // evenly over the waves; measured slower from 64 tokens on)
@@ -947,7 +940,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
        : small_router ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, xnb && !xb, s)
                       : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s, nullptr, xnb && !xb);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
-    if (!lroute) st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
+    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
   } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
@@ -955,7 +948,8 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   }
   if (st != BURNEXT_OK) return st;
 
-  if (fused_experts) {
+  FusedGeom fg{};
+  if ((flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg)) {
     st = run_fused(L, n, nt, xnb, fg, p, s);
     if (st != BURNEXT_OK) return st;
     return combine(L, x, y, xb, n, flags, p, s, 1, false, nullptr, &fg);
@@ -995,12 +989,6 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
       g.out_half = n * L->K * L->Dp;
     }
     if (gate_up && up_split) g.ksplit = kGateUpSplit;  // K-parts on the waves of a workgroup, summed there
-    if (gate_up && lroute) {
-      g.route_lg = p.logits;
-      g.route_T = (uint32_t)n;
-      g.route_E = L->E;
-      g.rout = RouteOut{p.topk_idx, p.topk_w, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec};
-    }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xnb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };

@@ -175,10 +175,9 @@ def test_route_small_ties_nan_signed_zero(M, oracle, E, K, n):
                                            (256, 2, 2, 16, "f32"), (200, 7, 3, 13, "f32"), (2880, 32, 4, 64, "bf16"),
                                            (2880, 128, 4, 1100, "bf16")])
 def test_route_dispatch_as_forward(M, oracle, D, E, K, n, dtype):
-    """Routing + dispatch by the forward's routing kernels (n <= 16: the one-workgroup kernel, which
-    the forward runs where the routing does not go into its gate_up launch; above: top-k then
-    dispatch): indices, weights, segment offsets and the entry list against the oracle's top-k and
-    counting sort."""
+    """Routing + dispatch exactly as the forward runs them (n <= 16: the fused one-workgroup kernel;
+    above: top-k then dispatch): indices, weights, segment offsets and the entry list against the
+    oracle's top-k and counting sort."""
     from burnext_amd import synth
     print(f"route+dispatch D={D} E={E} K={K} n={n} {dtype}", flush=True)
     L = _make(synth, D, 64, E, K, seed=21, dtype=dtype, with_gamma=True)
@@ -234,11 +233,10 @@ def _forward_case(M, oracle, L, x, dtype, flags=3, layout=None):
                                    (130, 6, 1), (128, 4, 16)])
 def test_forward_routing_ties(M, oracle, E, K, n):
     """Decode-sized forwards whose router logits are ties, a NaN, -0 and +0 (router weights zero,
-    biases chosen, so every token routes alike and a selected expert gets all n tokens): the first
-    six cases route inside the gate_up launch (every workgroup ranks the (token, expert) pairs
-    itself, with 1, 2, 4 or 8 lanes per pair), the last two run the routing kernel.  A wrong selection, order or weight would change
-    y, which is checked against oracle.moe_forward (NaN lowest, -0 == +0, equal values by lower
-    index)."""
+    biases chosen, so every token routes alike and a selected expert gets all n tokens, 16 at most:
+    two token passes where a pass holds 8): a wrong selection, order or weight in the forward's
+    routing (the one-workgroup routing kernel and its records) would change y, which is checked
+    against oracle.moe_forward (NaN lowest, -0 == +0, equal values by lower index)."""
     from burnext_amd import synth
     print(f"forward routing ties E={E} K={K} n={n}", flush=True)
     L = _make(synth, 64, 32, E, K, seed=23, dtype="f32")
