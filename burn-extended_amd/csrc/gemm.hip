@@ -315,6 +315,9 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
     const uint8_t *st = smem + (kg % kStages) * kStage;
     const uint8_t *sc = scl + ((kg >> 2) & 1u) * kScaleSlot + kP * 4u;
     BFrag b0, b1;
+    // the operand reads and MFMAs at raised wave priority, so that the other workgroup's waves on
+    // the SIMD issue their loads around them (C3 gate_up 402 -> 397 us, down 217.6 -> 216.0 us)
+    __builtin_amdgcn_s_setprio(1);
     read_b(st, sc, 0, b0);
     read_b(st, sc, 1, b1);
     mma(ar, sa_cur, b0, 0, P);
@@ -336,6 +339,7 @@ __global__ __launch_bounds__(256, 2) void expert_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_s_setprio(0);
     load_a(min(kg + 2u, nkg - 1u), ar);
     // at position 2, the next block's A scales (needed from K-group kg + 2 on)
     if constexpr (kP == 2u) load_as(min((kg >> 2) + 1u, nkq - 1u), sa_nxt);
