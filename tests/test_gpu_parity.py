@@ -449,6 +449,21 @@ def test_forward_f32_large_batch_gemv_records(M, oracle):
     assert err <= TOL_F32
 
 
+@pytest.mark.parametrize("D,F,E,K,n", [(256, 192, 32, 4, 24), (2880, 2880, 32, 4, 20), (320, 256, 16, 2, 30)])
+def test_forward_f32_packed_terms_full_columns(M, oracle, D, F, E, K, n):
+    """f32 batches above 16 tokens with at most 4 routed tokens per expert on average: 8 token rows
+    per pass, so the expert GEMVs put both activation terms into all 16 MFMA columns (term 1 of
+    token j in column 8 + j) and experts with more than 8 tokens take a second pass."""
+    from burnext_amd import synth
+    print(f"f32 packed terms D={D} F={F} E={E} K={K} n={n}", flush=True)
+    L = _make(synth, D, F, E, K, seed=31, dtype="f32", with_gamma=True)
+    x = synth.make_tokens(n, D, seed=32, dtype="f32")
+    y, y_ref = _forward_case(M, oracle, L, x, "f32", flags=3)
+    err = oracle.max_abs_rel(y, y_ref)
+    print(f"  max-abs-rel {err:.3e}")
+    assert err <= TOL_F32
+
+
 def test_forward_20b_f32_activations(M, oracle):
     """20B shape with f32 activations (three bf16 terms per activation) at the f32 bar."""
     from burnext_amd import synth
