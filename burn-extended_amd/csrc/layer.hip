@@ -387,8 +387,8 @@ uint64_t fused_rows(const burnext_moe_layer &L, uint64_t m) {
 
 // Workspace regions for n tokens.  Every region is sized for the largest need of any batch of
 // m <= n tokens, so burnext_moe_workspace_size(n) is non-decreasing in n and one workspace sized
-// for the largest batch serves every smaller one: the K-part buffers of decode-sized batches
-// (ypart in kDownSplitFew or kDownSplit parts, upart) are larger per token than a bigger batch's
+// for the largest batch serves every smaller one: the K-part buffer of decode-sized batches
+// (ypart in kDownSplitFew or kDownSplit parts) is larger per token than a bigger batch's
 // single-part ypart.
 WsLayout ws_layout(const burnext_moe_layer &L, uint64_t n) {
   WsLayout w{};
