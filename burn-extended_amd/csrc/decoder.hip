@@ -444,11 +444,6 @@ __device__ __forceinline__ void raw_vals(const RawQ<uint16_t> &r, float (&v)[4])
   v[3] = bf16_bits_to_f32((uint16_t)(r.v.y >> 16));
 }
 
-// The same chunk as attn_chunk_kernel for head_dim <= 64 and G <= 8, in one memory round trip:
-// every thread requests its q quad, then its key's (up to) 16 K quads and the 16 value quads its
-// (key lane kq, dim quad dq) slot of the value phase needs, before waiting for any of them.  Keys
-// past the window and quads past head_dim read a valid slot and are not used.  Same arithmetic
-// order as attn_chunk_kernel.
 // G consecutive floats of LDS (16-byte aligned for G >= 4, 8-byte for G = 2) in the widest
 // accesses that fit.
 template <uint32_t G>
@@ -482,8 +477,15 @@ __device__ __forceinline__ void lds_load_g(const float *p, float (&v)[G]) {
   }
 }
 
+// The same chunk as attn_chunk_kernel for head_dim <= 64 and G <= 8: every thread requests its q
+// quad and its key's (up to) 16 K quads before waiting for any of them, and the 16 value quads its
+// (key lane kq, dim quad dq) slot of the value phase needs as soon as its scores have consumed the
+// K quads -- K and V never held at once, so 4 workgroups share a CU (118 VGPRs) and a full
+// layer's 2 048 workgroups run in 2 rounds instead of 2.7 at 3 per CU (decoder step 3.505 ->
+// 3.489 ms against requesting the value quads with the K quads).  Keys past the window and quads
+// past head_dim read a valid slot and are not used.  Same arithmetic order as attn_chunk_kernel.
 template <typename KV, uint32_t G>
-__global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 4) void attn_chunk64_kernel(AttnArgs a) {
   __shared__ __align__(16) float q_l[G * 64];
   __shared__ __align__(16) float e_l[kAttnChunk * G];
   __shared__ float m_l[4 * G], l_l[4 * G];
@@ -504,12 +506,6 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
 #pragma unroll
   for (uint32_t u = 0; u < 16u; ++u) raw_load(kb + (size_t)min(u, nq - 1u) * 256u, kr[u]);
   const uint32_t kq = t >> 4, dq = t & 15u, dqc = min(dq, nq - 1u);
-  RawQ<KV> vr[16];
-#pragma unroll
-  for (uint32_t i = 0; i < 16u; ++i) {
-    const uint32_t key = min(kq + 16u * i, nkeys - 1u);
-    raw_load(vc + v_index(b, g, key_slot(a, i0 + key), 4u * dqc, a.kvH, a.cap_p, dk), vr[i]);
-  }
   if (t < nqq) *(float4 *)(q_l + 4u * t) = qv;
   __syncthreads();
   float s[G];
@@ -530,6 +526,15 @@ __global__ __launch_bounds__(256) void attn_chunk64_kernel(AttnArgs a) {
       }
     }
   }
+  // the value quads, requested once the scores hold what the K quads gave
+  __builtin_amdgcn_sched_barrier(0);
+  RawQ<KV> vr[16];
+#pragma unroll
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const uint32_t key = min(kq + 16u * i, nkeys - 1u);
+    raw_load(vc + v_index(b, g, key_slot(a, i0 + key), 4u * dqc, a.kvH, a.cap_p, dk), vr[i]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   // wave maxima and sums of the G heads: lane-0 reductions, the G chains interleaved
   float red[G];
 #pragma unroll
@@ -1059,7 +1064,7 @@ bool attn_direct_ok(uint32_t dk, uint32_t groups) {
 template <typename KV>
 hipError_t launch_attention_kv(uint32_t groups, dim3 grid, hipStream_t s, const AttnArgs &a) {
   if (a.ctx != nullptr && !attn_direct_ok(a.dk, groups)) return hipErrorInvalidValue;
-  if (a.dk <= 64u) {  // one memory round trip per chunk
+  if (a.dk <= 64u) {  // a chunk's q and K quads in one memory round trip, its V quads right after the scores
     switch (groups) {
       case 1: return launch_kernel(attn_chunk64_kernel<KV, 1>, grid, dim3(256), 0, s, a);
       case 2: return launch_kernel(attn_chunk64_kernel<KV, 2>, grid, dim3(256), 0, s, a);
