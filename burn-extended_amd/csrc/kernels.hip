@@ -893,14 +893,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
 // Results equal topk_kernel + block_dispatch.
 // ---------------------------------------------------------------------------------------------
 
-// Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
-struct RouteOut {
-  int32_t *topk_idx;
-  float *topk_w;
-  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
-  int32_t *exrec;
-};
-
 template <int J>
 __device__ void route_small_dispatch(uint32_t T, uint32_t E, uint32_t K, const RouteOut &o,
                                      int8_t (*rank_l)[kSmallRouteMaxTokens], int32_t *na_l);
@@ -1270,6 +1262,89 @@ __global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
   }
 }
 
+// Routing of one token (E <= kMaxExperts experts, K <= min(E, kMaxTopK)) inside a workgroup of at
+// least K threads: wave 0 takes the top K by K wave-wide maxima of the packed keys (topk_key and
+// wave_max_key, route_small_body's selection and order); then thread r < K places the expert of
+// rank r at its active slot, the number of selected experts with a lower index (the dispatch's
+// expert order, one token each), and writes that slot's record into lrec (LDS, [K][kRecWords]:
+// expert, segment offset = slot, 1 token, token 0, slot r).  With wout (workgroup 0 of the launch)
+// it also writes the routing outputs o: indices and softmax weights in rank order, segment offsets,
+// active list, entry list and records.  Returns K.  Every thread of the workgroup must call it.
+__device__ __forceinline__ uint32_t route_one_token(const float *lg, uint32_t E, uint32_t K, const RouteOut &o,
+                                                    bool wout, int32_t *lrec) {
+  __shared__ int32_t sel_l[kMaxTopK];
+  __shared__ float selv_l[kMaxTopK];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  if (tid < 64u) {
+    constexpr int J = (int)(kMaxExperts / 64u);
+    float v[J];
+    uint32_t kh[J], kl[J];
+    bool taken[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t e = lane + 64u * (uint32_t)j;
+      v[j] = e < E ? lg[e] : 0.0f;
+      const uint64_t key = topk_key(v[j], e);
+      kh[j] = (uint32_t)(key >> 32);
+      kl[j] = (uint32_t)key;
+      taken[j] = e >= E;
+    }
+    for (uint32_t r = 0; r < K; ++r) {
+      uint32_t bh = 0u, bl = 0u;  // below every real key (the low word ~index is never 0)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (!taken[j] && (kh[j] > bh || (kh[j] == bh && kl[j] > bl))) {
+          bh = kh[j];
+          bl = kl[j];
+        }
+      wave_max_key(bh, bl);
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (!taken[j] && kh[j] == bh && kl[j] == bl) {  // the one lane and chunk holding rank r
+          taken[j] = true;
+          sel_l[r] = (int32_t)(lane + 64u * (uint32_t)j);
+          selv_l[r] = v[j];
+        }
+    }
+  }
+  __syncthreads();
+  if (tid < K) {
+    const int32_t e = sel_l[tid];
+    int32_t pos = 0;
+    for (uint32_t u = 0; u < K; ++u) pos += sel_l[u] < e ? 1 : 0;
+    int32_t *rec = lrec + pos * (int32_t)kRecWords;
+    rec[0] = e;
+    rec[1] = pos;
+    rec[2] = 1;
+    rec[4] = 0;
+    rec[4 + kRecTokens] = (int32_t)tid;
+    if (wout) {
+      o.topk_idx[tid] = e;
+      o.topk_w[tid] = softmax_weight(selv_l, K, tid);
+      o.active[pos] = e;
+      o.perm[pos] = (int32_t)tid;
+      o.pos_of[tid] = pos;
+      int32_t *g = o.exrec + pos * (int32_t)kRecWords;
+      g[0] = e;
+      g[1] = pos;
+      g[2] = 1;
+      g[4] = 0;
+      g[4 + kRecTokens] = (int32_t)tid;
+    }
+  }
+  if (wout) {  // segment offsets: the selected experts below e; inactive slots
+    for (uint32_t e = tid; e <= E; e += blockDim.x) {
+      int32_t c = 0;
+      for (uint32_t u = 0; u < K; ++u) c += (uint32_t)sel_l[u] < e ? 1 : 0;
+      o.seg_off[e] = c;
+      if (e >= K && e < E) o.active[e] = -1;
+    }
+    if (tid == 0) *o.num_active = (int32_t)K;
+  }
+  __syncthreads();
+  return K;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Expert projection on MFMA.  Tiled MXFP4 layout of one expert (written by the layer upload):
 //   row tile rt (16 rows) occupies nb*256 bytes; inside it K-group kg (4 blocks of 32 columns)
@@ -1361,9 +1436,14 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
   constexpr bool kInWg = GATE_UP && SPLIT > 1;    // K-parts of a row tile on the 4 waves of a workgroup
   static_assert(!kInWg || SPLIT == 4, "one K-part per wave");
   const uint32_t nunits = kInWg ? nrt : nrt * nsplit;
-  // one round trip: num_active and the record table (the table is staged through the B area)
-  const uint32_t na = (uint32_t)*a.num_active;
-  {
+  // one round trip: num_active and the record table (the table is staged through the B area), or
+  // (single-token gate_up) the token's logits, routed here into the same table
+  uint32_t na;
+  if (GATE_UP && a.route1_lg != nullptr) {
+    const RouteOut ro = a.rout;
+    na = route_one_token(a.route1_lg, a.route1_E, a.topk, ro, blockIdx.x == 0, (int32_t *)smem);
+  } else {
+    na = (uint32_t)*a.num_active;
     const uint4 *src = (const uint4 *)a.exrec;
     uint4 *dst = (uint4 *)smem;
     const uint32_t nv = a.nrec * (kRecWords / 4u);
@@ -1863,9 +1943,14 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
 hipError_t configure_kernels() {
   const int big = 160 * 1024;
   hipError_t err = hipSuccess;
+// (the dynamic limit is what the CU's LDS leaves beside the kernel's static LDS)
 #define BX_ATTR(f)                                                                                                  \
   do {                                                                                                               \
-    hipError_t e_ = hipFuncSetAttribute((const void *)(f), hipFuncAttributeMaxDynamicSharedMemorySize, big);       \
+    hipFuncAttributes fa_{};                                                                                         \
+    hipError_t e_ = hipFuncGetAttributes(&fa_, (const void *)(f));                                                   \
+    if (e_ == hipSuccess)                                                                                            \
+      e_ = hipFuncSetAttribute((const void *)(f), hipFuncAttributeMaxDynamicSharedMemorySize,                        \
+                               big - (int)fa_.sharedSizeBytes);                                                      \
     if (e_ != hipSuccess && err == hipSuccess) err = e_;                                                             \
   } while (0)
   BX_ATTR((router_kernel<float, float, true>));
@@ -2055,6 +2140,9 @@ hipError_t launch_gemv(const GemvArgs &a, int nt, bool gate_up, bool x_bf16, uin
   const uint64_t nunits = (uint64_t)a.nrt * (a.ksplit > 1u ? a.ksplit : 1u);
   if (grid == 0 || nunits * std::max(kRoundWeight[0][0], kRoundWeight[1][0]) * grid >= (1ull << 32)) return hipErrorInvalidValue;
   const dim3 g(grid);
+  if (a.route1_lg && (!gate_up || a.route1_E > kMaxExperts || a.topk > kMaxTopK || a.topk > a.route1_E ||
+                      a.nrec < a.topk || a.topk > kGemvThreads))
+    return hipErrorInvalidValue;
   const size_t lds = gemv_launch_lds_bytes(nt, a.mt_max, a.nb, a.nrec, gate_up && a.ksplit > 1u);
   if (!gate_up && a.ksplit > 1u && a.ksplit != kDownSplit && a.ksplit != kDownSplitFew) return hipErrorInvalidValue;
   if (gate_up && a.ksplit > 1u && a.ksplit != kGateUpSplit) return hipErrorInvalidValue;

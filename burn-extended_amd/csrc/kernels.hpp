@@ -71,6 +71,14 @@ struct TopkArgs {
 constexpr uint32_t kRecWords = 32;
 constexpr uint32_t kRecTokens = 14;
 
+// Output pointers of the small-batch routing (top-k, softmax, dispatch, records).
+struct RouteOut {
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *seg_off, *perm, *pos_of, *active, *num_active;
+  int32_t *exrec;
+};
+
 struct DispatchArgs {
   const int32_t *topk_idx;
   int32_t *seg_off, *perm, *pos_of, *active, *num_active;
@@ -110,6 +118,14 @@ struct GemvArgs {
   // tiles, the workgroup sums the parts in order (bias in part 0) and writes the SwiGLU rows
   uint32_t ksplit;
   uint64_t out_half;
+  // gate_up of a single-token batch with its routing in the launch (route1_lg: the token's
+  // route1_E logits, topk = K <= kMaxTopK): every workgroup selects the top K itself and lays out
+  // the K records (one token each, experts in index order) in LDS; workgroup 0 also writes rout
+  // for the down projection and the combine.  seg_off, active, num_active, perm and exrec above
+  // are then unused by this launch.
+  const float *route1_lg;
+  uint32_t route1_E;
+  RouteOut rout;
 };
 
 // Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,

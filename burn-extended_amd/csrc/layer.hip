@@ -928,6 +928,10 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   const bool small_router = !pa && router_small_ok(*L, n, x, norm);
   const bool xnb = xb || experts_bf16;
   const int nt = xnb ? 1 : 2;
+  FusedGeom fg{};
+  const bool fused_experts = (flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg);
+  // a single token routes inside the gate_up launch (route_one_token: no routing launch)
+  const bool route1 = n == 1 && !fused_experts && L->E <= kMaxExperts && L->K <= kMaxTopK && L->K <= L->E;
   const GemvCfg cfg_up = gemv_cfg(*L, n, nt, true), cfg_dn = gemv_cfg(*L, n, nt, false);
   // down projection of decode-sized batches: every row tile's K range in ksplit fixed parts of
   // whole K-groups (separate work units, so the units are a fraction of a tile each and spread
@@ -940,7 +944,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
        : small_router ? run_router_small(L, x, xb, n, norm, p.rms, p.logits, p.xn, xnb && !xb, s)
                       : run_router(L, x, xb, n, norm, p.rms, p.logits, p.xn, s, nullptr, xnb && !xb);
   if (st == BURNEXT_OK && n <= kSmallRouteMaxTokens) {
-    st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
+    if (!route1) st = run_small_route(L, n, p, p.logits, p.topk_idx, p.topk_w, s);
   } else if (st == BURNEXT_OK) {
     st = run_topk(L, n, p.logits, p.topk_idx, p.topk_w, s);
     if (st == BURNEXT_OK)
@@ -948,8 +952,7 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   }
   if (st != BURNEXT_OK) return st;
 
-  FusedGeom fg{};
-  if ((flags & BURNEXT_FUSED_EXPERTS) && use_fused(*L, n, nt, pn != nullptr, fg)) {
+  if (fused_experts) {
     st = run_fused(L, n, nt, xnb, fg, p, s);
     if (st != BURNEXT_OK) return st;
     return combine(L, x, y, xb, n, flags, p, s, 1, false, nullptr, &fg);
@@ -989,6 +992,11 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
       g.out_half = n * L->K * L->Dp;
     }
     if (gate_up && up_split) g.ksplit = kGateUpSplit;  // K-parts on the waves of a workgroup, summed there
+    if (gate_up && route1) {
+      g.route1_lg = p.logits;
+      g.route1_E = L->E;
+      g.rout = RouteOut{p.topk_idx, p.topk_w, p.seg_off, p.perm, p.pos_of, p.active, p.num_active, p.exrec};
+    }
     ProfScope ps(L, s, gate_up ? kKGateUp : kKDown);
     return check_launch(launch_gemv(g, nt, gate_up, xnb, cf.grid, s), gate_up ? "gate_up launch" : "down launch");
   };
