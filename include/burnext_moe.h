@@ -173,7 +173,8 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
  * Kernel ids: 0 router, 1 top-k, 2 dispatch, 3 gate_up (with its SwiGLU), 4 down, 5 combine,
  * 6 reserved (records nothing), 7 the fused experts of BURNEXT_FUSED_EXPERTS (gate_up, SwiGLU and
  * down as one kernel; ids 3 and 4 then record nothing).  Batches of at most 16 tokens run top-k
- * and dispatch as one kernel, recorded under id 1; id 2 then records nothing. */
+ * and dispatch as one kernel, recorded under id 1; id 2 then records nothing.  A single-token
+ * forward routes inside its gate_up launch (id 3); ids 1 and 2 then record nothing. */
 #define BURNEXT_NUM_KERNELS 8
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t layer, int enable);
 burnext_status burnext_moe_profile_read(burnext_moe_layer_t layer, double *ms_total, uint64_t *launches,
