@@ -98,6 +98,31 @@ def test_decode_steps_match_oracle(D, oracle, case):
     dev.close()
 
 
+@pytest.mark.parametrize("kw", [dict(), dict(window_policy="full", cache_len=300, max_seq_len=700),
+                                dict(experts_bf16=True)])
+def test_decode_batch1_matches_oracle(D, oracle, kw):
+    """Batch-1 decoding: each MoE layer sees a single token, which routes inside its gate_up launch
+    (the top K picked by every workgroup, the records and routing outputs written there) after the
+    router that forms the residual row.  Teacher-forced past cache eviction (two key chunks in the
+    full-window case) against the decoder oracle (with the bf16 rows modelled for experts_bf16, four
+    steps: see test_decode_experts_bf16)."""
+    cfg = _cfg(D, **kw)
+    data = D.make_decoder(cfg, seed=16, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    print(f"[decoder] batch 1 {kw}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=1)
+    orc = oracle.DecoderOracle(data, 1)
+    tok = np.array([57], np.int32)
+    bf = cfg.experts_bf16
+    steps = 4 if bf else cfg.cache_len + 12
+    for pos in range(steps):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        torch.cuda.synchronize()
+        _check_step(oracle, TOL_EXPERTS_BF16 if bf else TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, (kw, pos))
+        tok = o_nxt
+    dev.close()
+
+
 @pytest.mark.parametrize("kw,caller", [
     (dict(sink_tokens=4), 0),                                       # every-other 8-row windows
     (dict(sink_tokens=3, window_policy="fixed", window=5), 0),
