@@ -170,11 +170,10 @@ __global__ __launch_bounds__(NW * 64) void dense_gemv_kernel(DenseArgs a) {
     uint32_t hi[2], lo[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      uint16_t t0[2], t1[2];
-      split_bf16<2>(vv[2 * u], t0);
-      split_bf16<2>(vv[2 * u + 1], t1);
-      hi[u] = (uint32_t)t0[0] | ((uint32_t)t1[0] << 16);
-      lo[u] = (uint32_t)t0[1] | ((uint32_t)t1[1] << 16);
+      uint32_t tp[2];
+      split_bf16x2<2>(vv[2 * u], vv[2 * u + 1], tp);
+      hi[u] = tp[0];
+      lo[u] = tp[1];
     }
     *(uint2 *)(bs + (size_t)j * ldk + 4u * qq) = make_uint2(hi[0], hi[1]);
     *(uint2 *)(bs + (size_t)(16u + j) * ldk + 4u * qq) = make_uint2(lo[0], lo[1]);

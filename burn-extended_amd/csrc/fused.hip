@@ -289,11 +289,10 @@ __global__ __launch_bounds__(kFusedWaves * 64) __attribute__((amdgpu_waves_per_e
           uint32_t pk[NT][4];
 #pragma unroll
           for (int v = 0; v < 8; v += 2) {
-            uint16_t t0[NT], t1[NT];
-            split_bf16<NT>(v8[v], t0);
-            split_bf16<NT>(v8[v + 1], t1);
+            uint32_t tp[NT];
+            split_bf16x2<NT>(v8[v], v8[v + 1], tp);
 #pragma unroll
-            for (int term = 0; term < NT; ++term) pk[term][v >> 1] = (uint32_t)t0[term] | ((uint32_t)t1[term] << 16);
+            for (int term = 0; term < NT; ++term) pk[term][v >> 1] = tp[term];
           }
 #pragma unroll
           for (int term = 0; term < NT; ++term)
@@ -376,13 +375,11 @@ __global__ __launch_bounds__(kFusedWaves * 64) __attribute__((amdgpu_waves_per_e
           if (ks1 == 1u) {
             const float o0 = swiglu_clamp_f(acc[0] + b1l[r0], acc[1] + b1l[r0 + 1u], a.alpha, a.limit);
             const float o1 = swiglu_clamp_f(acc[2] + b1l[r0 + 2u], acc[3] + b1l[r0 + 3u], a.alpha, a.limit);
-            uint16_t t0[NT], t1[NT];
-            split_bf16<NT>(o0, t0);
-            split_bf16<NT>(o1, t1);
+            uint32_t tp[NT];
+            split_bf16x2<NT>(o0, o1, tp);
 #pragma unroll
             for (int term = 0; term < NT; ++term)
-              *(uint32_t *)(act + ((size_t)term * 16u + m0 + i16) * AF + (r0 >> 1)) =
-                  (uint32_t)t0[term] | ((uint32_t)t1[term] << 16);
+              *(uint32_t *)(act + ((size_t)term * 16u + m0 + i16) * AF + (r0 >> 1)) = tp[term];
           } else {
             const bool hb = h == 0u;  // b1 in part 0
             *(float4 *)(pre + ((size_t)h * mtm + i16) * PR + r0) =

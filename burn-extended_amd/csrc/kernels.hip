@@ -1559,11 +1559,10 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
         uint32_t pk[NT][4];
 #pragma unroll
         for (int v = 0; v < 8; v += 2) {
-          uint16_t t0[NT], t1[NT];
-          split_bf16<NT>(v8[v], t0);
-          split_bf16<NT>(v8[v + 1], t1);
+          uint32_t tp[NT];
+          split_bf16x2<NT>(v8[v], v8[v + 1], tp);
 #pragma unroll
-          for (int term = 0; term < NT; ++term) pk[term][v >> 1] = (uint32_t)t0[term] | ((uint32_t)t1[term] << 16);
+          for (int term = 0; term < NT; ++term) pk[term][v >> 1] = tp[term];
         }
 #pragma unroll
         for (int term = 0; term < NT; ++term)

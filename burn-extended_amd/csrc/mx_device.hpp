@@ -39,6 +39,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// The same rounding for two values in one instruction (gfx950's v_cvt_pk_bf16_f32, first value in
+// the low half), checked on all 2^32 inputs against f32_to_bf16_bits.  Used by the activation
+// splits of the GEMV stagings only.
+typedef __bf16 bf16x2_hw_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  const f32x2_hw_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw_t));
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
 // Split an f32 into NT bf16 terms t0 + t1 + ... (each the rounded residual of the previous).
@@ -50,6 +60,19 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t (&t)[NT]) {
   for (int i = 0; i < NT; ++i) {
     t[i] = f32_to_bf16_bits(r);
     r = r - bf16_bits_to_f32(t[i]);
+  }
+}
+
+// The same split for two values at once: term i of (lo, hi) packed as one bf16 pair, lo in the low
+// half.
+template <int NT>
+__device__ __forceinline__ void split_bf16x2(float lo, float hi, uint32_t (&t)[NT]) {
+  float r0 = lo, r1 = hi;
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    t[i] = f32x2_to_bf16x2_bits(r0, r1);
+    r0 = r0 - __uint_as_float(t[i] << 16);
+    r1 = r1 - __uint_as_float(t[i] & 0xFFFF0000u);
   }
 }
 
