@@ -36,7 +36,24 @@ def build(verbose: bool = False) -> pathlib.Path:
     shutil.move(str(tmp), str(LIB))
     for o in objs:
         os.remove(o)
+    build_checks(verbose)
     return LIB
+
+
+# Test-only GPU programs (tests/native/*_check.hip, one executable each in lib/checks/): exhaustive
+# checks of device helpers the library compiles in, run by the GPU tests.
+CHECK_DIR = LIB_DIR / "checks"
+CHECKS = ["bf16_convert_check"]
+
+
+def build_checks(verbose: bool = False) -> list[pathlib.Path]:
+    CHECK_DIR.mkdir(parents=True, exist_ok=True)
+    out = []
+    for name in CHECKS:
+        exe = CHECK_DIR / name
+        _run([HIPCC, *FLAGS, "-o", str(exe), str(PKG.parent / "tests" / "native" / f"{name}.hip")], verbose)
+        out.append(exe)
+    return out
 
 
 # Host-side sanitizers for build_asan: every -fsanitize option is given to the host half of the
