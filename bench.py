@@ -166,7 +166,8 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
     # pass queues its steps in chunks behind a bounded GPU sleep longer than the chunk's enqueue
     # time and its kernels run back to back as in the untimed pass.  (Where the host keeps ahead,
     # the steps go out directly: queued behind a sleep, the prefill GEMMs measured 15% slower under
-    # the kernel tracer too.)
+    # the kernel tracer too, so prefill-sized batches (whose steps are long next to any launch gap)
+    # never queue behind one.)
     for L in layers:
         L.profile_enable(True)
     t0 = time.perf_counter()
@@ -178,7 +179,7 @@ def measure(name, layers, data, steps, warmup, with_cpu, cpu_seconds):
         L.profile_read()
     for L in layers:
         L.profile_enable(True)  # every pass read: its pairs return to the pool
-    gated = host_s > ms_step * 1e-3
+    gated = host_s > ms_step * 1e-3 and T < 1024
     chunk = 20 if gated else steps
     spans = []  # GPU time of each chunk's steps (after its sleep): the measured pass's own step
     for c0 in range(0, steps, chunk):
