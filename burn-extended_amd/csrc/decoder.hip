@@ -17,7 +17,10 @@
 //     burnext_moe_forward  the MoE layer (its own RmsNorm and residual) on the HIP MoE kernels;
 //                       its combine (combine_norm_kernel) also writes the next layer's xn (after
 //                       the last layer: norm_final), so rmsnorm_kernel runs for layer 0 only
-//   dense_gemv_kernel (LM head), logits_kernel + argmax_kernel
+//   LM head: lm_stream_kernel (equal runs of the tiled matrix per wave, logits and each
+//                       workgroup's best per row) + lm_fix_kernel (the tiles cut between runs) for
+//                       batches of at most 8 rows, else dense_gemv_kernel + logits_kernel; then
+//                       argmax_kernel
 //
 // Replaces src/models/gpt_oss.rs:101-113,226-252 and src/attention/streaming_mqa.rs:239-419
 // (Burn tensor ops on WGPU).
@@ -866,6 +869,235 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
   if (t == 0) a.next[b] = bi;
 }
 
+// ---------------------------------------------------------------------------------------------
+// LM head for batches of at most kLmMaxB rows: the K-split partials, their sum and the block
+// maxima of dense_gemv_kernel + logits_kernel in one streaming pass.  The tiled matrix's K-groups,
+// in layout order (tile t, K-group kg at linear index t nkg + kg, (t nkg + kg) KiB), are cut into W
+// contiguous equal runs, one per wave of a persistent grid (kLmWaves waves per workgroup, one
+// workgroup per CU): wave g streams K-groups [g I / W, (g + 1) I / W) of I = ntiles nkg in one
+// register pipeline of kLmSlots K-groups (each slot refilled right after its MFMA), against both
+// terms of the batch rows held in LDS for the whole K range (rows 0 .. B-1 the hi terms, B .. 2B-1
+// the lo terms, one MFMA per K-group with both in its 16 columns).  A tile the wave covers whole
+// ends in its logits (written when requested) and the wave's running best per row (`beats`), which
+// the workgroup reduces to one entry per row (slot blockIdx.x); a tile cut by the boundary g between
+// two runs (at most one cut per tile: runs are at least nkg long) leaves its head part (wave g - 1)
+// and tail part (wave g) in fix[g], which lm_fix_kernel adds; argmax_kernel reduces the entries.
+// Dummy refills past a run's end read the batch rows (resident in L2), not weights.
+// ---------------------------------------------------------------------------------------------
+constexpr uint32_t kLmWaves = 16;
+constexpr uint32_t kLmMaxB = 8;
+constexpr uint32_t kLmSlots = 6;
+constexpr uint32_t kLmMaxK = 4096;
+constexpr uint32_t kLmStage = kLmMaxB * kLmMaxK / 8u / (kLmWaves * 64u);  // batch-row chunks (8 floats) per thread
+
+struct LmArgs {
+  const uint8_t *w;  // tiled [ntiles][nkg] KiB
+  const float *x;    // [B][K]
+  float *logits;     // [B][V] or null
+  float *fix;        // [W][2][B][16]: head (side 0) and tail (side 1) parts of the tile cut at boundary g
+  float *bval;       // [B][nblk]: stream workgroup i's best of row b at b nblk + i, lm_fix_kernel
+                     // workgroup x's at b nblk + nblk_s + x
+  int32_t *bidx;     // [B][nblk]
+  uint64_t iters;    // ntiles * nkg
+  uint32_t iq, ir;   // iters = iq W + ir
+  uint32_t V, K, nkg, B, W, nblk, nblk_s;
+};
+
+// (bv, bi) <- the better of it and lane (lane ^ m)'s (`beats`; kNoIndex for none)
+__device__ __forceinline__ void best_xor(float &bv, int32_t &bi, int m) {
+  const float ov = __shfl_xor(bv, m, 64);
+  const int32_t oi = __shfl_xor(bi, m, 64);
+  if (oi != kNoIndex && (bi == kNoIndex || beats(ov, oi, bv, bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+__global__ __launch_bounds__(kLmWaves * 64) void lm_stream_kernel(LmArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t *bs = (uint16_t *)smem;  // [2B][ldk]
+  constexpr uint32_t CJ = kLmSlots;
+  const uint32_t nkg = a.nkg, Kp = nkg * 32u, ldk = Kp + 8u, B = a.B;
+  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+  const uint32_t gw = blockIdx.x * kLmWaves + wv;
+  const uint64_t beg = (uint64_t)gw * a.iters / a.W, end = (uint64_t)(gw + 1u) * a.iters / a.W;
+  // the batch rows' chunks first (the staging then waits for them alone: loads complete in order)
+  const uint32_t k8 = Kp / 8u, nch = B * k8;
+  // (no branch around a load: chunks outside the rows read row 0's first chunk and are zeroed at use)
+  float4 xv[kLmStage][2];
+#pragma unroll
+  for (uint32_t u = 0; u < kLmStage; ++u) {
+    const uint32_t id = threadIdx.x + u * kLmWaves * 64u, j = id / k8, k = (id - j * k8) * 8u;
+    const bool ok = id < nch && k < a.K;  // K % 8 == 0: a chunk is wholly inside or outside
+    const float *p = a.x + (ok ? (size_t)j * a.K + k : 0u);
+    xv[u][0] = *(const float4 *)p;
+    xv[u][1] = *(const float4 *)(p + 4);
+  }
+  const uint8_t *wl = a.w + lane * 16u;
+  const uint8_t *dummy = (const uint8_t *)a.x + lane * 16u;  // B K 4 >= 1 KiB
+  uint4 abuf[CJ];
+#pragma unroll
+  for (uint32_t j = 0; j < CJ; ++j) abuf[j] = load_stream16(beg + j < end ? wl + (beg + j) * 1024u : dummy);
+#pragma unroll
+  for (uint32_t u = 0; u < kLmStage; ++u) {
+    const uint32_t id = threadIdx.x + u * kLmWaves * 64u, j = id / k8, k = (id - j * k8) * 8u;
+    if (id >= nch) continue;
+    float v8[8] = {xv[u][0].x, xv[u][0].y, xv[u][0].z, xv[u][0].w, xv[u][1].x, xv[u][1].y, xv[u][1].z, xv[u][1].w};
+    if (k >= a.K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v8[e] = 0.0f;
+    }
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      uint32_t tp[2];
+      split_bf16x2<2>(v8[2 * p], v8[2 * p + 1], tp);
+      hi[p] = tp[0];
+      lo[p] = tp[1];
+    }
+    *(uint4 *)(bs + (size_t)j * ldk + k) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *(uint4 *)(bs + (size_t)(B + j) * ldk + k) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  }
+  __syncthreads();
+
+  const uint32_t i16 = lane & 15u, q = lane >> 4;
+  const bool bcol = i16 < 2u * B;
+  const uint16_t *brow = bs + (size_t)min(i16, 2u * B - 1u) * ldk + 8u * q;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float bv = -INFINITY;
+  int32_t bi = kNoIndex;
+  uint32_t tile = (uint32_t)(beg / nkg), kg = (uint32_t)(beg - (uint64_t)tile * nkg), kg_first = kg;
+  for (uint64_t base = beg; base < end; base += CJ) {
+#pragma unroll
+    for (uint32_t j = 0; j < CJ; ++j) {
+      const uint64_t cur = base + j;
+      const bool live = cur < end;  // wave-uniform
+      if (live) {
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        const u32x4_t r = *(const u32x4_t *)(brow + 32u * kg);
+        const u32x4_t raw = bcol ? r : zero;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, abuf[j]), __builtin_bit_cast(bf16x8_t, raw),
+                                                      acc, 0, 0, 0);
+      }
+      // every slot refills, past the run's end with the dummy: a static count of loads in flight
+      const uint64_t nx = cur + CJ;
+      abuf[j] = load_stream16(nx < end ? wl + nx * 1024u : dummy);
+      if (live) {
+        if (kg + 1u == nkg || cur + 1u == end) {
+          // token j's lo column (j + B) onto its hi column j: lanes i16 < B hold rows 4q .. 4q + 3
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) acc[rr] = acc[rr] + __shfl(acc[rr], (int)(lane + B), 64);
+          if (kg_first == 0u && kg + 1u == nkg) {  // whole tile
+            if (i16 < B) {
+#pragma unroll
+              for (uint32_t rr = 0; rr < 4u; ++rr) {
+                const uint32_t row = tile * 16u + 4u * q + rr;
+                if (row < a.V) {
+                  if (a.logits) a.logits[(size_t)i16 * a.V + row] = acc[rr];
+                  if (bi == kNoIndex || beats(acc[rr], (int32_t)row, bv, bi)) {
+                    bv = acc[rr];
+                    bi = (int32_t)row;
+                  }
+                }
+              }
+            }
+          } else if (i16 < B) {  // head (the run ends inside the tile) or tail (it began inside)
+            const uint32_t side = kg_first == 0u ? 0u : 1u, bnd = side == 0u ? gw + 1u : gw;
+            *(float4 *)(a.fix + (((size_t)bnd * 2u + side) * B + i16) * 16u + 4u * q) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+          }
+          acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (++kg == nkg) {
+          kg = 0;
+          kg_first = 0;
+          ++tile;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the run's best per row (lanes i16, i16 + 16, i16 + 32, i16 + 48 hold row i16's candidates),
+  // then the workgroup's over its waves
+  __shared__ float wbv[kLmWaves][kLmMaxB];
+  __shared__ int32_t wbi[kLmWaves][kLmMaxB];
+  best_xor(bv, bi, 16);
+  best_xor(bv, bi, 32);
+  if (q == 0u && i16 < B) {
+    wbv[wv][i16] = bv;
+    wbi[wv][i16] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x < B) {
+    float v = -INFINITY;
+    int32_t ix = kNoIndex;
+    for (uint32_t w = 0; w < kLmWaves; ++w) {
+      const int32_t oi = wbi[w][threadIdx.x];
+      if (oi != kNoIndex && (ix == kNoIndex || beats(wbv[w][threadIdx.x], oi, v, ix))) {
+        v = wbv[w][threadIdx.x];
+        ix = oi;
+      }
+    }
+    a.bval[(size_t)threadIdx.x * a.nblk + blockIdx.x] = v;
+    a.bidx[(size_t)threadIdx.x * a.nblk + blockIdx.x] = ix;
+  }
+}
+
+// The tiles cut between two runs: head + tail per row, logits when requested, and each
+// workgroup's best per row (slot nblk_s + blockIdx.x; boundary 0 and cuts on tile edges give no
+// candidate).  Workgroup (x, j): boundaries g = 256 x + t of batch row j.  The cuts
+// g I / W = g q + (g r) / W (I = q W + r) in 32-bit arithmetic.
+__global__ __launch_bounds__(256) void lm_fix_kernel(LmArgs a) {
+  const uint32_t j = blockIdx.y, t = threadIdx.x, g = blockIdx.x * 256u + t;
+  float bv = -INFINITY;
+  int32_t bi = kNoIndex;
+  if (g > 0u && g < a.W) {
+    const uint32_t cut = g * a.iq + (g * a.ir) / a.W;
+    const uint32_t tile = cut / a.nkg;
+    if (cut != tile * a.nkg) {
+      const float *hp = a.fix + (((size_t)g * 2u + 0u) * a.B + j) * 16u;
+      const float *tp = a.fix + (((size_t)g * 2u + 1u) * a.B + j) * 16u;
+      float h[16], u[16];
+#pragma unroll
+      for (uint32_t i = 0; i < 16u; i += 4u) {
+        *(float4 *)(h + i) = *(const float4 *)(hp + i);
+        *(float4 *)(u + i) = *(const float4 *)(tp + i);
+      }
+#pragma unroll
+      for (uint32_t i = 0; i < 16u; ++i) {
+        const uint32_t row = tile * 16u + i;
+        if (row < a.V) {
+          const float v = h[i] + u[i];
+          if (a.logits) a.logits[(size_t)j * a.V + row] = v;
+          if (bi == kNoIndex || beats(v, (int32_t)row, bv, bi)) {
+            bv = v;
+            bi = (int32_t)row;
+          }
+        }
+      }
+    }
+  }
+  __shared__ float wbv[4];
+  __shared__ int32_t wbi[4];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) best_xor(bv, bi, m);
+  if ((t & 63u) == 0u) {
+    wbv[t >> 6] = bv;
+    wbi[t >> 6] = bi;
+  }
+  __syncthreads();
+  if (t == 0u) {
+    float v = -INFINITY;
+    int32_t ix = kNoIndex;
+    for (uint32_t w = 0; w < 4u; ++w)
+      if (wbi[w] != kNoIndex && (ix == kNoIndex || beats(wbv[w], wbi[w], v, ix))) {
+        v = wbv[w];
+        ix = wbi[w];
+      }
+    a.bval[(size_t)j * a.nblk + a.nblk_s + blockIdx.x] = v;
+    a.bidx[(size_t)j * a.nblk + a.nblk_s + blockIdx.x] = ix;
+  }
+}
+
 // f32 rows [B][len][kvH][dk] of one layer -> cache slots 0 .. len-1 (k_index or v_index layout).
 struct CacheLoadArgs {
   const float *src;
@@ -965,6 +1197,22 @@ struct GWs {
   uint32_t nblk;
 };
 
+// The streaming LM head (lm_stream_kernel) serves batches of at most kLmMaxB rows whose d_model
+// fits its LDS staging (K <= kLmMaxK, K % 8 == 0, a batch of at least 1 KiB for the dummy refills)
+// and vocabularies of at least one row tile per wave of one workgroup (and fewer than 2^32
+// K-groups: lm_fix_kernel's 32-bit cuts).
+bool lm_stream_ok(const burnext_gptoss &M, uint32_t B) {
+  const uint32_t K = M.lm.K;
+  return B >= 1u && B <= kLmMaxB && K <= kLmMaxK && K % 8u == 0u && (uint64_t)B * K * 4u >= 1024u &&
+         M.lm.ntiles >= kLmWaves && (uint64_t)M.lm.ntiles * M.lm.nkg < (1ull << 32);
+}
+// Its waves: one workgroup per CU, at most one wave per row tile (so every run spans at least nkg
+// K-groups and a tile is cut at most once).
+uint32_t lm_waves(const burnext_gptoss &M) {
+  return std::min<uint32_t>((uint32_t)M.num_cus, M.lm.ntiles / kLmWaves) * kLmWaves;
+}
+size_t lm_lds_bytes(uint32_t B, uint32_t nkg) { return 2ull * B * (nkg * 32u + 8u) * 2u; }
+
 GWs gptoss_ws(const burnext_gptoss &M, uint32_t B, uint64_t moe_bytes) {
   GWs w{};
   uint64_t off = 0;
@@ -974,11 +1222,14 @@ GWs gptoss_ws(const burnext_gptoss &M, uint32_t B, uint64_t moe_bytes) {
     return o;
   };
   const auto &c = M.cfg;
-  uint64_t part_elems = (uint64_t)M.lm.parts * B * M.lm.N;
+  const bool lm_stream = lm_stream_ok(M, B);
+  const uint32_t lw = lm_waves(M);
+  // the LM head's partials (K-split path) or its cut tiles' parts (streaming path)
+  uint64_t part_elems = lm_stream ? (uint64_t)lw * 2u * B * 16u : (uint64_t)M.lm.parts * B * M.lm.N;
   for (const auto &m : M.qkv) part_elems = std::max<uint64_t>(part_elems, (uint64_t)m.parts * B * m.N);
   for (const auto &m : M.wo) part_elems = std::max<uint64_t>(part_elems, (uint64_t)m.parts * B * m.N);
   const uint64_t max_chunks = cdiv(c.cache_len, kAttnChunk);
-  w.nblk = (uint32_t)cdiv(c.vocab_size, kLogitsPerBlock);
+  w.nblk = lm_stream ? lw / kLmWaves + (uint32_t)cdiv(lw, 256) : (uint32_t)cdiv(c.vocab_size, kLogitsPerBlock);
   w.hid = take((uint64_t)B * c.d_model * 4);
   w.hid2 = take((uint64_t)B * c.d_model * 4);
   w.xn = take((uint64_t)B * c.d_model * 4);
@@ -1251,6 +1502,11 @@ burnext_status burnext_gptoss_create(const burnext_gptoss_config *cfg, const bur
   M->cap_p = (uint32_t)align_up(c.cache_len, 64);
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) M->num_cus = cus;
+  if (hipFuncSetAttribute((const void *)lm_stream_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lm_lds_bytes(kLmMaxB, kLmMaxK / 32u)) != hipSuccess) {
+    delete M;
+    return set_error(BURNEXT_DEVICE_ERROR, "hipFuncSetAttribute (LM head LDS) failed");
+  }
   M->moe.assign(moe_layers, moe_layers + c.n_layers);
   burnext_status st = upload(M, &M->emb, w->tok_emb, (size_t)V * D);
   auto up_dense = [&](DenseMat &m, const DenseMat &geom, const std::vector<uint16_t> &t) -> burnext_status {
@@ -1500,11 +1756,36 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     st = hip_check(launch_kernel(rmsnorm_kernel, dim3(B), dim3(256), 0, s, nf), "final RmsNorm launch");
     if (st != BURNEXT_OK) return st;
   }
-  st = dense_gemv(M->lm, xn, B, part, s);
-  if (st != BURNEXT_OK) return st;
-  LogitsArgs la{part, (uint64_t)B * c.vocab_size, M->lm.parts, c.vocab_size, w.nblk, logits, bval, bidx};
-  st = hip_check(launch_kernel(logits_kernel, dim3(w.nblk, B), dim3(256), 0, s, la), "logits launch");
-  if (st != BURNEXT_OK) return st;
+  if (lm_stream_ok(*M, B)) {
+    LmArgs la{};
+    la.w = M->lm.w;
+    la.x = xn;
+    la.logits = logits;
+    la.fix = part;
+    la.bval = bval;
+    la.bidx = bidx;
+    la.iters = (uint64_t)M->lm.ntiles * M->lm.nkg;
+    la.V = c.vocab_size;
+    la.K = M->lm.K;
+    la.nkg = M->lm.nkg;
+    la.B = B;
+    la.W = lm_waves(*M);
+    la.iq = (uint32_t)(la.iters / la.W);
+    la.ir = (uint32_t)(la.iters % la.W);
+    la.nblk = w.nblk;
+    la.nblk_s = la.W / kLmWaves;
+    st = hip_check(launch_kernel(lm_stream_kernel, dim3(la.W / kLmWaves), dim3(kLmWaves * 64), lm_lds_bytes(B, la.nkg), s, la),
+                   "LM head launch");
+    if (st != BURNEXT_OK) return st;
+    st = hip_check(launch_kernel(lm_fix_kernel, dim3((uint32_t)cdiv(la.W, 256), B), dim3(256), 0, s, la), "LM head fix-up launch");
+    if (st != BURNEXT_OK) return st;
+  } else {
+    st = dense_gemv(M->lm, xn, B, part, s);
+    if (st != BURNEXT_OK) return st;
+    LogitsArgs la{part, (uint64_t)B * c.vocab_size, M->lm.parts, c.vocab_size, w.nblk, logits, bval, bidx};
+    st = hip_check(launch_kernel(logits_kernel, dim3(w.nblk, B), dim3(256), 0, s, la), "logits launch");
+    if (st != BURNEXT_OK) return st;
+  }
   ArgmaxArgs ga{bval, bidx, w.nblk, next_tokens};
   st = hip_check(launch_kernel(argmax_kernel, dim3(B), dim3(256), 0, s, ga), "argmax launch");
   if (st != BURNEXT_OK) return st;

@@ -161,6 +161,28 @@ def test_decode_sink_tokens(D, oracle, kw, caller):
     dev.close()
 
 
+@pytest.mark.parametrize("vocab,B", [(1000, 1), (1000, 5), (1000, 8), (4099, 3), (1000, 12), (509, 16)])
+def test_decode_lm_head_paths(D, oracle, vocab, B):
+    """The LM head's two paths against the oracle's logits and greedy tokens: batches of at most 8
+    rows stream the matrix in equal runs of K-groups, one per wave (vocabularies of 1000 and 4099
+    rows: runs that cut row tiles, whose two parts the fix-up kernel adds, and a last tile of 8 or 3
+    rows); 12 and 16 rows take the K-split GEMV and the logits kernel."""
+    cfg = _cfg(D, vocab_size=vocab)
+    data = D.make_decoder(cfg, seed=17, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
+    print(f"[decoder] LM head vocab={vocab} B={B}", flush=True)
+    dev = D.GptOssDecoder(data, max_batch=B)
+    orc = oracle.DecoderOracle(data, B)
+    rng = np.random.default_rng(3)
+    tok = rng.integers(0, cfg.vocab_size, B).astype(np.int32)
+    for pos in range(4):
+        nxt, lg, hid = dev.decode(torch.from_numpy(tok).cuda(), pos, logits=True, hidden=True)
+        o_nxt, o_lg, o_hid = orc.step(tok, pos)
+        torch.cuda.synchronize()
+        _check_step(oracle, TOL_F32, nxt, lg, hid, o_nxt, o_lg, o_hid, (vocab, B, pos))
+        tok = o_nxt
+    dev.close()
+
+
 def test_decode_bf16_cache(D, oracle):
     cfg = _cfg(D, kv_bf16=True)
     data = D.make_decoder(cfg, seed=12, sinks_std=0.8, norm_std=0.1, moe_dtype="f32")
