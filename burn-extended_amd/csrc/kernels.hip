@@ -1732,6 +1732,167 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(3)
 }
 
 // ---------------------------------------------------------------------------------------------
+// Down projection + combine of a single-token batch (top-k K <= 4, the down K range in
+// kDownSplitFew parts): workgroup r (one per 16-row tile of the D outputs) of 16 waves; wave w
+// takes slot p = w / 4 (expert topk_idx[p], SwiGLU row pos_of[p]) and K-part h = w % 4 of tile r --
+// the down GEMV's work unit, with its operand layout, K order, NT-term B rows (both terms in the
+// columns of one MFMA) and bias in part 0 -- and leaves its 16 rows in LDS; threads 0..15 then
+// add them as combine_kernel does (parts in order, slots ascending, acc + part sum x w_p, then
+// x + acc): the same bits as the two launches, one launch fewer.  Waves of slots >= K take no
+// unit.  The B rows are requested before the weights (loads complete in order).
+// ---------------------------------------------------------------------------------------------
+size_t down_combine1_lds_bytes(int nt, uint32_t nb) {
+  return (size_t)kDownComb1MaxK * (size_t)nt * (nb * 32u + 8u) * 2u + kDownComb1MaxK * kDownSplitFew * 16u * 4u;
+}
+
+template <int NT, typename XT>
+__global__ __launch_bounds__(1024) void down_combine1_kernel(DownComb1Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr uint32_t CJ = kGemvKgPerWave;
+  const uint32_t Kp = a.nb * 32u, ldk = Kp + 8u, K = a.K;
+  uint16_t *bs = (uint16_t *)smem;  // [slot][term][ldk]
+  float *red = (float *)(smem + (size_t)kDownComb1MaxK * NT * ldk * 2u);  // [slot][part][16]
+  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+  const uint32_t p = wv >> 2, h = wv & 3u, rt = blockIdx.x;
+  const bool live = p < K;  // wave-uniform
+  const uint32_t i16 = lane & 15u, q = lane >> 4;
+  const uint32_t nkg = (a.nb + 3u) >> 2, tail = a.nb - 4u * (nkg - 1u);
+  const uint32_t H = (nkg + kDownSplitFew - 1u) / kDownSplitFew;  // the down GEMV's parts
+  const uint32_t kg0 = min(h * H, nkg), kg1 = min(kg0 + H, nkg);
+  // B staging: chunk c = thread + 1024 u of slot c / k8n, inputs 8 (c % k8n) ..
+  const uint32_t k8n = Kp >> 3, nitm = K * k8n;
+  constexpr uint32_t SB = (kDownComb1MaxK * kDownComb1MaxKp / 8u + 1023u) / 1024u;  // chunks per thread
+  int32_t pos[SB];
+#pragma unroll
+  for (uint32_t u = 0; u < SB; ++u) {
+    const uint32_t id = min(threadIdx.x + u * 1024u, nitm - 1u);
+    pos[u] = a.pos_of[id / k8n];
+  }
+  const int32_t e = a.topk_idx[live ? p : 0u];
+  Chunk8<float> cx[SB];
+#pragma unroll
+  for (uint32_t u = 0; u < SB; ++u) {
+    const uint32_t id = min(threadIdx.x + u * 1024u, nitm - 1u), j = id / k8n, kb = (id - j * k8n) * 8u;
+    chunk_load(cx[u], a.act + (size_t)pos[u] * a.act_stride + kb);
+  }
+  const uint8_t *wt = a.wb + (size_t)e * a.wb_estride + (size_t)rt * a.nb * 256u;
+  const uint8_t *stp = a.ws + (size_t)e * a.ws_estride + (size_t)rt * a.nb * 16u;
+  auto lane_ok = [&](uint32_t kg) { return kg < kg1 && q < (kg + 1u == nkg ? tail : 4u); };
+  uint4 abuf[CJ];
+  uint32_t sbuf[CJ];
+#pragma unroll
+  for (uint32_t j = 0; j < CJ; ++j) {
+    const uint32_t kg = kg0 + j;
+    const bool ok = lane_ok(kg);
+    abuf[j] = load_stream16(wt + (ok ? kg * 1024u + lane * 16u : 0u));
+    sbuf[j] = *(const uint32_t *)(stp + (ok ? kg * 64u + (lane & ~3u) : 0u));
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < SB; ++u) {
+    const uint32_t id = threadIdx.x + u * 1024u;
+    if (id >= nitm) continue;
+    const uint32_t j = id / k8n, kb = (id - j * k8n) * 8u;
+    float v8[8];
+    chunk_vals(cx[u], v8);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) v8[v] = kb + (uint32_t)v < a.kt ? v8[v] : 0.0f;
+    uint32_t pk[NT][4];
+#pragma unroll
+    for (int v = 0; v < 8; v += 2) {
+      uint32_t tp[NT];
+      split_bf16x2<NT>(v8[v], v8[v + 1], tp);
+#pragma unroll
+      for (int term = 0; term < NT; ++term) pk[term][v >> 1] = tp[term];
+    }
+#pragma unroll
+    for (int term = 0; term < NT; ++term)
+      *(uint4 *)(bs + ((size_t)j * NT + term) * ldk + kb) = make_uint4(pk[term][0], pk[term][1], pk[term][2], pk[term][3]);
+  }
+  __syncthreads();
+  if (live) {
+    // B column i16: term i16 of this slot's row (columns >= NT zero)
+    const bool bcol = i16 < (uint32_t)NT;
+    const uint16_t *brow = bs + ((size_t)p * NT + min(i16, (uint32_t)NT - 1u)) * ldk;
+    const uint32_t sshift = 8u * (lane & 3u);
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t s0 = kg0; s0 < kg1; s0 += CJ) {
+#pragma unroll
+      for (uint32_t j = 0; j < CJ; ++j) {
+        const uint32_t kg = s0 + j;
+        const bool ok = lane_ok(kg);
+        const bool bok = bcol && ok;
+        const float sc = ok ? e8m0_to_f32((sbuf[j] >> sshift) & 0xFFu) : 1.0f;
+        const uint32_t kb = ok ? 32u * (4u * kg + q) : 0u;
+        const uint32_t wd[4] = {abuf[j].x, abuf[j].y, abuf[j].z, abuf[j].w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const bf16x8_t A = fp4x8_to_bf16x8(wd[s], sc);
+          const u32x4_t r = *(const u32x4_t *)(brow + kb + 8u * s);
+          const u32x4_t zero = {0u, 0u, 0u, 0u};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8_t, bok ? r : zero), acc, 0, 0, 0);
+        }
+        // next step's K-group j (a part longer than CJ K-groups; else the tile's first block again)
+        const uint32_t nkg_ = kg + CJ;
+        const bool nok = lane_ok(nkg_);
+        abuf[j] = load_stream16(wt + (nok ? nkg_ * 1024u + lane * 16u : 0u));
+        sbuf[j] = *(const uint32_t *)(stp + (nok ? nkg_ * 64u + (lane & ~3u) : 0u));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if constexpr (NT == 2) {  // the lo term's column 1 onto column 0
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] + __shfl(acc[r], (int)(lane + 1u), 64);
+    }
+    if (i16 == 0u) {
+      const uint32_t r0 = rt * 16u + 4u * q;
+      const f32x4_t b4 = h ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}
+                           : *(const f32x4_t *)(a.bias + (size_t)e * a.bias_estride + r0);
+      *(float4 *)(red + (p * kDownSplitFew + h) * 16u + 4u * q) =
+          make_float4(acc[0] + b4[0], acc[1] + b4[1], acc[2] + b4[2], acc[3] + b4[3]);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16u) {
+    const uint32_t row = rt * 16u + threadIdx.x;
+    if (row < a.D) {
+      float acc = 0.0f;
+      for (uint32_t pp = 0; pp < K; ++pp) {
+        const float *rp = red + pp * kDownSplitFew * 16u + threadIdx.x;
+        float v = rp[0];
+#pragma unroll
+        for (uint32_t hh = 1; hh < kDownSplitFew; ++hh) v = v + rp[hh * 16u];
+        acc = acc + v * a.topk_w[pp];
+      }
+      const XT *x = (const XT *)a.x;
+      XT *y = (XT *)a.y;
+      float xv = 0.0f;
+      if (a.add_residual) {
+        if constexpr (sizeof(XT) == 2) xv = bf16_bits_to_f32(x[row]);
+        else xv = x[row];
+      }
+      if constexpr (sizeof(XT) == 2) {
+        y[row] = f32_to_bf16_bits(xv + acc);
+      } else {
+        y[row] = xv + acc;
+      }
+    }
+  }
+}
+
+hipError_t launch_down_combine1(const DownComb1Args &a, int nt, bool x_bf16, hipStream_t s) {
+  if (a.K == 0u || a.K > kDownComb1MaxK || a.nb * 32u > kDownComb1MaxKp || a.D == 0u || a.nrt * 16u < a.D)
+    return hipErrorInvalidValue;
+  const size_t lds = down_combine1_lds_bytes(nt, a.nb);
+  const dim3 grid((a.D + 15u) / 16u), block(1024);
+  if (nt == 1) {
+    return x_bf16 ? launch_kernel(down_combine1_kernel<1, uint16_t>, grid, block, lds, s, a)
+                  : launch_kernel(down_combine1_kernel<1, float>, grid, block, lds, s, a);
+  }
+  if (nt == 2 && !x_bf16) return launch_kernel(down_combine1_kernel<2, float>, grid, block, lds, s, a);
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------------------
 // Combine: y[t, d] = (add_residual ? x[t, d] : 0) + sum_{p asc} yslot[t*K + p, d] * w_p, where the
 // down projection already wrote yslot = down_p + b2[e_p] token-major (f32, in NP K-parts, or bf16
 // when PB).  Every load of a thread is independent of the others (one memory round trip); four
@@ -1952,6 +2113,9 @@ hipError_t configure_kernels() {
                                big - (int)fa_.sharedSizeBytes);                                                      \
     if (e_ != hipSuccess && err == hipSuccess) err = e_;                                                             \
   } while (0)
+  BX_ATTR((down_combine1_kernel<1, uint16_t>));
+  BX_ATTR((down_combine1_kernel<1, float>));
+  BX_ATTR((down_combine1_kernel<2, float>));
   BX_ATTR((router_kernel<float, float, true>));
   BX_ATTR((router_kernel<float, uint16_t, true>));
   BX_ATTR((router_kernel<uint16_t, float, true>));

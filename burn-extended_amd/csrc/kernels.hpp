@@ -128,6 +128,29 @@ struct GemvArgs {
   RouteOut rout;
 };
 
+// Single-token batches (top-k <= kDownComb1MaxK) whose down projection takes kDownSplitFew K-parts:
+// the down GEMV and the combine in one launch (down_combine1_kernel).  Weights, biases and geometry
+// as GemvArgs (down); act the gate_up launch's SwiGLU rows [pos][act_stride] f32 (position
+// pos_of[p] for slot p); y[d] = x[d] (add_residual, else 0) + sum over slots p (ascending) of
+// w_p * (sum of the 4 parts).  K inputs (F padded to 32) at most kDownComb1MaxKp.
+constexpr uint32_t kDownComb1MaxK = 4;
+constexpr uint32_t kDownComb1MaxKp = 4096;
+struct DownComb1Args {
+  const uint8_t *wb, *ws;
+  uint64_t wb_estride, ws_estride;
+  const float *bias;  // b2 [E, rows_p]
+  uint32_t bias_estride, nrt, nb, kt, D, K;
+  const float *act;
+  uint32_t act_stride;
+  const int32_t *topk_idx, *pos_of;
+  const float *topk_w;
+  const void *x;  // [D] x dtype (token 0)
+  void *y;        // [D] x dtype
+  uint32_t add_residual;
+};
+hipError_t launch_down_combine1(const DownComb1Args &a, int nt, bool x_bf16, hipStream_t s);
+size_t down_combine1_lds_bytes(int nt, uint32_t nb);
+
 // Routing of a decode-sized batch (n <= kSmallRouteMaxTokens) by one workgroup: top-k, softmax,
 // dispatch, all outputs to global.
 struct SmallRouteArgs {

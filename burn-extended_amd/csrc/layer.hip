@@ -1002,6 +1002,34 @@ burnext_status forward_impl(burnext_moe_layer *L, const void *x, burnext_dtype x
   };
   st = gemv(true);
   if (st != BURNEXT_OK) return st;
+  // a single token routed in gate_up, down in kDownSplitFew parts and no fused norm: the down
+  // projection and the combine in one launch (down_combine1_kernel, the same arithmetic)
+  if (route1 && ksplit == kDownSplitFew && !pn && L->K <= kDownComb1MaxK && L->w2.nb * 32u <= kDownComb1MaxKp &&
+      (nt == 1 || !xb)) {
+    DownComb1Args d{};
+    d.wb = L->w2.blocks;
+    d.ws = L->w2.scales;
+    d.wb_estride = L->w2.blocks_per_expert;
+    d.ws_estride = L->w2.scales_per_expert;
+    d.bias = L->b2;
+    d.bias_estride = L->w2.rows_p;
+    d.nrt = L->w2.nrt;
+    d.nb = L->w2.nb;
+    d.kt = L->w2.cols;
+    d.D = L->D;
+    d.K = L->K;
+    d.act = p.act;
+    d.act_stride = L->Fp;
+    d.topk_idx = p.topk_idx;
+    d.pos_of = p.pos_of;
+    d.topk_w = p.topk_w;
+    d.x = x;
+    d.y = y;
+    d.add_residual = (flags & BURNEXT_ADD_RESIDUAL) ? 1u : 0u;
+    ProfScope ps(L, s, kKDown);
+    st = check_launch(launch_down_combine1(d, nt, xb, s), "down + combine launch");
+    return st == BURNEXT_OK ? ok() : st;
+  }
   st = gemv(false);
   if (st != BURNEXT_OK) return st;
 

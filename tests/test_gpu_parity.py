@@ -300,6 +300,25 @@ def test_forward_flags_f32(M, oracle, flags):
     assert oracle.max_abs_rel(y, y_ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("D,F,E,K,dtype,flags", [
+    (2880, 2880, 128, 4, "bf16", 3), (2880, 2880, 32, 4, "f32", 3), (600, 520, 8, 3, "f32", 1),
+    (600, 520, 8, 4, "bf16", 0), (600, 520, 8, 2, "f32", 2), (2880, 2880, 32, 6, "bf16", 3)])
+def test_forward_single_token(M, oracle, D, F, E, K, dtype, flags):
+    """Single-token forwards: the routing inside the gate_up launch and, where the down projection
+    takes 4 K-parts and top-k <= 4, the down projection and the combine in one launch
+    (down_combine1_kernel: slots, parts, bias in part 0, residual or not, bf16 or f32 rows; D = 600
+    ends in an 8-row tile, F = 520 in a K-group of one block); top-6 keeps the two launches."""
+    from burnext_amd import synth
+    L = _make(synth, D, F, E, K, seed=5, dtype=dtype, with_gamma=True)
+    x = synth.make_tokens(1, D, seed=6, dtype=dtype)
+    print(f"[parity] single token D={D} F={F} E={E} K={K} {dtype} flags={flags}", flush=True)
+    y, y_ref = _forward_case(M, oracle, L, x, dtype, flags=flags)
+    err = oracle.max_abs_rel(y, y_ref)
+    moe_err = oracle.max_abs_rel(y - (x if flags & 2 else 0), y_ref - (x if flags & 2 else 0))
+    tol = TOL_F32 if dtype == "f32" else TOL_BF16
+    assert err <= tol and moe_err <= tol, (err, moe_err)
+
+
 def test_forward_20b_decode_bf16(M, oracle):
     """Config 2 (GPT-OSS-20B MoE, T=8, bf16), interleaved gate_up."""
     from burnext_amd import synth
