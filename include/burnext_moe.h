@@ -174,7 +174,9 @@ burnext_status burnext_mxfp4_dequant(const burnext_mxfp4_desc *desc, const uint8
  * 6 reserved (records nothing), 7 the fused experts of BURNEXT_FUSED_EXPERTS (gate_up, SwiGLU and
  * down as one kernel; ids 3 and 4 then record nothing).  Batches of at most 16 tokens run top-k
  * and dispatch as one kernel, recorded under id 1; id 2 then records nothing.  A single-token
- * forward routes inside its gate_up launch (id 3); ids 1 and 2 then record nothing. */
+ * forward routes inside its gate_up launch (id 3); ids 1 and 2 then record nothing, and where its
+ * down projection runs with the combine in one launch (top-k <= 4, no fused norm) that launch is
+ * recorded under id 4 and id 5 records nothing. */
 #define BURNEXT_NUM_KERNELS 8
 burnext_status burnext_moe_profile_enable(burnext_moe_layer_t layer, int enable);
 burnext_status burnext_moe_profile_read(burnext_moe_layer_t layer, double *ms_total, uint64_t *launches,
