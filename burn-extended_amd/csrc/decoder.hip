@@ -223,25 +223,49 @@ struct QkvPostArgs {
   uint32_t B, nH, kvH, dk, cap_p, slot, pos, head_stride;
 };
 
-template <typename KV>
+// P > 0: exactly P parts, all of a thread's loads (its P part pairs, bias pair and RoPE pair)
+// requested before any is used -- one memory round trip (a loop over a run-time part count waits
+// for each part in turn); P = 0: a.parts parts in a loop.
+template <typename KV, uint32_t P>
 __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   const uint32_t b = blockIdx.y, qd = a.nH * a.dk, kd = a.kvH * a.dk, N = qd + 2u * kd;
   const uint32_t pr = blockIdx.x * blockDim.x + threadIdx.x;
   if (pr >= N / 2u) return;
   const uint32_t o = 2u * pr;
-  float s0 = 0.0f, s1 = 0.0f;
-  for (uint32_t h = 0; h < a.parts; ++h) {
-    const float2 p = *(const float2 *)(a.part + (size_t)h * a.part_stride + (size_t)b * N + o);
-    s0 = s0 + p.x;
-    s1 = s1 + p.y;
-  }
-  const float x0 = s0 + a.bias[o], x1 = s1 + a.bias[o + 1u];
   const uint32_t half = a.dk / 2u;
+  const bool rot = o < qd + kd;  // q or k: rotate
+  const uint32_t local = o < qd ? o : (rot ? o - qd : o - qd - kd), hh = local / a.dk, i = (local - hh * a.dk) / 2u;
+  const uint32_t p = a.pos + hh * a.head_stride;
+  float2 cs = make_float2(1.0f, 0.0f);
+  float s0 = 0.0f, s1 = 0.0f;
+  const float *pp = a.part + (size_t)b * N + o;
+  if constexpr (P > 0) {
+    float2 pv[P];
+#pragma unroll
+    for (uint32_t h = 0; h < P; ++h) pv[h] = *(const float2 *)(pp + (size_t)h * a.part_stride);
+    const float2 bv = *(const float2 *)(a.bias + o);
+    const float2 csl = *(const float2 *)(a.rope + ((size_t)p * half + i) * 2u);  // in the table for v rows too
+    if (rot) cs = csl;
+#pragma unroll
+    for (uint32_t h = 0; h < P; ++h) {
+      s0 = s0 + pv[h].x;
+      s1 = s1 + pv[h].y;
+    }
+    s0 = s0 + bv.x;
+    s1 = s1 + bv.y;
+  } else {
+    for (uint32_t h = 0; h < a.parts; ++h) {
+      const float2 v = *(const float2 *)(pp + (size_t)h * a.part_stride);
+      s0 = s0 + v.x;
+      s1 = s1 + v.y;
+    }
+    s0 = s0 + a.bias[o];
+    s1 = s1 + a.bias[o + 1u];
+    if (rot) cs = *(const float2 *)(a.rope + ((size_t)p * half + i) * 2u);
+  }
+  const float x0 = s0, x1 = s1;
   KV *kc = (KV *)a.kc, *vc = (KV *)a.vc;
-  if (o < qd + kd) {  // q or k: rotate
-    const uint32_t local = o < qd ? o : o - qd, hh = local / a.dk, i = (local - hh * a.dk) / 2u;
-    const uint32_t p = a.pos + hh * a.head_stride;
-    const float2 cs = *(const float2 *)(a.rope + ((size_t)p * half + i) * 2u);
+  if (rot) {
     const float y0 = x0 * cs.x - x1 * cs.y, y1 = x1 * cs.x + x0 * cs.y;
     if (o < qd) {
       *(float2 *)(a.qbuf + (size_t)b * qd + local) = make_float2(y0, y1);
@@ -251,6 +275,21 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   } else {
     const uint32_t local = o - qd - kd, hh = local / a.dk;
     kv_store2(vc + v_index(b, hh, a.slot, local - hh * a.dk, a.kvH, a.cap_p, a.dk), x0, x1);
+  }
+}
+
+template <typename KV>
+hipError_t launch_qkv_post(const QkvPostArgs &a, dim3 grid, hipStream_t s) {
+  switch (a.parts) {  // the part counts dense_plan gives (1 .. 8 at d_model <= 4096): one round trip
+    case 1: return launch_kernel(qkv_post_kernel<KV, 1>, grid, dim3(256), 0, s, a);
+    case 2: return launch_kernel(qkv_post_kernel<KV, 2>, grid, dim3(256), 0, s, a);
+    case 3: return launch_kernel(qkv_post_kernel<KV, 3>, grid, dim3(256), 0, s, a);
+    case 4: return launch_kernel(qkv_post_kernel<KV, 4>, grid, dim3(256), 0, s, a);
+    case 5: return launch_kernel(qkv_post_kernel<KV, 5>, grid, dim3(256), 0, s, a);
+    case 6: return launch_kernel(qkv_post_kernel<KV, 6>, grid, dim3(256), 0, s, a);
+    case 7: return launch_kernel(qkv_post_kernel<KV, 7>, grid, dim3(256), 0, s, a);
+    case 8: return launch_kernel(qkv_post_kernel<KV, 8>, grid, dim3(256), 0, s, a);
+    default: return launch_kernel(qkv_post_kernel<KV, 0>, grid, dim3(256), 0, s, a);
   }
 }
 
@@ -1679,8 +1718,7 @@ burnext_status burnext_gptoss_decode(burnext_gptoss_t M, const int32_t *tokens, 
     qa.pos = pos;
     qa.head_stride = c.rope_head_stride;
     const dim3 qgrid((uint32_t)cdiv(N3 / 2, 256), B);
-    st = hip_check(c.kv_bf16 ? launch_kernel(qkv_post_kernel<uint16_t>, qgrid, dim3(256), 0, s, qa)
-                             : launch_kernel(qkv_post_kernel<float>, qgrid, dim3(256), 0, s, qa),
+    st = hip_check(c.kv_bf16 ? launch_qkv_post<uint16_t>(qa, qgrid, s) : launch_qkv_post<float>(qa, qgrid, s),
                    "q/k/v post launch");
     if (st != BURNEXT_OK) return st;
     const uint32_t lw = layer_window(c, l, window);  // 0 = Full
