@@ -1192,22 +1192,25 @@ __global__ __launch_bounds__(512) void router_front_kernel(PreFrontArgs a) {
   if (c < nc) {
     const size_t o = (size_t)t * D + 8u * c;
     float sv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    Chunk8<float> rc, bc;  // requested with the parts: one round trip
+    chunk_load(rc, a.resid + o);
+    chunk_load(bc, a.bias + 8u * c);
     for (uint32_t h0 = 0; h0 < a.nparts; h0 += 8u) {
       Chunk8<float> pc[8];
 #pragma unroll
       for (uint32_t u = 0; u < 8u; ++u) chunk_load(pc[u], a.part + (size_t)min(h0 + u, a.nparts - 1u) * a.part_stride + o);
+      // every part's add is unconditional (+0 for the clamped reloads past nparts: sv starts at +0
+      // and is never -0, so sv + 0 == sv): a conditional add let the compiler sink each load into
+      // its branch and wait for the parts one at a time
 #pragma unroll
       for (uint32_t u = 0; u < 8u; ++u) {
-        if (h0 + u >= a.nparts) break;
         float pv[8];
         chunk_vals(pc[u], pv);
+        const bool use = h0 + u < a.nparts;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sv[j] = sv[j] + pv[j];
+        for (int j = 0; j < 8; ++j) sv[j] = sv[j] + (use ? pv[j] : 0.0f);
       }
     }
-    Chunk8<float> rc, bc;
-    chunk_load(rc, a.resid + o);
-    chunk_load(bc, a.bias + 8u * c);
     float rv[8], bv[8], xv[8];
     chunk_vals(rc, rv);
     chunk_vals(bc, bv);
@@ -2018,6 +2021,9 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
         for (int h = 1; h < NP; ++h) yh[h - 1][r][u] = *(const float4 *)(yp + h * a.part_stride + row);
       }
     }
+    // every request of the pass is out before the sums consume any (the scheduler otherwise
+    // interleaves them slot by slot, one memory round trip per slot)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int h = 1; h < NP; ++h)
 #pragma unroll
