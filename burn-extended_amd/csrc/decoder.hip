@@ -712,73 +712,32 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineAttnArgs a) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6, nc = a.nchunk;
   const float *base = a.part + ((size_t)b * a.kvH + g) * nc * (size_t)groups * rec;
   float *rinv = cl + (size_t)nc * groups;
-  // phase 1 for up to 64 chunks: every (m, l) pair and sink of the wave's heads requested at once
-  // (one memory round trip), then the same maxima, exponentials and lane-strided sums as the loop
-  // below, which serves longer caches
-  if (nc <= 64u && groups <= 16u) {
-    constexpr uint32_t JW = 4;  // heads per wave (groups <= 16)
-    float mv[JW], lv[JW], sk[JW];
-#pragma unroll
-    for (uint32_t u = 0; u < JW; ++u) {
-      const uint32_t j = min(w + 4u * u, groups - 1u), c = min(lane, nc - 1u);
+  for (uint32_t j = w; j < groups; j += 4u) {
+    const float sink = a.sinks ? a.sinks[g * groups + j] : -INFINITY;
+    float M = sink;
+    for (uint32_t c = lane; c < nc; c += 64u) M = fmaxf(M, base[((size_t)c * groups + j) * rec]);
+    M = wave_max(M);
+    float L = 0.0f;
+    for (uint32_t c = lane; c < nc; c += 64u) {
       const float *pc = base + ((size_t)c * groups + j) * rec;
-      mv[u] = pc[0];
-      lv[u] = pc[1];
-      sk[u] = a.sinks ? a.sinks[g * groups + j] : -INFINITY;
+      const float f = expf(pc[0] - M);
+      cl[c * groups + j] = f;
+      L = L + pc[1] * f;
     }
-#pragma unroll
-    for (uint32_t u = 0; u < JW; ++u) {
-      const uint32_t j = w + 4u * u;
-      if (j >= groups) break;  // wave-uniform
-      const bool has = lane < nc;
-      float M = has ? fmaxf(sk[u], mv[u]) : sk[u];
-      M = wave_max(M);
-      float L = 0.0f;
-      if (has) {
-        const float f = expf(mv[u] - M);
-        cl[lane * groups + j] = f;
-        L = L + lv[u] * f;
-      }
-      L = wave_sum_butterfly(L);
-      if (lane == 0) rinv[j] = 1.0f / (L + (a.sinks ? expf(sk[u] - M) : 0.0f));
-    }
-  } else {
-    for (uint32_t j = w; j < groups; j += 4u) {
-      const float sink = a.sinks ? a.sinks[g * groups + j] : -INFINITY;
-      float M = sink;
-      for (uint32_t c = lane; c < nc; c += 64u) M = fmaxf(M, base[((size_t)c * groups + j) * rec]);
-      M = wave_max(M);
-      float L = 0.0f;
-      for (uint32_t c = lane; c < nc; c += 64u) {
-        const float *pc = base + ((size_t)c * groups + j) * rec;
-        const float f = expf(pc[0] - M);
-        cl[c * groups + j] = f;
-        L = L + pc[1] * f;
-      }
-      L = wave_sum_butterfly(L);
-      if (lane == 0) rinv[j] = 1.0f / (L + (a.sinks ? expf(sink - M) : 0.0f));
-    }
+    L = wave_sum_butterfly(L);
+    if (lane == 0) rinv[j] = 1.0f / (L + (a.sinks ? expf(sink - M) : 0.0f));
   }
   __syncthreads();
   const uint32_t half = dk / 2u;
   for (uint32_t i = t; i < groups * half; i += blockDim.x) {
     const uint32_t j = i / half, d = 2u * (i - j * half);
     float ax = 0.0f, ay = 0.0f;
-    // chunks in blocks of 32: a block's value pairs requested at once (clamped past nc, not used),
-    // then added in chunk order
-    for (uint32_t c0 = 0; c0 < nc; c0 += 32u) {
-      float2 v[32];
-#pragma unroll
-      for (uint32_t u = 0; u < 32u; ++u)
-        v[u] = *(const float2 *)(base + ((size_t)min(c0 + u, nc - 1u) * groups + j) * rec + 2u + d);
-#pragma unroll
-      for (uint32_t u = 0; u < 32u; ++u) {
-        if (c0 + u < nc) {
-          const float f = cl[(c0 + u) * groups + j];
-          ax = fmaf(v[u].x, f, ax);
-          ay = fmaf(v[u].y, f, ay);
-        }
-      }
+#pragma unroll 8
+    for (uint32_t c = 0; c < nc; ++c) {
+      const float f = cl[c * groups + j];
+      const float2 v = *(const float2 *)(base + ((size_t)c * groups + j) * rec + 2u + d);
+      ax = fmaf(v.x, f, ax);
+      ay = fmaf(v.y, f, ay);
     }
     const float r = rinv[j];
     *(float2 *)(a.ctx + (size_t)b * a.nH * dk + (size_t)(g * groups + j) * dk + d) = make_float2(ax * r, ay * r);
