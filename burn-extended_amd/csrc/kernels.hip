@@ -792,9 +792,18 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_count_kernel(Dispatch
   __syncthreads();
   const uint32_t t = blockIdx.x * kDispatchChunk + tid;
   if (t < a.n) {
-    for (uint32_t p = 0; p < K; ++p) {
-      const int32_t e = a.topk_idx[(size_t)t * K + p];
-      if (e >= 0 && (uint32_t)e < E) atomicAdd(&cnt[e], 1);
+    if (K <= 8u) {  // the token's K indices requested together (a loop waits for each in turn)
+      int32_t ev[8];
+#pragma unroll
+      for (uint32_t p = 0; p < 8u; ++p) ev[p] = a.topk_idx[(size_t)t * K + min(p, K - 1u)];
+#pragma unroll
+      for (uint32_t p = 0; p < 8u; ++p)
+        if (p < K && ev[p] >= 0 && (uint32_t)ev[p] < E) atomicAdd(&cnt[ev[p]], 1);
+    } else {
+      for (uint32_t p = 0; p < K; ++p) {
+        const int32_t e = a.topk_idx[(size_t)t * K + p];
+        if (e >= 0 && (uint32_t)e < E) atomicAdd(&cnt[e], 1);
+      }
     }
   }
   __syncthreads();
@@ -815,19 +824,36 @@ __global__ __launch_bounds__(kDispatchChunk) void dispatch_wide_kernel(DispatchA
   __syncthreads();
   // every chunk's counts, all loads issued together: totals and earlier-chunk sums (LDS integer
   // atomics, order-independent)
-  for (uint32_t i = tid; i < nchunk * E; i += kDispatchChunk) {
-    const uint32_t c2 = i / E, e = i - c2 * E;
-    const int32_t v = a.chunk_cnt[i];
-    if (v != 0) {
-      atomicAdd(&call[e], v);
-      if (c2 < c) atomicAdd(&cbef[e], v);
+  // (8 per thread at a time, clamped past the end: a plain loop waited for each load in turn)
+  const uint32_t ncnt = nchunk * E;
+  for (uint32_t i0 = tid; i0 < ncnt; i0 += 8u * kDispatchChunk) {
+    int32_t v[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) v[u] = a.chunk_cnt[min(i0 + u * kDispatchChunk, ncnt - 1u)];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t i = i0 + u * kDispatchChunk;
+      if (i < ncnt && v[u] != 0) {
+        const uint32_t c2 = i / E, e = i - c2 * E;
+        atomicAdd(&call[e], v[u]);
+        if (c2 < c) atomicAdd(&cbef[e], v[u]);
+      }
     }
   }
   __syncthreads();
   if (t < n) {
-    for (uint32_t p = 0; p < K; ++p) {
-      const int32_t e = a.topk_idx[(size_t)t * K + p];
-      if (e >= 0 && (uint32_t)e < E) atomicOr(&bm[e * W + (tid >> 5)], 1u << (tid & 31u));
+    if (K <= 8u) {  // the token's K indices requested together
+      int32_t ev[8];
+#pragma unroll
+      for (uint32_t p = 0; p < 8u; ++p) ev[p] = a.topk_idx[(size_t)t * K + min(p, K - 1u)];
+#pragma unroll
+      for (uint32_t p = 0; p < 8u; ++p)
+        if (p < K && ev[p] >= 0 && (uint32_t)ev[p] < E) atomicOr(&bm[ev[p] * W + (tid >> 5)], 1u << (tid & 31u));
+    } else {
+      for (uint32_t p = 0; p < K; ++p) {
+        const int32_t e = a.topk_idx[(size_t)t * K + p];
+        if (e >= 0 && (uint32_t)e < E) atomicOr(&bm[e * W + (tid >> 5)], 1u << (tid & 31u));
+      }
     }
   }
   __syncthreads();
