@@ -389,22 +389,30 @@ __global__ __launch_bounds__(kRowsThreads) void router_rows_kernel(RouterArgs a)
     *(float4 *)(d + 256) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
 
-  // this wave's token rows as f32 (zeros beyond D)
+  // this wave's token rows as f32 (zeros beyond D), every chunk requested before any is used: no
+  // branch around a load (a branch per chunk made the wave wait for the chunks one by one), so
+  // chunks past D or of an inactive wave read a valid chunk and are zeroed
   float xv[T][RC][8];
+  {
+    Chunk8<XT> cx[T][RC];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int i = 0; i < RC; ++i) {
-      const uint32_t c0 = 512u * i + 8u * lane;
-      Chunk8<XT> c;
-      if (active && c0 < D) {
-        chunk_load(c, x + (size_t)(t0 + min((uint32_t)t, nt - 1u)) * D + c0);
-        chunk_vals(c, xv[t][i]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[t][i][j] = 0.0f;
+      for (int i = 0; i < RC; ++i) {
+        const uint32_t c0 = min(512u * i + 8u * lane, D - 8u);
+        const uint32_t row = min(t0 + min((uint32_t)t, max(nt, 1u) - 1u), a.n - 1u);
+        chunk_load(cx[t][i], x + (size_t)row * D + c0);
       }
-    }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        const bool ok = active && 512u * i + 8u * lane < D;
+        chunk_vals(cx[t][i], xv[t][i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[t][i][j] = ok ? xv[t][i][j] : 0.0f;
+      }
+  }
 
   // r per token
   float r[T];
